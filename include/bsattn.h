@@ -1,0 +1,173 @@
+/*
+ * bsattn.h -- C ABI of the MI355X (gfx950) block-sparse decode-attention
+ * library (libbsattn.so).
+ *
+ * One `bsattn_cache` is one layer's KV cache for up to `max_seqs`
+ * sequences: a paged pool of `block_size`-token pages in HBM, a per-sequence
+ * block table, and one mean-pooled summary key per full block and KV head.
+ * It stands in for the reference's per-layer `KVCache` object
+ * (Libraries/MLXLMCommon/KVCache.swift:38-77) and its decode attention
+ * (`attentionWithCacheUpdate`, Libraries/MLXLMCommon/AttentionUtils.swift:37-77).
+ *
+ * ABI rules
+ *  - every call returns an int status: BSATTN_OK (0) or a negative code; the
+ *    message of the last failure on the calling thread is bsattn_last_error();
+ *    no C++ exception crosses the ABI;
+ *  - tensors are caller-owned device pointers, dense, in the reference's
+ *    [batch, heads, tokens, head_dim] order; fp16/bf16 data is raw 16-bit;
+ *  - work is enqueued on the caller's hipStream_t (`stream`, NULL = the
+ *    default stream) and nothing synchronizes the host except where stated;
+ *  - a handle is thread-compatible, not thread-safe, and is used with one
+ *    stream at a time (the reference guards a cache the same way:
+ *    Libraries/MLXLMCommon/ModelContainer.swift:32-33).
+ */
+#ifndef BSATTN_H
+#define BSATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BSATTN_VERSION 1
+
+/* status codes */
+#define BSATTN_OK 0
+#define BSATTN_ERR_INVALID (-1)  /* bad argument / unsupported shape */
+#define BSATTN_ERR_HIP (-2)      /* a HIP runtime call failed */
+#define BSATTN_ERR_NO_PAGES (-3) /* the page pool is exhausted */
+#define BSATTN_ERR_RANGE (-4)    /* sequence id or length out of range */
+
+/* element types of q / k / v / output / summaries */
+#define BSATTN_F16 0
+#define BSATTN_BF16 1
+
+typedef struct bsattn_cache bsattn_cache;
+
+/* Cache geometry.  Mirrors the knobs of QuantizedKVCache
+ * (groupSize / bits: KVCache.swift:728-744) plus the block-sparse ones. */
+typedef struct bsattn_desc {
+  int32_t max_seqs;           /* sequences (batch rows) the cache can hold */
+  int32_t num_q_heads;        /* Hq */
+  int32_t num_kv_heads;       /* Hkv; Hq % Hkv == 0, Hq / Hkv <= 16 */
+  int32_t head_dim;           /* D; 128 */
+  int32_t block_size;         /* tokens per block (= page): 32 or 64 */
+  int32_t dtype;              /* BSATTN_F16 or BSATTN_BF16 */
+  int32_t kv_bits;            /* 0: K/V stored in dtype; 4 or 8: affine (dtype f16) */
+  int32_t group_size;         /* affine group along head_dim: 64 */
+  int32_t top_k;              /* scored blocks kept per (sequence, kv head) */
+  int32_t sink_blocks;        /* leading blocks always kept */
+  int32_t recent_blocks;      /* trailing blocks always kept; >= 1 */
+  int32_t max_blocks_per_seq; /* block-table width */
+  int64_t num_pages;          /* physical pages; 0 = max_seqs * max_blocks_per_seq */
+  int32_t device;             /* HIP device ordinal */
+  int32_t reserved[3];        /* must be 0 */
+} bsattn_desc;
+
+/* Derived sizes, for callers sizing buffers. */
+typedef struct bsattn_info {
+  int32_t nsel_max;        /* sink + recent + top_k: width of index outputs */
+  int32_t num_splits;      /* attention partials per (sequence, q head) */
+  int64_t page_bytes;      /* bytes of one page across all kv heads, incl. summaries */
+  int64_t pool_bytes;      /* device bytes held by the handle */
+  int64_t free_pages;      /* pages not owned by any sequence */
+} bsattn_info;
+
+int32_t bsattn_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* bsattn_last_error(void);
+
+/* Creates an empty cache.  Replaces constructing a KVCacheSimple /
+ * QuantizedKVCache in LanguageModel.newCache
+ * (Libraries/MLXLMCommon/LanguageModel.swift:215-230). */
+int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out);
+int bsattn_cache_destroy(bsattn_cache* cache);
+int bsattn_cache_info(const bsattn_cache* cache, bsattn_info* out);
+
+/* Tokens held by sequence `seq` (the reference's `offset`,
+ * KVCache.swift:40). */
+int bsattn_seq_len(const bsattn_cache* cache, int32_t seq, int32_t* out_len);
+
+/* Appends n_tokens tokens to each listed sequence: k, v are
+ * [n_seqs, Hkv, n_tokens, D] in dtype.  Blocks that become full get their
+ * summary written.  seq_ids (host, n_seqs distinct ids) may be NULL for
+ * rows 0..n_seqs-1.  On a quantized cache the keys/values are quantized on
+ * append.  Replaces KVCacheSimple.update(keys:values:)
+ * (KVCache.swift:328-371) and QuantizedKVCache.updateQuantized
+ * (KVCache.swift:816-889). */
+int bsattn_append(bsattn_cache* cache, const void* k, const void* v,
+                  const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
+                  void* stream);
+
+/* Appends already-quantized tokens in MLX layout: *_w [n, Hkv, L, D*bits/32]
+ * uint32, *_s / *_b [n, Hkv, L, D/group_size] fp16.  Same layout as the
+ * (wq, scales, biases) tuples of QuantizedKVCache.state
+ * (KVCache.swift:906-925). */
+int bsattn_append_quantized(bsattn_cache* cache, const uint32_t* k_w,
+                            const void* k_s, const void* k_b,
+                            const uint32_t* v_w, const void* v_s,
+                            const void* v_b, const int32_t* seq_ids,
+                            int32_t n_seqs, int32_t n_tokens, void* stream);
+
+/* Selector-index API (no reference counterpart; additive).  Scores every
+ * candidate block with max over the GQA group of q . summary, keeps sink and
+ * recent blocks and the top_k best (ties -> lower index).  q is
+ * [n_seqs, Hq, 1, D]; idx_out (device) is [n_seqs, Hkv, nsel_max] int32:
+ * ascending block indices, padded with -1. */
+int bsattn_select(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
+                  int32_t n_seqs, int32_t* idx_out, void* stream);
+
+/* Attention of q [n_seqs, Hq, 1, D] over the blocks listed in idx
+ * ([n_seqs, Hkv, nsel_max], -1 padded; device) -> out [n_seqs, Hq, 1, D]
+ * in dtype.  softmax(q k^T * scale) v over the gathered tokens, GQA head h
+ * reading kv head h / (Hq/Hkv) (as the dense path of AttentionUtils.swift:68-75
+ * and KVCache.swift:1533-1621 computes over all tokens). */
+int bsattn_attend(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
+                  int32_t n_seqs, const int32_t* idx, float scale, void* out,
+                  void* stream);
+
+/* bsattn_select then bsattn_attend.  idx_out may be NULL (library
+ * workspace).  The decode branch of attentionWithCacheUpdate
+ * (AttentionUtils.swift:68-75) after the cache update. */
+int bsattn_decode(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
+                  int32_t n_seqs, float scale, void* out, int32_t* idx_out,
+                  void* stream);
+
+/* Drops the last n_tokens of each listed sequence (clamped to its length);
+ * writes the number trimmed per sequence to trimmed (host, may be NULL).
+ * KVCacheSimple.trim (KVCache.swift:396-402). */
+int bsattn_trim(bsattn_cache* cache, const int32_t* seq_ids, int32_t n_seqs,
+                int32_t n_tokens, int32_t* trimmed, void* stream);
+
+/* Empties the listed sequences and returns their pages to the pool. */
+int bsattn_reset(bsattn_cache* cache, const int32_t* seq_ids, int32_t n_seqs,
+                 void* stream);
+
+/* Deep copy (KVCacheSimple.copy, KVCache.swift:429-437). */
+int bsattn_copy(const bsattn_cache* src, bsattn_cache** out, void* stream);
+
+/* Writes the listed sequences' keys and values in the reference layout
+ * [n_seqs, Hkv, T, D] (device); all listed sequences must hold T tokens.
+ * The `state` getter of KVCacheSimple (KVCache.swift:373-384).  On a
+ * quantized cache use bsattn_export_quantized. */
+int bsattn_export(const bsattn_cache* cache, const int32_t* seq_ids,
+                  int32_t n_seqs, void* k_out, void* v_out, void* stream);
+
+/* Quantized state in MLX layout (see bsattn_append_quantized).
+ * QuantizedKVCache.state getter (KVCache.swift:906-925). */
+int bsattn_export_quantized(const bsattn_cache* cache, const int32_t* seq_ids,
+                            int32_t n_seqs, uint32_t* k_w, void* k_s,
+                            void* k_b, uint32_t* v_w, void* v_s, void* v_b,
+                            void* stream);
+
+/* Block summaries of one sequence: out [Hkv, T / block_size, D] (device,
+ * dtype; fp16 for quantized caches). */
+int bsattn_export_summaries(const bsattn_cache* cache, int32_t seq, void* out,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BSATTN_H */

@@ -1,0 +1,290 @@
+"""BlockSparseKVCache: the host-side mirror of the reference's KVCache
+protocol (Libraries/MLXLMCommon/KVCache.swift:38-77) for the block-sparse
+cache, over the C ABI of libbsattn.so.
+
+Member names follow the Swift protocol (offset, maxSize, update, state,
+metaState, isTrimmable, trim, makeMask, copy) plus the additive
+selector-index API (blockSize, topK, sinkBlocks, recentBlocks,
+selectBlocks).  Misuse raises (the Swift code traps with fatalError /
+precondition, e.g. KVCache.swift:386-388); library failures raise
+BsattnError carrying the C status code.
+
+torch tensors are used only as device memory and streams; every
+computation runs in the HIP kernels of libbsattn.so.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import BsattnError, check, i32_array, lib
+
+_DTYPES = {torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class BlockSparseKVCache:
+    """One layer's paged KV cache for up to `max_seqs` sequences."""
+
+    def __init__(self, *, max_seqs: int, num_q_heads: int, num_kv_heads: int,
+                 head_dim: int = 128, block_size: int = 64,
+                 dtype: torch.dtype = torch.bfloat16, kv_bits: int = 0,
+                 group_size: int = 64, top_k: int = 32, sink_blocks: int = 1,
+                 recent_blocks: int = 1, max_blocks_per_seq: int = 512,
+                 num_pages: int = 0, device: int | torch.device = 0,
+                 _handle: Optional[ctypes.c_void_p] = None):
+        if dtype not in _DTYPES:
+            raise TypeError(f"dtype {dtype} unsupported (float16 or bfloat16)")
+        self.device = torch.device("cuda", device if isinstance(device, int) else device.index or 0)
+        self.dtype = dtype
+        self.desc = _lib.Desc(
+            max_seqs=max_seqs, num_q_heads=num_q_heads, num_kv_heads=num_kv_heads,
+            head_dim=head_dim, block_size=block_size, dtype=_DTYPES[dtype], kv_bits=kv_bits,
+            group_size=group_size, top_k=top_k, sink_blocks=sink_blocks,
+            recent_blocks=recent_blocks, max_blocks_per_seq=max_blocks_per_seq,
+            num_pages=num_pages, device=self.device.index)
+        if _handle is None:
+            h = ctypes.c_void_p()
+            check(lib().bsattn_cache_create(ctypes.byref(self.desc), ctypes.byref(h)))
+            self._h = h
+        else:
+            self._h = _handle
+        info = _lib.Info()
+        check(lib().bsattn_cache_info(self._h, ctypes.byref(info)))
+        self.nselMax = info.nsel_max
+        self.numSplits = info.num_splits
+        self.poolBytes = info.pool_bytes
+
+    # -- lifetime ----------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().bsattn_cache_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- geometry ------------------------------------------------------------
+    @property
+    def blockSize(self) -> int:
+        return self.desc.block_size
+
+    @property
+    def topK(self) -> int:
+        return self.desc.top_k
+
+    @property
+    def sinkBlocks(self) -> int:
+        return self.desc.sink_blocks
+
+    @property
+    def recentBlocks(self) -> int:
+        return self.desc.recent_blocks
+
+    @property
+    def bits(self) -> int:
+        return self.desc.kv_bits
+
+    @property
+    def groupSize(self) -> int:
+        return self.desc.group_size
+
+    @property
+    def maxSize(self):
+        return None
+
+    @property
+    def freePages(self) -> int:
+        info = _lib.Info()
+        check(lib().bsattn_cache_info(self._h, ctypes.byref(info)))
+        return int(info.free_pages)
+
+    def seqLen(self, seq: int) -> int:
+        out = ctypes.c_int32()
+        check(lib().bsattn_seq_len(self._h, seq, ctypes.byref(out)))
+        return out.value
+
+    @property
+    def offset(self) -> int:
+        """Tokens held by sequence 0 (the reference keeps one offset for the
+        whole batch, KVCache.swift:40)."""
+        return self.seqLen(0)
+
+    # -- KV writes -----------------------------------------------------------
+    def _check_kv(self, t: torch.Tensor, name: str) -> None:
+        if t.device != self.device or t.dtype != self.dtype or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {self.dtype} tensor on {self.device}")
+        if t.dim() != 4 or t.shape[1] != self.desc.num_kv_heads or t.shape[3] != self.desc.head_dim:
+            raise ValueError(f"{name} must be [B, {self.desc.num_kv_heads}, L, {self.desc.head_dim}], got {tuple(t.shape)}")
+
+    def append(self, keys: torch.Tensor, values: torch.Tensor,
+               seq_ids: Optional[Sequence[int]] = None) -> None:
+        """Appends keys/values [B, Hkv, L, D] to sequences seq_ids (default
+        0..B-1)."""
+        self._check_kv(keys, "keys")
+        self._check_kv(values, "values")
+        if keys.shape != values.shape:
+            raise ValueError("keys and values shapes differ")
+        B, _, L, _ = keys.shape
+        ids = i32_array(seq_ids)
+        check(lib().bsattn_append(self._h, _ptr(keys), _ptr(values), ids, B, L,
+                                  _stream(self.device)))
+
+    def update(self, keys: torch.Tensor, values: torch.Tensor):
+        """KVCache.update (KVCache.swift:328-371): append, then return all
+        cached keys/values [B, Hkv, offset, D]."""
+        self.append(keys, values)
+        return self.export(list(range(keys.shape[0])))
+
+    def export(self, seq_ids: Sequence[int]):
+        B = len(seq_ids)
+        T = self.seqLen(seq_ids[0])
+        shape = (B, self.desc.num_kv_heads, T, self.desc.head_dim)
+        k = torch.empty(shape, dtype=self.dtype, device=self.device)
+        v = torch.empty(shape, dtype=self.dtype, device=self.device)
+        check(lib().bsattn_export(self._h, i32_array(seq_ids), B, _ptr(k), _ptr(v),
+                                  _stream(self.device)))
+        return k, v
+
+    def exportSummaries(self, seq: int) -> torch.Tensor:
+        n = self.seqLen(seq) // self.blockSize
+        out = torch.empty((self.desc.num_kv_heads, n, self.desc.head_dim), dtype=self.dtype,
+                          device=self.device)
+        if n:
+            check(lib().bsattn_export_summaries(self._h, seq, _ptr(out), _stream(self.device)))
+        return out
+
+    # -- selector-index API and attention -----------------------------------
+    def _check_q(self, q: torch.Tensor) -> int:
+        if q.device != self.device or q.dtype != self.dtype or not q.is_contiguous():
+            raise ValueError(f"queries must be a contiguous {self.dtype} tensor on {self.device}")
+        if q.dim() != 4 or q.shape[1] != self.desc.num_q_heads or q.shape[2] != 1 \
+                or q.shape[3] != self.desc.head_dim:
+            raise ValueError(f"queries must be [B, {self.desc.num_q_heads}, 1, {self.desc.head_dim}], "
+                             f"got {tuple(q.shape)}")
+        return q.shape[0]
+
+    def selectBlocks(self, queries: torch.Tensor,
+                     seq_ids: Optional[Sequence[int]] = None) -> torch.Tensor:
+        """Selected block indices [B, Hkv, nselMax] int32, ascending, -1 padded."""
+        B = self._check_q(queries)
+        idx = torch.empty((B, self.desc.num_kv_heads, self.nselMax), dtype=torch.int32,
+                          device=self.device)
+        check(lib().bsattn_select(self._h, _ptr(queries), i32_array(seq_ids), B, _ptr(idx),
+                                  _stream(self.device)))
+        return idx
+
+    def attend(self, queries: torch.Tensor, idx: torch.Tensor, scale: float,
+               seq_ids: Optional[Sequence[int]] = None) -> torch.Tensor:
+        B = self._check_q(queries)
+        if idx.dtype != torch.int32 or idx.device != self.device or not idx.is_contiguous() \
+                or tuple(idx.shape) != (B, self.desc.num_kv_heads, self.nselMax):
+            raise ValueError("idx must be a contiguous int32 [B, Hkv, nselMax] tensor on the cache device")
+        out = torch.empty_like(queries)
+        check(lib().bsattn_attend(self._h, _ptr(queries), i32_array(seq_ids), B, _ptr(idx),
+                                  ctypes.c_float(scale), _ptr(out), _stream(self.device)))
+        return out
+
+    def decode(self, queries: torch.Tensor, scale: float,
+               seq_ids: Optional[Sequence[int]] = None,
+               idx_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        B = self._check_q(queries)
+        out = torch.empty_like(queries)
+        idx_p = None
+        if idx_out is not None:
+            if idx_out.dtype != torch.int32 or tuple(idx_out.shape) != (B, self.desc.num_kv_heads, self.nselMax):
+                raise ValueError("idx_out must be int32 [B, Hkv, nselMax]")
+            idx_p = _ptr(idx_out)
+        check(lib().bsattn_decode(self._h, _ptr(queries), i32_array(seq_ids), B,
+                                  ctypes.c_float(scale), _ptr(out), idx_p, _stream(self.device)))
+        return out
+
+    # -- KVCache protocol: state, trim, mask, copy -----------------------------
+    @property
+    def state(self) -> List[torch.Tensor]:
+        n = self.batchSize()
+        if n == 0:
+            return []
+        return list(self.export(list(range(n))))
+
+    @state.setter
+    def state(self, arrays: List[torch.Tensor]) -> None:
+        if len(arrays) != 2:
+            raise ValueError("BlockSparseKVCache state must have exactly 2 arrays (keys, values)")
+        k, v = arrays
+        self.reset(list(range(self.desc.max_seqs)))
+        if k.shape[2] > 0:
+            self.append(k.contiguous(), v.contiguous())
+
+    @property
+    def metaState(self) -> List[str]:
+        d = self.desc
+        return [str(d.block_size), str(d.top_k), str(d.sink_blocks), str(d.recent_blocks),
+                str(self.offset), str(d.kv_bits), str(d.group_size)]
+
+    @metaState.setter
+    def metaState(self, values: List[str]) -> None:
+        if len(values) != 7:
+            raise ValueError("BlockSparseKVCache metaState must have exactly 7 values")
+        want = [int(x) for x in values]
+        d = self.desc
+        have = [d.block_size, d.top_k, d.sink_blocks, d.recent_blocks, want[4], d.kv_bits, d.group_size]
+        if want != have:
+            raise ValueError(f"metaState {values} does not match this cache's geometry")
+        if self.offset != want[4]:
+            raise ValueError(f"metaState offset {want[4]} != cached tokens {self.offset}")
+
+    def batchSize(self) -> int:
+        """Number of leading sequences that hold tokens."""
+        n = 0
+        while n < self.desc.max_seqs and self.seqLen(n) > 0:
+            n += 1
+        return n
+
+    @property
+    def isTrimmable(self) -> bool:
+        return True
+
+    def trim(self, n: int, seq_ids: Optional[Sequence[int]] = None) -> int:
+        ids = list(seq_ids) if seq_ids is not None else list(range(max(self.batchSize(), 1)))
+        out = (ctypes.c_int32 * len(ids))()
+        check(lib().bsattn_trim(self._h, i32_array(ids), len(ids), n, out, _stream(self.device)))
+        return int(out[0])
+
+    def reset(self, seq_ids: Sequence[int]) -> None:
+        check(lib().bsattn_reset(self._h, i32_array(seq_ids), len(seq_ids), _stream(self.device)))
+
+    def makeMask(self, n: int, windowSize=None, returnArray: bool = False):
+        """BaseKVCache.makeMask (KVCache.swift:160-174): decode needs none."""
+        if n == 1:
+            return "none"
+        if returnArray or (windowSize is not None and n > windowSize):
+            return "array"
+        return "causal"
+
+    def copy(self) -> "BlockSparseKVCache":
+        h = ctypes.c_void_p()
+        check(lib().bsattn_copy(self._h, ctypes.byref(h), _stream(self.device)))
+        d = self.desc
+        return BlockSparseKVCache(
+            max_seqs=d.max_seqs, num_q_heads=d.num_q_heads, num_kv_heads=d.num_kv_heads,
+            head_dim=d.head_dim, block_size=d.block_size, dtype=self.dtype, kv_bits=d.kv_bits,
+            group_size=d.group_size, top_k=d.top_k, sink_blocks=d.sink_blocks,
+            recent_blocks=d.recent_blocks, max_blocks_per_seq=d.max_blocks_per_seq,
+            num_pages=d.num_pages, device=self.device.index, _handle=h)
+
+
+__all__ = ["BlockSparseKVCache", "BsattnError"]

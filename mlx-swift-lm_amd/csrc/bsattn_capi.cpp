@@ -1,0 +1,501 @@
+// bsattn_capi.cpp -- the C ABI of include/bsattn.h: page-pool manager,
+// per-sequence block tables, argument checking and kernel sequencing.
+//
+// The host copy of lengths / block tables is authoritative; the device copy
+// (`meta`) is brought up to date in stream order by small patch launches
+// whose payload travels in the kernel arguments, so no host staging buffer
+// can be overwritten while a copy is still pending.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/bsattn.h"
+#include "bsattn_internal.h"
+
+using namespace bsattn;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(BSATTN_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(call, what)              \
+  do {                                   \
+    hipError_t e_ = (call);              \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+}  // namespace
+
+struct bsattn_cache {
+  bsattn_desc d{};
+  Geometry geo{};
+  int64_t num_pages = 0;
+  size_t pool_bytes = 0, summ_bytes = 0, meta_words = 0;
+  float* scores = nullptr;    // [max_seqs][hkv][mbps]
+  int32_t* idx_ws = nullptr;  // [max_seqs][hkv][nsel_max]
+  float* partials = nullptr;  // [max_seqs][hq][nsplit][D + 2]
+  std::vector<int32_t> len;
+  std::vector<std::vector<int32_t>> pages;
+  std::vector<int32_t> free_pages;  // stack; back() is handed out next
+};
+
+namespace {
+
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    ok = hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+int validate_desc(const bsattn_desc& d) {
+  if (d.max_seqs < 1) return fail(BSATTN_ERR_INVALID, "max_seqs must be >= 1 (got %d)", d.max_seqs);
+  if (d.num_kv_heads < 1 || d.num_q_heads < 1 || d.num_q_heads % d.num_kv_heads != 0)
+    return fail(BSATTN_ERR_INVALID, "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)",
+                d.num_q_heads, d.num_kv_heads);
+  const int G = d.num_q_heads / d.num_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16)
+    return fail(BSATTN_ERR_INVALID, "GQA group %d unsupported (1, 2, 4, 8 or 16)", G);
+  if (16 % d.num_kv_heads != 0)
+    return fail(BSATTN_ERR_INVALID, "num_kv_heads %d unsupported (must divide 16)", d.num_kv_heads);
+  if (d.head_dim != kHeadDim) return fail(BSATTN_ERR_INVALID, "head_dim %d unsupported (128)", d.head_dim);
+  if (d.block_size != 32 && d.block_size != 64)
+    return fail(BSATTN_ERR_INVALID, "block_size %d unsupported (32 or 64)", d.block_size);
+  if (d.dtype != BSATTN_F16 && d.dtype != BSATTN_BF16)
+    return fail(BSATTN_ERR_INVALID, "dtype %d unknown", d.dtype);
+  if (d.kv_bits != 0) return fail(BSATTN_ERR_INVALID, "kv_bits %d: quantized caches not available in this build", d.kv_bits);
+  if (d.top_k < 0 || d.sink_blocks < 0) return fail(BSATTN_ERR_INVALID, "top_k and sink_blocks must be >= 0");
+  if (d.recent_blocks < 1) return fail(BSATTN_ERR_INVALID, "recent_blocks must be >= 1 (the partial block is never scored)");
+  if (d.max_blocks_per_seq < 1 || d.max_blocks_per_seq > 12288)
+    return fail(BSATTN_ERR_INVALID, "max_blocks_per_seq %d out of range [1, 12288]", d.max_blocks_per_seq);
+  const int64_t nsel = (int64_t)d.top_k + d.sink_blocks + d.recent_blocks;
+  if (nsel > 4096) return fail(BSATTN_ERR_INVALID, "sink + recent + top_k = %lld too large", (long long)nsel);
+  if (d.num_pages < 0) return fail(BSATTN_ERR_INVALID, "num_pages must be >= 0");
+  for (int r : d.reserved)
+    if (r != 0) return fail(BSATTN_ERR_INVALID, "reserved fields must be 0");
+  return BSATTN_OK;
+}
+
+// Seq list -> vector (validated, distinct)
+int seq_list(const bsattn_cache* c, const int32_t* ids, int32_t n, std::vector<int32_t>& out) {
+  if (n < 1) return fail(BSATTN_ERR_INVALID, "n_seqs must be >= 1 (got %d)", n);
+  if (n > c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "n_seqs %d exceeds max_seqs %d", n, c->d.max_seqs);
+  out.resize(n);
+  std::vector<char> seen(c->d.max_seqs, 0);
+  for (int i = 0; i < n; ++i) {
+    const int s = ids ? ids[i] : i;
+    if (s < 0 || s >= c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "sequence id %d out of range [0, %d)", s, c->d.max_seqs);
+    if (seen[s]) return fail(BSATTN_ERR_INVALID, "sequence id %d listed twice", s);
+    seen[s] = 1;
+    out[i] = s;
+  }
+  return BSATTN_OK;
+}
+
+int flush_patches(bsattn_cache* c, std::vector<std::pair<int32_t, int32_t>>& p, hipStream_t s) {
+  for (size_t i = 0; i < p.size(); i += kMaxPatch) {
+    PatchBatch pb{};
+    pb.n = (int32_t)std::min<size_t>(kMaxPatch, p.size() - i);
+    for (int k = 0; k < pb.n; ++k) {
+      pb.idx[k] = p[i + k].first;
+      pb.val[k] = p[i + k].second;
+    }
+    HIP_TRY(launch_patch(c->geo, pb, s), "patch launch");
+  }
+  p.clear();
+  return BSATTN_OK;
+}
+
+int release_pages(bsattn_cache* c, int seq, int keep_blocks) {
+  auto& pg = c->pages[seq];
+  while ((int)pg.size() > keep_blocks) {
+    c->free_pages.push_back(pg.back());
+    pg.pop_back();
+  }
+  return BSATTN_OK;
+}
+
+// Reserve pages for new lengths; on failure nothing changes.
+int reserve_pages(bsattn_cache* c, const std::vector<int32_t>& seqs, int L,
+                  std::vector<std::pair<int32_t, int32_t>>& patches) {
+  const int tb = c->d.block_size;
+  int64_t need = 0;
+  for (int s : seqs) {
+    const int64_t newlen = (int64_t)c->len[s] + L;
+    if (newlen > (int64_t)c->d.max_blocks_per_seq * tb)
+      return fail(BSATTN_ERR_RANGE, "sequence %d would hold %lld tokens > max_blocks_per_seq * block_size = %d",
+                  s, (long long)newlen, c->d.max_blocks_per_seq * tb);
+    need += (newlen + tb - 1) / tb - (int64_t)c->pages[s].size();
+  }
+  if (need > (int64_t)c->free_pages.size())
+    return fail(BSATTN_ERR_NO_PAGES, "page pool exhausted: need %lld pages, %zu free", (long long)need,
+                c->free_pages.size());
+  for (int s : seqs) {
+    const int newlen = c->len[s] + L;
+    const int nblk = (newlen + tb - 1) / tb;
+    auto& pg = c->pages[s];
+    while ((int)pg.size() < nblk) {
+      const int32_t p = c->free_pages.back();
+      c->free_pages.pop_back();
+      patches.emplace_back(c->geo.bt_off + s * c->d.max_blocks_per_seq + (int)pg.size(), p);
+      pg.push_back(p);
+    }
+  }
+  return BSATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t bsattn_version(void) { return BSATTN_VERSION; }
+
+const char* bsattn_last_error(void) { return g_err.c_str(); }
+
+int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
+  if (!desc || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  *out = nullptr;
+  int rc = validate_desc(*desc);
+  if (rc) return rc;
+  DeviceGuard dg(desc->device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", desc->device);
+  bsattn_cache* c = new (std::nothrow) bsattn_cache();
+  if (!c) return fail(BSATTN_ERR_INVALID, "host allocation failed");
+  c->d = *desc;
+  const bsattn_desc& d = c->d;
+  c->num_pages = d.num_pages ? d.num_pages : (int64_t)d.max_seqs * d.max_blocks_per_seq;
+  Geometry& g = c->geo;
+  g.hq = d.num_q_heads;
+  g.hkv = d.num_kv_heads;
+  g.group = d.num_q_heads / d.num_kv_heads;
+  g.tb = d.block_size;
+  g.dtype = d.dtype;
+  g.kv_bits = d.kv_bits;
+  g.gsize = d.group_size;
+  g.top_k = d.top_k;
+  g.ns = d.sink_blocks;
+  g.nr = d.recent_blocks;
+  g.nsel_max = d.top_k + d.sink_blocks + d.recent_blocks;
+  g.nsplit = (g.nsel_max + kWaves - 1) / kWaves;
+  g.mbps = d.max_blocks_per_seq;
+  g.bt_off = d.max_seqs;
+  // slab: K tile [Tb][D] then V tile [D][Tb], 16-bit elements
+  g.k_off = 0;
+  g.v_off = (int64_t)d.block_size * kHeadDim * 2;
+  g.slab_bytes = 2 * g.v_off;
+  g.ks_off = g.kb_off = g.vs_off = g.vb_off = 0;
+  c->pool_bytes = (size_t)c->num_pages * g.hkv * g.slab_bytes;
+  c->summ_bytes = (size_t)c->num_pages * g.hkv * kHeadDim * 2;
+  c->meta_words = (size_t)d.max_seqs * (1 + d.max_blocks_per_seq);
+  auto cleanup = [&](int code) {
+    (void)hipFree(g.pool);
+    (void)hipFree(g.summ);
+    (void)hipFree(g.meta);
+    (void)hipFree(c->scores);
+    (void)hipFree(c->idx_ws);
+    (void)hipFree(c->partials);
+    delete c;
+    return code;
+  };
+  hipError_t e;
+  if ((e = hipMalloc((void**)&g.pool, c->pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(pool)"));
+  if ((e = hipMalloc((void**)&g.summ, c->summ_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(summaries)"));
+  if ((e = hipMalloc((void**)&g.meta, c->meta_words * 4)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(meta)"));
+  if ((e = hipMalloc((void**)&c->scores, (size_t)d.max_seqs * g.hkv * g.mbps * 4)) != hipSuccess)
+    return cleanup(hip_fail(e, "hipMalloc(scores)"));
+  if ((e = hipMalloc((void**)&c->idx_ws, (size_t)d.max_seqs * g.hkv * g.nsel_max * 4)) != hipSuccess)
+    return cleanup(hip_fail(e, "hipMalloc(indices)"));
+  if ((e = hipMalloc((void**)&c->partials, (size_t)d.max_seqs * g.hq * g.nsplit * (kHeadDim + 2) * 4)) != hipSuccess)
+    return cleanup(hip_fail(e, "hipMalloc(partials)"));
+  // zeroed pages: never-written token slots hold finite values
+  if ((e = hipMemset(g.pool, 0, c->pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(pool)"));
+  if ((e = hipMemset(g.summ, 0, c->summ_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(summaries)"));
+  if ((e = hipMemset(g.meta, 0, c->meta_words * 4)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(meta)"));
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(hip_fail(e, "hipDeviceSynchronize"));
+  c->len.assign(d.max_seqs, 0);
+  c->pages.assign(d.max_seqs, {});
+  c->free_pages.resize(c->num_pages);
+  for (int64_t i = 0; i < c->num_pages; ++i) c->free_pages[i] = (int32_t)(c->num_pages - 1 - i);
+  *out = c;
+  return BSATTN_OK;
+}
+
+int bsattn_cache_destroy(bsattn_cache* c) {
+  if (!c) return BSATTN_OK;
+  DeviceGuard dg(c->d.device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(c->geo.pool);
+  (void)hipFree(c->geo.summ);
+  (void)hipFree(c->geo.meta);
+  (void)hipFree(c->scores);
+  (void)hipFree(c->idx_ws);
+  (void)hipFree(c->partials);
+  delete c;
+  return BSATTN_OK;
+}
+
+int bsattn_cache_info(const bsattn_cache* c, bsattn_info* out) {
+  if (!c || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  out->nsel_max = c->geo.nsel_max;
+  out->num_splits = c->geo.nsplit;
+  out->page_bytes = (int64_t)c->geo.hkv * (c->geo.slab_bytes + kHeadDim * 2);
+  out->pool_bytes = (int64_t)(c->pool_bytes + c->summ_bytes + c->meta_words * 4);
+  out->free_pages = (int64_t)c->free_pages.size();
+  return BSATTN_OK;
+}
+
+int bsattn_seq_len(const bsattn_cache* c, int32_t seq, int32_t* out_len) {
+  if (!c || !out_len) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (seq < 0 || seq >= c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "sequence id %d out of range", seq);
+  *out_len = c->len[seq];
+  return BSATTN_OK;
+}
+
+int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* seq_ids,
+                  int32_t n_seqs, int32_t n_tokens, void* stream) {
+  if (!c || !k || !v) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (c->d.kv_bits != 0) return fail(BSATTN_ERR_INVALID, "quantize-on-append is not available; use bsattn_append_quantized");
+  if (n_tokens < 1) return fail(BSATTN_ERR_INVALID, "n_tokens must be >= 1 (got %d)", n_tokens);
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  DeviceGuard dg(c->d.device);
+  hipStream_t s = (hipStream_t)stream;
+  std::vector<std::pair<int32_t, int32_t>> patches;
+  rc = reserve_pages(c, seqs, n_tokens, patches);
+  if (rc) return rc;
+  const int tb = c->d.block_size;
+  for (int s_ : seqs) patches.emplace_back(s_, c->len[s_] + n_tokens);
+  rc = flush_patches(c, patches, s);
+  if (rc) return rc;
+  const size_t row_elems = (size_t)c->geo.hkv * n_tokens * kHeadDim;
+  for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
+    AppendBatch ab{};
+    SummaryBatch sb{};
+    ab.n = std::min(kMaxBatch, n_seqs - i0);
+    ab.L = n_tokens;
+    int max_count = 0;
+    for (int i = 0; i < ab.n; ++i) {
+      const int sq = seqs[i0 + i];
+      ab.seq[i] = sq;
+      ab.old_len[i] = c->len[sq];
+      const int first = c->len[sq] / tb;
+      const int last = (c->len[sq] + n_tokens) / tb;  // exclusive: full blocks after
+      sb.seq[i] = sq;
+      sb.first[i] = first;
+      sb.count[i] = last - first;
+      max_count = std::max(max_count, last - first);
+    }
+    sb.n = ab.n;
+    const uint16_t* kk = (const uint16_t*)k + (size_t)i0 * row_elems;
+    const uint16_t* vv = (const uint16_t*)v + (size_t)i0 * row_elems;
+    HIP_TRY(launch_append(c->geo, ab, kk, vv, s), "append launch");
+    if (max_count > 0) HIP_TRY(launch_summary(c->geo, sb, max_count, s), "summary launch");
+  }
+  for (int s_ : seqs) c->len[s_] += n_tokens;
+  return BSATTN_OK;
+}
+
+int bsattn_append_quantized(bsattn_cache* c, const uint32_t*, const void*, const void*,
+                            const uint32_t*, const void*, const void*, const int32_t*, int32_t,
+                            int32_t, void*) {
+  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  return fail(BSATTN_ERR_INVALID, "quantized caches are not available in this build");
+}
+
+static int do_select(bsattn_cache* c, const void* q, const std::vector<int32_t>& seqs,
+                     int32_t* idx_out, hipStream_t s) {
+  const int tb = c->d.block_size;
+  const int n = (int)seqs.size();
+  for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
+    SeqBatch b{};
+    b.n = std::min(kMaxBatch, n - i0);
+    int max_cand = 0;
+    for (int i = 0; i < b.n; ++i) {
+      b.ids[i] = seqs[i0 + i];
+      const int nb = (c->len[b.ids[i]] + tb - 1) / tb;
+      max_cand = std::max(max_cand, nb - c->geo.nr - c->geo.ns);
+    }
+    const uint16_t* qq = (const uint16_t*)q + (size_t)i0 * c->geo.hq * kHeadDim;
+    float* sc = c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps;
+    int32_t* io = idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max;
+    if (max_cand > c->geo.top_k) HIP_TRY(launch_score(c->geo, b, qq, sc, max_cand, s), "score launch");
+    HIP_TRY(launch_topk(c->geo, b, sc, io, s), "top-k launch");
+  }
+  return BSATTN_OK;
+}
+
+static int do_attend(bsattn_cache* c, const void* q, const std::vector<int32_t>& seqs,
+                     const int32_t* idx, float scale, void* out, hipStream_t s) {
+  const int n = (int)seqs.size();
+  const size_t elem = 2;
+  for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
+    SeqBatch b{};
+    b.n = std::min(kMaxBatch, n - i0);
+    for (int i = 0; i < b.n; ++i) b.ids[i] = seqs[i0 + i];
+    const size_t qoff = (size_t)i0 * c->geo.hq * kHeadDim * elem;
+    HIP_TRY(launch_attend(c->geo, b, (const char*)q + qoff,
+                          idx + (size_t)i0 * c->geo.hkv * c->geo.nsel_max, scale,
+                          (char*)out + qoff,
+                          c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2), s),
+            "attend launch");
+  }
+  return BSATTN_OK;
+}
+
+int bsattn_select(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
+                  int32_t* idx_out, void* stream) {
+  if (!c || !q || !idx_out) return fail(BSATTN_ERR_INVALID, "null argument");
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  DeviceGuard dg(c->d.device);
+  return do_select(c, q, seqs, idx_out, (hipStream_t)stream);
+}
+
+int bsattn_attend(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
+                  const int32_t* idx, float scale, void* out, void* stream) {
+  if (!c || !q || !idx || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  DeviceGuard dg(c->d.device);
+  return do_attend(c, q, seqs, idx, scale, out, (hipStream_t)stream);
+}
+
+int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
+                  float scale, void* out, int32_t* idx_out, void* stream) {
+  if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  DeviceGuard dg(c->d.device);
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* idx = idx_out ? idx_out : c->idx_ws;
+  rc = do_select(c, q, seqs, idx, s);
+  if (rc) return rc;
+  return do_attend(c, q, seqs, idx, scale, out, s);
+}
+
+int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
+                int32_t* trimmed, void* stream) {
+  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (n_tokens < 0) return fail(BSATTN_ERR_INVALID, "n_tokens must be >= 0");
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  DeviceGuard dg(c->d.device);
+  std::vector<std::pair<int32_t, int32_t>> patches;
+  for (int i = 0; i < n_seqs; ++i) {
+    const int sq = seqs[i];
+    const int t = std::min(c->len[sq], n_tokens);
+    if (trimmed) trimmed[i] = t;
+    c->len[sq] -= t;
+    release_pages(c, sq, (c->len[sq] + c->d.block_size - 1) / c->d.block_size);
+    patches.emplace_back(sq, c->len[sq]);
+  }
+  return flush_patches(c, patches, (hipStream_t)stream);
+}
+
+int bsattn_reset(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* stream) {
+  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  DeviceGuard dg(c->d.device);
+  std::vector<std::pair<int32_t, int32_t>> patches;
+  for (int sq : seqs) {
+    c->len[sq] = 0;
+    release_pages(c, sq, 0);
+    patches.emplace_back(sq, 0);
+  }
+  return flush_patches(c, patches, (hipStream_t)stream);
+}
+
+int bsattn_copy(const bsattn_cache* src, bsattn_cache** out, void* stream) {
+  if (!src || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  int rc = bsattn_cache_create(&src->d, out);
+  if (rc) return rc;
+  bsattn_cache* c = *out;
+  DeviceGuard dg(src->d.device);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  if ((e = hipMemcpyAsync(c->geo.pool, src->geo.pool, src->pool_bytes, hipMemcpyDeviceToDevice, s)) != hipSuccess ||
+      (e = hipMemcpyAsync(c->geo.summ, src->geo.summ, src->summ_bytes, hipMemcpyDeviceToDevice, s)) != hipSuccess ||
+      (e = hipMemcpyAsync(c->geo.meta, src->geo.meta, src->meta_words * 4, hipMemcpyDeviceToDevice, s)) != hipSuccess) {
+    bsattn_cache_destroy(c);
+    *out = nullptr;
+    return hip_fail(e, "copy");
+  }
+  c->len = src->len;
+  c->pages = src->pages;
+  c->free_pages = src->free_pages;
+  return BSATTN_OK;
+}
+
+int bsattn_export(const bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* k_out,
+                  void* v_out, void* stream) {
+  if (!c || !k_out || !v_out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (c->d.kv_bits != 0) return fail(BSATTN_ERR_INVALID, "quantized cache: use bsattn_export_quantized");
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  const int T = c->len[seqs[0]];
+  for (int sq : seqs)
+    if (c->len[sq] != T) return fail(BSATTN_ERR_INVALID, "listed sequences hold different token counts");
+  if (T == 0) return BSATTN_OK;
+  DeviceGuard dg(c->d.device);
+  const size_t row = (size_t)c->geo.hkv * T * kHeadDim * 2;
+  for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
+    SeqBatch b{};
+    b.n = std::min(kMaxBatch, n_seqs - i0);
+    for (int i = 0; i < b.n; ++i) b.ids[i] = seqs[i0 + i];
+    HIP_TRY(launch_export(c->geo, b, T, (char*)k_out + i0 * row, (char*)v_out + i0 * row,
+                          (hipStream_t)stream),
+            "export launch");
+  }
+  return BSATTN_OK;
+}
+
+int bsattn_export_quantized(const bsattn_cache* c, const int32_t*, int32_t, uint32_t*, void*, void*,
+                            uint32_t*, void*, void*, void*) {
+  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  return fail(BSATTN_ERR_INVALID, "quantized caches are not available in this build");
+}
+
+int bsattn_export_summaries(const bsattn_cache* c, int32_t seq, void* out, void* stream) {
+  if (!c || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (seq < 0 || seq >= c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "sequence id %d out of range", seq);
+  const int nfull = c->len[seq] / c->d.block_size;
+  if (nfull == 0) return BSATTN_OK;
+  DeviceGuard dg(c->d.device);
+  HIP_TRY(launch_export_summaries(c->geo, seq, nfull, out, (hipStream_t)stream), "export summaries launch");
+  return BSATTN_OK;
+}
+
+}  // extern "C"

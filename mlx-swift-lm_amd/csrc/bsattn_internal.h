@@ -1,0 +1,83 @@
+// bsattn_internal.h -- shared between the kernels (bsattn_kernels.hip) and
+// the cache manager / C ABI (bsattn_capi.cpp).  Plain structs passed by
+// value as kernel arguments; no device code here.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace bsattn {
+
+constexpr int kHeadDim = 128;
+constexpr int kMaxBatch = 64;   // sequences per launch (host splits larger calls)
+constexpr int kMaxPatch = 240;  // metadata words patched per launch
+constexpr int kWaves = 4;       // waves per attention workgroup (one block each)
+
+// Static geometry of one cache, copied into every launch.
+struct Geometry {
+  int32_t hq, hkv, group;     // group = hq / hkv
+  int32_t tb;                 // tokens per block
+  int32_t dtype;              // 0 f16, 1 bf16
+  int32_t kv_bits;            // 0, 4, 8
+  int32_t gsize;              // affine group size
+  int32_t top_k, ns, nr, nsel_max, nsplit;
+  int32_t mbps;               // block-table width
+  int32_t bt_off;             // offset of the block table inside meta
+  int64_t slab_bytes;         // bytes of one (page, kv head) slab
+  // byte offsets inside a slab
+  int64_t k_off, v_off, ks_off, kb_off, vs_off, vb_off;
+  uint8_t* pool;              // [num_pages][hkv] slabs
+  uint16_t* summ;             // [num_pages][hkv][D]
+  int32_t* meta;              // [max_seqs] lengths, then [max_seqs][mbps] pages
+};
+
+struct SeqBatch {
+  int32_t n;
+  int32_t ids[kMaxBatch];
+};
+
+struct AppendBatch {
+  int32_t n, L;
+  int32_t seq[kMaxBatch];
+  int32_t old_len[kMaxBatch];
+};
+
+struct SummaryBatch {
+  int32_t n;
+  int32_t seq[kMaxBatch];
+  int32_t first[kMaxBatch];
+  int32_t count[kMaxBatch];
+};
+
+struct PatchBatch {
+  int32_t n;
+  int32_t idx[kMaxPatch];
+  int32_t val[kMaxPatch];
+};
+
+// launchers (bsattn_kernels.hip); return hipError_t of the launch
+hipError_t launch_patch(const Geometry& g, const PatchBatch& pb, hipStream_t s);
+hipError_t launch_append(const Geometry& g, const AppendBatch& ab, const void* k,
+                         const void* v, hipStream_t s);
+hipError_t launch_append_quantized(const Geometry& g, const AppendBatch& ab,
+                                   const uint32_t* kw, const void* ks, const void* kb,
+                                   const uint32_t* vw, const void* vs, const void* vb,
+                                   hipStream_t s);
+hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
+                          hipStream_t s);
+hipError_t launch_score(const Geometry& g, const SeqBatch& b, const void* q,
+                        float* scores, int max_cand, hipStream_t s);
+hipError_t launch_topk(const Geometry& g, const SeqBatch& b, const float* scores,
+                       int32_t* idx, hipStream_t s);
+hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q,
+                         const int32_t* idx, float scale, void* out, float* partials,
+                         hipStream_t s);
+hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out,
+                         void* v_out, hipStream_t s);
+hipError_t launch_export_quantized(const Geometry& g, const SeqBatch& b, int T,
+                                   uint32_t* kw, void* ks, void* kb, uint32_t* vw,
+                                   void* vs, void* vb, hipStream_t s);
+hipError_t launch_export_summaries(const Geometry& g, int seq, int nfull, void* out,
+                                   hipStream_t s);
+
+}  // namespace bsattn

@@ -1,0 +1,133 @@
+"""Shared helpers for the tests: seeded workload generation with the oracle's
+counter-based RNG, oracle evaluation per (sequence, kv head), and the GPU
+upload / comparison plumbing."""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import numpy as np
+
+import oracle as O
+
+DT = {"f16": O.F16, "bf16": O.BF16}
+
+# Streams of the counter-based RNG
+S_Q, S_K, S_V, S_SALIENT, S_LEN, S_SHUFFLE = 0, 1, 2, 3, 4, 5
+
+
+@dataclass
+class Workload:
+    """Seeded decode workload: sequences of (possibly different) lengths."""
+    seed: int
+    B: int
+    Hq: int
+    Hkv: int
+    D: int
+    Tb: int
+    dtype: str
+    lens: List[int]
+    top_k: int
+    ns: int = 1
+    nr: int = 1
+    salient_frac: float = 0.0
+    salient_mult: float = 8.0
+    q: np.ndarray = field(default=None, repr=False)       # [B, Hq, D]
+    keys: List[np.ndarray] = field(default=None, repr=False)    # per seq [Hkv, T, D]
+    values: List[np.ndarray] = field(default=None, repr=False)
+
+    @property
+    def G(self):
+        return self.Hq // self.Hkv
+
+    @property
+    def scale(self):
+        return 1.0 / math.sqrt(self.D)
+
+    @property
+    def nsel_max(self):
+        return self.ns + self.nr + self.top_k
+
+
+def make_workload(seed, B, Hq, Hkv, T, Tb, dtype, top_k, ns=1, nr=1, D=128,
+                  salient_frac=0.0, lens=None) -> Workload:
+    """Keys of sequence b, kv head h, token t, dim d use element index
+    ((b*Hkv + h)*Tcap + t)*D + d of stream 1 (values: stream 2); q uses
+    (b*Hq + hq)*D + d of stream 0.  salient_frac of each (b, h)'s token
+    positions (chosen on stream 3) have their keys scaled by 8 before
+    rounding."""
+    lens = list(lens) if lens is not None else [T] * B
+    Tcap = max(lens)
+    w = Workload(seed, B, Hq, Hkv, D, Tb, dtype, lens, top_k, ns, nr, salient_frac)
+    w.q = O.fill_normal(seed, S_Q, 0, (B, Hq, D), dtype)
+    w.keys, w.values = [], []
+    for b in range(B):
+        Tl = lens[b]
+        mult = None
+        if salient_frac > 0:
+            mult = np.ones((Hkv, Tl), np.float64)
+            cnt = int(round(salient_frac * Tl))
+            for h in range(Hkv):
+                pos = O.choose_positions(seed, S_SALIENT, b * Hkv + h, Tl, cnt)
+                mult[h, pos] = w.salient_mult
+        k = np.empty((Hkv, Tl, D), np.uint16)
+        v = np.empty((Hkv, Tl, D), np.uint16)
+        for h in range(Hkv):
+            start = ((b * Hkv + h) * Tcap) * D
+            k[h] = O.fill_normal(seed, S_K, start, (Tl, D), dtype,
+                                 row_mult=None if mult is None else mult[h])
+            v[h] = O.fill_normal(seed, S_V, start, (Tl, D), dtype)
+        w.keys.append(k)
+        w.values.append(v)
+    return w
+
+
+def oracle_decode(w: Workload):
+    """-> idx [B, Hkv, nsel_max] int32, out [B, Hq, D] float64, summaries per seq."""
+    idx = np.full((w.B, w.Hkv, w.nsel_max), -1, np.int32)
+    out = np.zeros((w.B, w.Hq, w.D), np.float64)
+    for b in range(w.B):
+        for h in range(w.Hkv):
+            i, n, o = O.decode_head(w.q[b, h * w.G:(h + 1) * w.G], w.keys[b][h], w.values[b][h],
+                                    w.Tb, w.ns, w.nr, w.top_k, w.scale, w.dtype)
+            idx[b, h] = i
+            out[b, h * w.G:(h + 1) * w.G] = o
+    return idx, out
+
+
+def oracle_summaries(w: Workload, b: int) -> np.ndarray:
+    return np.stack([O.summaries(w.keys[b][h], w.Tb, w.dtype) for h in range(w.Hkv)])
+
+
+def ulp(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Spacing of the output dtype at |x|."""
+    mant = 10 if dtype == "f16" else 7
+    ax = np.maximum(np.abs(x), 2.0 ** -14)
+    return 2.0 ** (np.floor(np.log2(ax)) - mant)
+
+
+def output_error(gpu_out: np.ndarray, ref: np.ndarray, dtype: str) -> float:
+    """Error of a dtype-rounded output against the fp64 oracle, net of the
+    final rounding to dtype: max(|gpu - ref| - ulp(ref)/2)."""
+    return float(np.max(np.abs(gpu_out - ref) - 0.5 * ulp(ref, dtype)))
+
+
+# ---------------------------------------------------------------------------
+# torch plumbing (GPU tests only)
+# ---------------------------------------------------------------------------
+
+def to_dev(a: np.ndarray, dtype: str, device):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a).view(np.int16))
+    return t.to(device).view(torch.float16 if dtype == "f16" else torch.bfloat16)
+
+
+def from_dev(t) -> np.ndarray:
+    import torch
+    return t.detach().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def torch_dtype(dtype: str):
+    import torch
+    return torch.float16 if dtype == "f16" else torch.bfloat16

@@ -1,0 +1,252 @@
+"""HIP path vs the CPU oracle, through the C ABI (libbsattn.so via ctypes).
+
+Bars:
+  * block summaries and selected block indices: bit-exact;
+  * attention outputs: max-abs error <= 2e-3 against the fp64 oracle, net of
+    the final rounding of the output to fp16/bf16 (|gpu - ref| - ulp(ref)/2).
+"""
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from common import (Workload, from_dev, make_workload, oracle_decode, oracle_summaries,
+                    output_error, to_dev, torch_dtype)
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def new_cache(w: Workload, mbps=None, num_pages=0):
+    from bsattn import BlockSparseKVCache
+    mbps = mbps or (max(w.lens) + w.Tb - 1) // w.Tb + 2
+    return BlockSparseKVCache(max_seqs=w.B, num_q_heads=w.Hq, num_kv_heads=w.Hkv, head_dim=w.D,
+                              block_size=w.Tb, dtype=torch_dtype(w.dtype), top_k=w.top_k,
+                              sink_blocks=w.ns, recent_blocks=w.nr, max_blocks_per_seq=mbps,
+                              num_pages=num_pages, device=0)
+
+
+def fill(cache, w: Workload, device, chunk=None, seed=7):
+    """Append every sequence's tokens; with `chunk`, round-robin in random-size
+    chunks so the sequences' pages interleave in the pool."""
+    if chunk is None:
+        for b in range(w.B):
+            if w.lens[b]:
+                cache.append(to_dev(w.keys[b][None], w.dtype, device),
+                             to_dev(w.values[b][None], w.dtype, device), seq_ids=[b])
+        return
+    rng = np.random.default_rng(seed)
+    pos = [0] * w.B
+    while any(pos[b] < w.lens[b] for b in range(w.B)):
+        for b in rng.permutation(w.B):
+            if pos[b] >= w.lens[b]:
+                continue
+            n = int(min(w.lens[b] - pos[b], rng.integers(1, chunk + 1)))
+            k = np.ascontiguousarray(w.keys[b][:, pos[b]:pos[b] + n][None])
+            v = np.ascontiguousarray(w.values[b][:, pos[b]:pos[b] + n][None])
+            cache.append(to_dev(k, w.dtype, device), to_dev(v, w.dtype, device), seq_ids=[int(b)])
+            pos[b] += n
+
+
+def run_and_check(cache, w: Workload, device, check_summaries=True):
+    import torch
+    q = to_dev(w.q[:, :, None, :], w.dtype, device)
+    idx_ref, out_ref = oracle_decode(w)
+    idx = cache.selectBlocks(q)
+    out = cache.attend(q, idx, w.scale)
+    out2 = cache.decode(q, w.scale)
+    torch.cuda.synchronize()
+    idx = idx.cpu().numpy()
+    assert np.array_equal(idx, idx_ref), f"selected blocks differ: {np.argwhere(idx != idx_ref)[:5]}"
+    got = O.to_f32(from_dev(out).reshape(w.B, w.Hq, w.D), w.dtype).astype(np.float64)
+    got2 = from_dev(out2).reshape(w.B, w.Hq, w.D)
+    assert np.array_equal(from_dev(out).reshape(w.B, w.Hq, w.D), got2), "decode != select + attend"
+    err = output_error(got, out_ref, w.dtype)
+    assert err <= TOL, f"output error {err:.3g} > {TOL}"
+    if check_summaries:
+        for b in range(w.B):
+            s = from_dev(cache.exportSummaries(b))
+            assert np.array_equal(s, oracle_summaries(w, b)), f"summaries differ for seq {b}"
+    return err
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_config1_single_decode(gpu, dtype):
+    """B=1, Hq=32, Hkv=8, D=128, 4096 tokens in 64-token blocks, top-8 + sink + newest."""
+    log(f"[config1] dtype={dtype}")
+    w = make_workload(1000, B=1, Hq=32, Hkv=8, T=4096, Tb=64, dtype=dtype, top_k=8)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    err = run_and_check(cache, w, gpu)
+    log(f"[config1] dtype={dtype} err={err:.3g}")
+
+
+def test_config2_batched_salient(gpu):
+    """B=8, 32k context, bf16, 1% of keys scaled x8, top-32 + sink + recent."""
+    log("[config2] generating")
+    w = make_workload(1001, B=8, Hq=32, Hkv=8, T=32768, Tb=64, dtype="bf16", top_k=32,
+                      salient_frac=0.01)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    err = run_and_check(cache, w, gpu)
+    log(f"[config2] err={err:.3g}")
+
+
+@pytest.mark.parametrize("dtype,Tb,Hq,Hkv", [
+    ("f16", 64, 32, 8), ("bf16", 64, 32, 8), ("f16", 32, 32, 8), ("bf16", 32, 64, 4),
+    ("f16", 64, 16, 16), ("bf16", 64, 16, 8), ("f16", 32, 16, 2),
+])
+def test_ragged_paged(gpu, dtype, Tb, Hq, Hkv):
+    """Ragged lengths (partial last blocks, shorter than one block, fewer
+    candidates than top_k) with interleaved page order."""
+    lens = [1, Tb - 1, Tb, Tb + 1, 7 * Tb + 5, 40 * Tb + 17, 23 * Tb]
+    log(f"[ragged] {dtype} Tb={Tb} Hq={Hq} Hkv={Hkv}")
+    w = make_workload(2000 + Tb + Hq, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb,
+                      dtype=dtype, top_k=6, ns=2, nr=2, lens=lens)
+    cache = new_cache(w)
+    fill(cache, w, gpu, chunk=3 * Tb + 7)
+    run_and_check(cache, w, gpu)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_topk_covering_all_blocks_is_dense(gpu, dtype):
+    """top_k >= number of blocks -> every block is attended and the result is
+    dense decode attention (the reference's path, AttentionUtils.swift:68-75)."""
+    w = make_workload(3000, B=2, Hq=32, Hkv=8, T=1000, Tb=64, dtype=dtype, top_k=64)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    run_and_check(cache, w, gpu)
+    import torch
+    q = to_dev(w.q[:, :, None, :], w.dtype, gpu)
+    out = O.to_f32(from_dev(cache.decode(q, w.scale)).reshape(w.B, w.Hq, w.D), dtype)
+    for b in range(w.B):
+        for h in range(w.Hkv):
+            ref = O.dense(w.q[b, h * 4:(h + 1) * 4], w.keys[b][h], w.values[b][h], w.scale, dtype)
+            assert output_error(out[b, h * 4:(h + 1) * 4].astype(np.float64), ref, dtype) <= TOL
+
+
+def test_ties_break_to_lower_index(gpu):
+    """Every full block of a sequence has the same keys -> equal scores ->
+    the lowest-index candidates are kept."""
+    w = make_workload(3100, B=2, Hq=32, Hkv=8, T=20 * 64 + 9, Tb=64, dtype="bf16", top_k=5)
+    for b in range(w.B):
+        for h in range(w.Hkv):
+            blk = w.keys[b][h][:64].copy()
+            for j in range(w.lens[b] // 64):
+                w.keys[b][h][j * 64:(j + 1) * 64] = blk
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    run_and_check(cache, w, gpu)
+    q = to_dev(w.q[:, :, None, :], w.dtype, gpu)
+    idx = cache.selectBlocks(q).cpu().numpy()
+    nb = -(-w.lens[0] // 64)
+    assert list(idx[0, 0]) == [0, 1, 2, 3, 4, 5, nb - 1]
+
+
+def test_decode_loop_with_appends(gpu):
+    """Variable-length sequences; each step appends one token per sequence
+    (crossing block boundaries, summaries refreshed on fill), then
+    select + attend; every step checked against the oracle."""
+    import torch
+    Tb, steps = 64, 70
+    lens0 = [100, 130, 190, 64]
+    total = [l + steps for l in lens0]
+    w = make_workload(3200, B=4, Hq=32, Hkv=8, T=max(total), Tb=Tb, dtype="f16", top_k=2,
+                      lens=total)
+    cache = new_cache(w)
+    for b in range(w.B):
+        k = np.ascontiguousarray(w.keys[b][:, :lens0[b]][None])
+        v = np.ascontiguousarray(w.values[b][:, :lens0[b]][None])
+        cache.append(to_dev(k, "f16", gpu), to_dev(v, "f16", gpu), seq_ids=[b])
+    worst = 0.0
+    for s in range(steps):
+        cur = [l + s + 1 for l in lens0]
+        k = np.stack([w.keys[b][:, cur[b] - 1:cur[b]] for b in range(w.B)])
+        v = np.stack([w.values[b][:, cur[b] - 1:cur[b]] for b in range(w.B)])
+        cache.append(to_dev(k, "f16", gpu), to_dev(v, "f16", gpu))
+        ws = Workload(w.seed, w.B, w.Hq, w.Hkv, w.D, Tb, "f16", cur, w.top_k, w.ns, w.nr)
+        ws.q = w.q
+        ws.keys = [w.keys[b][:, :cur[b]] for b in range(w.B)]
+        ws.values = [w.values[b][:, :cur[b]] for b in range(w.B)]
+        worst = max(worst, run_and_check(cache, ws, gpu, check_summaries=(s % 10 == 9)))
+    log(f"[decode-loop] worst err={worst:.3g}")
+
+
+def test_cache_contract_export_copy_trim(gpu):
+    """Structural contract of the reference's KVCacheTests
+    (Tests/MLXLMTests/KVCacheTests.swift:15-180): state round trip, copy()
+    independence, trim semantics."""
+    import torch
+    w = make_workload(3300, B=2, Hq=32, Hkv=8, T=300, Tb=64, dtype="bf16", top_k=2)
+    cache = new_cache(w, mbps=16)
+    fill(cache, w, gpu)
+    k, v = cache.state
+    assert tuple(k.shape) == (2, 8, 300, 128)
+    assert np.array_equal(from_dev(k), np.stack(w.keys))
+    assert np.array_equal(from_dev(v), np.stack(w.values))
+    assert cache.offset == 300 and cache.metaState[4] == "300"
+    # copy is independent
+    c2 = cache.copy()
+    extra = to_dev(np.stack(w.keys)[:, :, :5], "bf16", gpu)
+    c2.append(extra, extra)
+    assert c2.offset == 305 and cache.offset == 300
+    k1, _ = cache.state
+    assert np.array_equal(from_dev(k1), np.stack(w.keys))
+    # trim: back to 300 - 40 tokens then re-append the same 40 -> same results as before
+    assert cache.trim(40) == 40 and cache.offset == 260
+    tail_k = np.ascontiguousarray(np.stack(w.keys)[:, :, 260:])
+    tail_v = np.ascontiguousarray(np.stack(w.values)[:, :, 260:])
+    cache.append(to_dev(tail_k, "bf16", gpu), to_dev(tail_v, "bf16", gpu))
+    run_and_check(cache, w, gpu)
+    # trim clamps at the length
+    assert cache.trim(10_000) == 300 and cache.offset == 0
+    # state setter restores
+    cache.state = [k, v]
+    run_and_check(cache, w, gpu)
+    # reset returns every page
+    free_before = cache.freePages
+    cache.reset([0, 1])
+    assert cache.freePages == free_before + 2 * 5
+
+
+def test_attention_with_cache_update(gpu):
+    """attentionWithCacheUpdate: append the new token, then block-sparse decode."""
+    from bsattn import attentionWithCacheUpdate
+    T = 700
+    w = make_workload(3400, B=3, Hq=32, Hkv=8, T=T + 1, Tb=64, dtype="bf16", top_k=4)
+    cache = new_cache(w)
+    for b in range(w.B):
+        cache.append(to_dev(w.keys[b][None, :, :T], "bf16", gpu),
+                     to_dev(w.values[b][None, :, :T], "bf16", gpu), seq_ids=[b])
+    newk = np.ascontiguousarray(np.stack([w.keys[b][:, T:] for b in range(w.B)]))
+    newv = np.ascontiguousarray(np.stack([w.values[b][:, T:] for b in range(w.B)]))
+    q = to_dev(w.q[:, :, None, :], "bf16", gpu)
+    out = attentionWithCacheUpdate(q, to_dev(newk, "bf16", gpu), to_dev(newv, "bf16", gpu),
+                                   cache, w.scale)
+    _, ref = oracle_decode(w)
+    got = O.to_f32(from_dev(out).reshape(w.B, w.Hq, w.D), "bf16").astype(np.float64)
+    assert output_error(got, ref, "bf16") <= TOL
+
+
+def test_errors_are_status_codes(gpu):
+    from bsattn import BsattnError
+    w = make_workload(3500, B=1, Hq=32, Hkv=8, T=64, Tb=64, dtype="f16", top_k=2)
+    cache = new_cache(w, mbps=2, num_pages=2)
+    fill(cache, w, gpu)
+    big = to_dev(np.zeros((1, 8, 200, 128), np.uint16), "f16", gpu)
+    with pytest.raises(BsattnError) as e:
+        cache.append(big, big)  # would need 5 blocks > max_blocks_per_seq = 2
+    assert e.value.code == -4
+    assert cache.offset == 64  # failed call changed nothing
+    with pytest.raises(BsattnError):
+        cache.append(big[:, :, :64], big[:, :, :64], seq_ids=[3])  # bad sequence id
