@@ -9,7 +9,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libbsattn.so")
+# BSATTN_LIBRARY selects another build of the same C ABI (e.g. a tuning variant)
+LIB_PATH = os.environ.get("BSATTN_LIBRARY") or os.path.join(HERE, "libbsattn.so")
 
 OK = 0
 ERR_INVALID = -1

@@ -94,7 +94,8 @@ int validate_desc(const bsattn_desc& d) {
   if (d.max_blocks_per_seq < 1 || d.max_blocks_per_seq > 12288)
     return fail(BSATTN_ERR_INVALID, "max_blocks_per_seq %d out of range [1, 12288]", d.max_blocks_per_seq);
   const int64_t nsel = (int64_t)d.top_k + d.sink_blocks + d.recent_blocks;
-  if (nsel > 4096) return fail(BSATTN_ERR_INVALID, "sink + recent + top_k = %lld too large", (long long)nsel);
+  if (nsel > (int64_t)kMaxSplits * kWaves)
+    return fail(BSATTN_ERR_INVALID, "sink + recent + top_k = %lld exceeds %d", (long long)nsel, kMaxSplits * kWaves);
   if (d.num_pages < 0) return fail(BSATTN_ERR_INVALID, "num_pages must be >= 0");
   for (int r : d.reserved)
     if (r != 0) return fail(BSATTN_ERR_INVALID, "reserved fields must be 0");
@@ -210,7 +211,7 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   g.slab_bytes = 2 * g.v_off;
   g.ks_off = g.kb_off = g.vs_off = g.vb_off = 0;
   c->pool_bytes = (size_t)c->num_pages * g.hkv * g.slab_bytes;
-  c->summ_bytes = (size_t)c->num_pages * g.hkv * kHeadDim * 2;
+  c->summ_bytes = (size_t)d.max_seqs * g.hkv * g.mbps * kHeadDim * 2;
   c->meta_words = (size_t)d.max_seqs * (1 + d.max_blocks_per_seq);
   auto cleanup = [&](int code) {
     (void)hipFree(g.pool);
@@ -330,22 +331,19 @@ int bsattn_append_quantized(bsattn_cache* c, const uint32_t*, const void*, const
 
 static int do_select(bsattn_cache* c, const void* q, const std::vector<int32_t>& seqs,
                      int32_t* idx_out, hipStream_t s) {
-  const int tb = c->d.block_size;
   const int n = (int)seqs.size();
   for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
     SeqBatch b{};
     b.n = std::min(kMaxBatch, n - i0);
-    int max_cand = 0;
+    int max_chunks = 0;
     for (int i = 0; i < b.n; ++i) {
       b.ids[i] = seqs[i0 + i];
-      const int nb = (c->len[b.ids[i]] + tb - 1) / tb;
-      max_cand = std::max(max_cand, nb - c->geo.nr - c->geo.ns);
+      max_chunks = std::max(max_chunks, select_chunks(c->geo, c->len[b.ids[i]]));
     }
     const uint16_t* qq = (const uint16_t*)q + (size_t)i0 * c->geo.hq * kHeadDim;
     float* sc = c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps;
     int32_t* io = idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max;
-    if (max_cand > c->geo.top_k) HIP_TRY(launch_score(c->geo, b, qq, sc, max_cand, s), "score launch");
-    HIP_TRY(launch_topk(c->geo, b, sc, io, s), "top-k launch");
+    HIP_TRY(launch_select(c->geo, b, qq, sc, io, max_chunks, s), "select launch");
   }
   return BSATTN_OK;
 }

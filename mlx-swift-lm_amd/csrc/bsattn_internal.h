@@ -11,7 +11,11 @@ namespace bsattn {
 constexpr int kHeadDim = 128;
 constexpr int kMaxBatch = 64;   // sequences per launch (host splits larger calls)
 constexpr int kMaxPatch = 240;  // metadata words patched per launch
-constexpr int kWaves = 4;       // waves per attention workgroup (one block each)
+#ifndef BSATTN_WAVES
+#define BSATTN_WAVES 4
+#endif
+constexpr int kWaves = BSATTN_WAVES;  // waves per attention workgroup (one block each)
+constexpr int kMaxSplits = 256;       // attention splits per (sequence, kv head)
 
 // Static geometry of one cache, copied into every launch.
 struct Geometry {
@@ -27,7 +31,7 @@ struct Geometry {
   // byte offsets inside a slab
   int64_t k_off, v_off, ks_off, kb_off, vs_off, vb_off;
   uint8_t* pool;              // [num_pages][hkv] slabs
-  uint16_t* summ;             // [num_pages][hkv][D]
+  uint16_t* summ;             // [max_seqs][hkv][mbps][D], by logical block
   int32_t* meta;              // [max_seqs] lengths, then [max_seqs][mbps] pages
 };
 
@@ -65,10 +69,10 @@ hipError_t launch_append_quantized(const Geometry& g, const AppendBatch& ab,
                                    hipStream_t s);
 hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
                           hipStream_t s);
-hipError_t launch_score(const Geometry& g, const SeqBatch& b, const void* q,
-                        float* scores, int max_cand, hipStream_t s);
-hipError_t launch_topk(const Geometry& g, const SeqBatch& b, const float* scores,
-                       int32_t* idx, hipStream_t s);
+int select_chunks(const Geometry& g, int len);
+// scoring workgroups per (sequence, kv head) for `len` tokens (0: no ranking)
+hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                         int32_t* idx, int max_chunks, hipStream_t s);
 hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q,
                          const int32_t* idx, float scale, void* out, float* partials,
                          hipStream_t s);

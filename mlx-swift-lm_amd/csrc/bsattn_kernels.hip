@@ -2,10 +2,13 @@
 // path: append, block summary, block scoring, top-K select, gathered
 // split-K attention and the split combine.
 //
-// Page slab layout (one slab per (physical page, kv head), Tb tokens):
-//   K tile  [Tb][D]   token-major  (a token's key = 256 contiguous bytes)
-//   V tile  [D][Tb]   dim-major    (a dim's Tb values contiguous)
-// Summaries: [page][kv head][D], written when a block fills.
+// Page slab layout (one slab per (physical page, kv head), Tb tokens): the
+// K and V tiles are stored in MFMA-fragment-major order, i.e. as the
+// sequence of 1 KiB register fragments (64 lanes x 16 B) the attention
+// kernel feeds to v_mfma_f32_16x16x32, so every load instruction of the
+// gather reads 1 KiB of contiguous memory.  k_elem / v_elem give the element
+// offset of (token, dim).  Summaries: [seq][kv head][block][D], by logical
+// block, written when a block fills.
 //
 // Bit-exact parts (summary, score, selection) use __fadd_rn / __fmul_rn so
 // the compiler cannot contract or reorder them; the order is the one the
@@ -89,6 +92,31 @@ __device__ __forceinline__ const int32_t* block_table(const Geometry& g, int seq
 }
 
 // ---------------------------------------------------------------------------
+// fragment-major tile addressing (element offsets inside a K or V tile)
+//  K: fragment (t, s) for QK token tile t and k-step s; lane (m, g) holds
+//     dims 32*s + 8*g .. +7 of token tok_of(m / 4, 4*t + m % 4).
+//  V: fragment (dt, s2) for dim tile dt and PV k-step s2; lane (n, g) holds
+//     tokens 32*s2 + 8*g .. +7 of dim 16*dt + n.
+// tok_of(g, e) = 32*(e/8) + 8*g + e%8 is the token whose score lands in
+// accumulator entry e of lane group g (see k_attend).
+// ---------------------------------------------------------------------------
+__host__ __device__ inline int tok_of(int g, int e) { return 32 * (e >> 3) + 8 * g + (e & 7); }
+
+__host__ __device__ inline int k_elem(int tok, int d) {
+  const int e = 8 * (tok >> 5) + (tok & 7);  // accumulator entry of the token
+  const int t = e >> 2, m = 4 * ((tok >> 3) & 3) + (e & 3);
+  const int s = d >> 5, g = (d >> 3) & 3;
+  return (((t * 4 + s) * 64 + m + 16 * g) << 3) + (d & 7);
+}
+
+__host__ __device__ inline int v_elem(int tb, int tok, int d) {
+  const int ks2 = tb >> 5;
+  const int s2 = tok >> 5, g = (tok >> 3) & 3;
+  const int dt = d >> 4, n = d & 15;
+  return (((dt * ks2 + s2) * 64 + n + 16 * g) << 3) + (tok & 7);
+}
+
+// ---------------------------------------------------------------------------
 // metadata patch: meta[idx[i]] = val[i]
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_patch(int32_t* meta, PatchBatch pb) {
@@ -115,20 +143,26 @@ __global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
   const u32x4 kr = *(const u32x4*)(k + src);
   const u32x4 vr = *(const u32x4*)(v + src);
   uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
-  *(u32x4*)((uint16_t*)(slab + geo.k_off) + slot * kHeadDim + 8 * c) = kr;
+  // dims 8c .. 8c+7 of a key are 16 contiguous bytes of the K tile
+  *(u32x4*)((uint16_t*)(slab + geo.k_off) + k_elem(slot, 8 * c)) = kr;
   uint16_t* Vt = (uint16_t*)(slab + geo.v_off);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const uint32_t w = vr[e >> 1];
-    Vt[(8 * c + e) * geo.tb + slot] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xFFFFu));
+    Vt[v_elem(geo.tb, slot, 8 * c + e)] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xFFFFu));
   }
 }
 
 // ---------------------------------------------------------------------------
 // block summary: one workgroup per (block, kv head, sequence), one thread
 // per dim; sequential fp32 fold over the block's tokens, times 1/Tb.
+// Summaries are stored by logical block: summ[seq][kv head][block][D].
 // grid (max_count, Hkv, n)
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ uint16_t* summary_row(const Geometry& g, int seq, int h, int j) {
+  return g.summ + (((size_t)seq * g.hkv + h) * g.mbps + j) * kHeadDim;
+}
+
 template <int DT>
 __global__ __launch_bounds__(128) void k_summary(Geometry geo, SummaryBatch sb) {
   const int bi = blockIdx.z, h = blockIdx.y;
@@ -139,76 +173,19 @@ __global__ __launch_bounds__(128) void k_summary(Geometry geo, SummaryBatch sb) 
   const int d = threadIdx.x;
   const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
   const uint16_t* Kt = (const uint16_t*)(slab + geo.k_off);
-  float acc = to_f32<DT>(Kt[d]);
-  for (int t = 1; t < geo.tb; ++t) acc = __fadd_rn(acc, to_f32<DT>(Kt[t * kHeadDim + d]));
-  geo.summ[((size_t)page * geo.hkv + h) * kHeadDim + d] =
-      from_f32<DT>(__fmul_rn(acc, 1.0f / (float)geo.tb));
+  float acc = to_f32<DT>(Kt[k_elem(0, d)]);
+  for (int t = 1; t < geo.tb; ++t) acc = __fadd_rn(acc, to_f32<DT>(Kt[k_elem(t, d)]));
+  summary_row(geo, seq, h, j)[d] = from_f32<DT>(__fmul_rn(acc, 1.0f / (float)geo.tb));
 }
 
 // ---------------------------------------------------------------------------
-// block scoring: 16 lanes per (block, kv head) row, 8 dims per lane.
-// grid (ceil(max_cand / per_wg), n); needs 16 % Hkv == 0.
+// block scoring: workgroup (chunk, kv head, sequence) scores kSelChunk
+// candidate blocks of one (sequence, kv head); 16 lanes per block, 8 dims
+// per lane; summaries are contiguous by logical block, so every load issues
+// up front with no indirection.  grid (chunks, Hkv, n)
 // ---------------------------------------------------------------------------
-constexpr int kScoreIters = 8;
+constexpr int kSelChunk = 64;
 
-template <int DT, int G>
-__global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
-                                               const uint16_t* __restrict__ q,
-                                               float* __restrict__ scores) {
-  const int bi = blockIdx.y;
-  const int seq = sb.ids[bi];
-  const int len = geo.meta[seq];
-  const int nb = (len + geo.tb - 1) / geo.tb;
-  const int c0 = geo.ns, c1 = nb - geo.nr;
-  if (c1 - c0 <= geo.top_k) return;  // every candidate is kept; no ranking
-  const int r = threadIdx.x >> 4, c = threadIdx.x & 15;
-  const int hkv = geo.hkv;
-  const int h = r % hkv;
-  const int bpi = 16 / hkv;
-  const int bofs = r / hkv;
-  float qv[G][8];
-  const uint16_t* qrow = q + ((size_t)bi * geo.hq + h * G) * kHeadDim + 8 * c;
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const u32x4 raw = *(const u32x4*)(qrow + (size_t)g * kHeadDim);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      qv[g][e] = to_f32<DT>((uint16_t)((e & 1) ? (raw[e >> 1] >> 16) : (raw[e >> 1] & 0xFFFFu)));
-  }
-  const int32_t* bt = block_table(geo, seq);
-  float* srow = scores + ((size_t)bi * hkv + h) * geo.mbps;
-  const int jbase = c0 + blockIdx.x * (bpi * kScoreIters);
-  for (int it = 0; it < kScoreIters; ++it) {
-    const int j = jbase + it * bpi + bofs;
-    if (j >= c1) break;  // whole 16-lane row leaves together
-    const int page = bt[j];
-    const u32x4 raw = *(const u32x4*)(geo.summ + ((size_t)page * hkv + h) * kHeadDim + 8 * c);
-    float s[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      s[e] = to_f32<DT>((uint16_t)((e & 1) ? (raw[e >> 1] >> 16) : (raw[e >> 1] & 0xFFFFu)));
-    float best = 0.0f;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float acc = __fmul_rn(qv[g][0], s[0]);
-#pragma unroll
-      for (int e = 1; e < 8; ++e) acc = __fadd_rn(acc, __fmul_rn(qv[g][e], s[e]));
-      acc = __fadd_rn(acc, __shfl_xor(acc, 1, 64));
-      acc = __fadd_rn(acc, __shfl_xor(acc, 2, 64));
-      acc = __fadd_rn(acc, __shfl_xor(acc, 4, 64));
-      acc = __fadd_rn(acc, __shfl_xor(acc, 8, 64));
-      if (g == 0 || acc > best) best = acc;
-    }
-    if (c == 0) srow[j] = best;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// top-K select: one workgroup per (kv head, sequence).  MSB-first radix
-// select (4 x 8 bits) of the K-th largest key, then ties by ascending
-// index, then compaction of forced + chosen blocks in ascending order.
-// dynamic LDS: keys[mbps] (u32) + flags[mbps] (u8)
-// ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t score_key(float s) {
   if (__builtin_isnan(s)) return 0u;
   if (s == 0.0f) s = 0.0f;
@@ -216,12 +193,77 @@ __device__ __forceinline__ uint32_t score_key(float s) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+template <int DT>
+__device__ __forceinline__ void unpack8(const u32x4 raw, float* out) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    out[e] = to_f32<DT>((uint16_t)((e & 1) ? (raw[e >> 1] >> 16) : (raw[e >> 1] & 0xFFFFu)));
+}
+
+__host__ __device__ inline bool ranked_select(const Geometry& g, int nc) {
+  return nc > g.top_k && g.top_k > 0;
+}
+
+template <int DT, int G>
+__global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
+                                               const uint16_t* __restrict__ q,
+                                               float* __restrict__ scores) {
+  constexpr int P = kSelChunk / 16;
+  const int tid = threadIdx.x;
+  const int chunk = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
+  const int seq = sb.ids[bi];
+  const int len = geo.meta[seq];
+  const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
+  const int c0 = geo.ns, c1 = nb - geo.nr;
+  if (!ranked_select(geo, c1 - c0)) return;
+  const int j0 = c0 + chunk * kSelChunk + (tid >> 4);
+  if (j0 >= c1) return;  // rows are 16-lane aligned, so whole rows leave
+  const int c = tid & 15;
+  const uint16_t* sbase = summary_row(geo, seq, h, 0) + 8 * c;
+  u32x4 raw[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int j = j0 + 16 * p;
+    raw[p] = (j < c1) ? *(const u32x4*)(sbase + (size_t)j * kHeadDim) : u32x4{0u, 0u, 0u, 0u};
+  }
+  float qv[G][8];
+  const uint16_t* qrow = q + ((size_t)bi * geo.hq + h * G) * kHeadDim + 8 * c;
+#pragma unroll
+  for (int g = 0; g < G; ++g) unpack8<DT>(*(const u32x4*)(qrow + (size_t)g * kHeadDim), qv[g]);
+  float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int j = j0 + 16 * p;
+    if (j < c1) {
+      float s[8];
+      unpack8<DT>(raw[p], s);
+      float best = 0.0f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float acc = __fmul_rn(qv[g][0], s[0]);
+#pragma unroll
+        for (int e = 1; e < 8; ++e) acc = __fadd_rn(acc, __fmul_rn(qv[g][e], s[e]));
+        acc = __fadd_rn(acc, __shfl_xor(acc, 1, 64));
+        acc = __fadd_rn(acc, __shfl_xor(acc, 2, 64));
+        acc = __fadd_rn(acc, __shfl_xor(acc, 4, 64));
+        acc = __fadd_rn(acc, __shfl_xor(acc, 8, 64));
+        if (g == 0 || acc > best) best = acc;
+      }
+      if (c == 0) srow[j] = best;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// top-K select: one workgroup per (kv head, sequence).  MSB-first radix
+// select (4 x 8 bits) of the K-th largest key, ties by ascending index, then
+// compaction of forced + chosen blocks in ascending order.
+// dynamic LDS: keys[mbps] (u32) + flags[mbps] (u8).  grid (Hkv, n)
+// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_topk(Geometry geo, SeqBatch sb,
                                               const float* __restrict__ scores,
                                               int32_t* __restrict__ idx_out) {
   extern __shared__ uint32_t smem[];
-  uint32_t* keys = smem;
-  uint8_t* flags = (uint8_t*)(smem + geo.mbps);
   __shared__ uint32_t hist[256];
   __shared__ int s_tmp[4];
   __shared__ int s_sel[2];
@@ -230,14 +272,18 @@ __global__ __launch_bounds__(256) void k_topk(Geometry geo, SeqBatch sb,
   const int seq = sb.ids[bi];
   const int len = geo.meta[seq];
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
-  int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
   const int c0 = geo.ns, c1 = nb - geo.nr, nc = c1 - c0;
+  const bool ranked = ranked_select(geo, nc);
+  const float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
+  uint32_t* keys = smem;
+  uint8_t* flags = (uint8_t*)(smem + geo.mbps);
+  int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
+  if (ranked)
+    for (int i = tid; i < nc; i += 256) keys[i] = score_key(srow[c0 + i]);
   for (int j = tid; j < nb; j += 256)
-    flags[j] = (j < geo.ns || j >= nb - geo.nr || (nc > 0 && nc <= geo.top_k)) ? 1 : 0;
+    flags[j] = (j < geo.ns || j >= nb - geo.nr || (nc > 0 && !ranked)) ? 1 : 0;
   __syncthreads();
-  if (nc > geo.top_k && geo.top_k > 0) {
-    const float* sc = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
-    for (int i = tid; i < nc; i += 256) keys[i] = score_key(sc[c0 + i]);
+  if (ranked) {
     uint32_t prefix = 0u, mask = 0u;
     int krem = geo.top_k;
     for (int sh = 24; sh >= 0; sh -= 8) {
@@ -292,70 +338,73 @@ __global__ __launch_bounds__(256) void k_topk(Geometry geo, SeqBatch sb,
 }
 
 // ---------------------------------------------------------------------------
-// gathered attention.  Workgroup = 4 waves = 4 consecutive selected slots of
+// gathered attention.  Workgroup = W waves = W consecutive selected slots of
 // one (sequence, kv head); each wave does one block with MFMA 16x16x32:
-//   S^T[token][head] = K[token][:] . Q[head][:]   (A = K rows, B = Q^T)
-//   O[head][dim]     = P[head][token] . V[token][dim]  (A = P, B = V)
-// Token order inside the QK tiles is chosen so that the S accumulator of
-// lane (head n, group g) holds tokens TPG*g .. TPG*g+TPG-1, which is exactly
-// the A-operand layout the PV product needs (no shuffles).  Any permutation
-// of the contraction index is legal as long as A and B agree; the head-dim
-// chunk of lane group g at k-step s is dims 32*g + 8*s .. +7.
+//   S^T[token][head] = K[token][:] . Q[head][:]       (A = K rows, B = Q^T)
+//   O[head][dim]     = P[head][token] . V[token][dim] (A = P,      B = V)
+// The contraction index may be permuted freely as long as A and B agree:
+//  - QK, k-step s, lane group g: head dims 32*s + 8*g .. +7;
+//  - the QK tile rows are ordered so that the S accumulator of lane (head n,
+//    group g) holds tokens tok_of(g, e), e = 0..Tb/4-1, which is the
+//    A-operand layout PV needs (no shuffles).
+// The tiles are stored fragment-major, so each K/V load is 1 KiB contiguous.
 // bf16: P is split into hi + lo bf16 parts (two MFMAs) for ~16-bit P.
+// Every K/V load of a wave is issued before the first wait (a scheduling
+// barrier keeps the compiler from interleaving them with the MFMAs), so
+// each wave pays one memory round trip.
+// With more than one split, each workgroup writes an unnormalised partial
+// (o, m, l) for k_combine.
 // grid (nsplit, Hkv, n)
 // ---------------------------------------------------------------------------
-template <int DT, int TB, int G>
-__global__ __launch_bounds__(256) void k_attend(Geometry geo, SeqBatch sb,
-                                                const uint16_t* __restrict__ q,
-                                                const int32_t* __restrict__ idx,
-                                                float sl2, uint16_t* __restrict__ out,
-                                                float* __restrict__ partials) {
+template <int DT, int TB, int G, int W>
+__global__ __launch_bounds__(64 * W) void k_attend(Geometry geo, SeqBatch sb,
+                                                   const uint16_t* __restrict__ q,
+                                                   const int32_t* __restrict__ idx,
+                                                   float sl2, uint16_t* __restrict__ out,
+                                                   float* __restrict__ partials) {
   constexpr int NT = TB / 16;   // QK token tiles
-  constexpr int TPG = TB / 4;   // tokens per lane group
+  constexpr int EPL = TB / 4;   // scores per lane
   constexpr int KS2 = TB / 32;  // PV k-steps
-  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
-  __shared__ float s_o[kWaves][G][kHeadDim];
+  constexpr int NTH = 64 * W;
+  __shared__ float s_m[W][16], s_l[W][16];
+  __shared__ float s_o[W][G][kHeadDim];
   const int split = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int seq = sb.ids[bi];
-  const int slot = split * kWaves + wave;
+  const int slot = split * W + wave;
   int j = -1;
   if (slot < geo.nsel_max) j = idx[((size_t)bi * geo.hkv + h) * geo.nsel_max + slot];
   j = uniform(j);
   const int len = uniform(geo.meta[seq]);
   // -1 and indices past the sequence's last block contribute nothing
   if (j >= geo.mbps || (int64_t)j * TB >= len) j = -1;
+  u32x4 qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
+  if (n < G) {
+    const uint16_t* src = q + ((size_t)bi * geo.hq + h * G + n) * kHeadDim + 8 * g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = *(const u32x4*)(src + 32 * s);
+  }
   if (j >= 0) {
     const int page = uniform(block_table(geo, seq)[j]);
     const int valid = min(TB, len - j * TB);
     const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
-    const uint16_t* Kt = (const uint16_t*)(slab + geo.k_off);
-    const uint16_t* Vt = (const uint16_t*)(slab + geo.v_off);
+    // fragment-major tiles: fragment f of lane l is 16 B at (f * 64 + l) * 16
+    const u32x4* Kf = (const u32x4*)(slab + geo.k_off) + lane;
+    const u32x4* Vf = (const u32x4*)(slab + geo.v_off) + lane;
     u32x4 kf[NT][4];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int tok = TPG * (n >> 2) + 4 * t + (n & 3);
-      const u32x4* src = (const u32x4*)(Kt + tok * kHeadDim + 32 * g);
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kf[t][s] = src[s];
-    }
+      for (int s = 0; s < 4; ++s) kf[t][s] = __builtin_nontemporal_load(Kf + (t * 4 + s) * 64);
     u32x4 vf[8][KS2];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const u32x4* src = (const u32x4*)(Vt + (16 * dt + n) * TB + TPG * g);
+    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int s2 = 0; s2 < KS2; ++s2) vf[dt][s2] = src[s2];
-    }
-    u32x4 qf[4];
-    if (n < G) {
-      const u32x4* src = (const u32x4*)(q + ((size_t)bi * geo.hq + h * G + n) * kHeadDim + 32 * g);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qf[s] = src[s];
-    } else {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
-    }
+      for (int s2 = 0; s2 < KS2; ++s2) vf[dt][s2] = __builtin_nontemporal_load(Vf + (dt * KS2 + s2) * 64);
+    __builtin_amdgcn_sched_barrier(0);
     // S^T = K . Q^T
     f32x4 acc[NT];
 #pragma unroll
@@ -365,7 +414,7 @@ __global__ __launch_bounds__(256) void k_attend(Geometry geo, SeqBatch sb,
       for (int s = 0; s < 4; ++s) acc[t] = mfma16x16x32<DT>(kf[t][s], qf[s], acc[t]);
     }
     // softmax over this block (log2 domain)
-    float pv[TPG];
+    float pv[EPL];
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -373,7 +422,7 @@ __global__ __launch_bounds__(256) void k_attend(Geometry geo, SeqBatch sb,
       for (int i = 0; i < 4; ++i) {
         const int e = 4 * t + i;
         float x = acc[t][i] * sl2;
-        if (TPG * g + e >= valid) x = -INFINITY;
+        if (tok_of(g, e) >= valid) x = -INFINITY;
         pv[e] = x;
         mx = fmaxf(mx, x);
       }
@@ -381,14 +430,15 @@ __global__ __launch_bounds__(256) void k_attend(Geometry geo, SeqBatch sb,
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     float ps = 0.f;
 #pragma unroll
-    for (int e = 0; e < TPG; ++e) {
+    for (int e = 0; e < EPL; ++e) {
       const float p = (n < G) ? __builtin_amdgcn_exp2f(pv[e] - mx) : 0.f;
       pv[e] = p;
       ps += p;
     }
     ps += __shfl_xor(ps, 16, 64);
     ps += __shfl_xor(ps, 32, 64);
-    // P operand (A): lane (head n, group g), k-step s2 -> tokens TPG*g + 8*s2 + 0..7
+    // P operand (A): lane (head n, group g), k-step s2, element 2*jj (+1)
+    // -> tokens tok_of(g, 8*s2 + 2*jj (+1)) = 32*s2 + 8*g + 2*jj (+1)
     u32x4 pf[KS2];
     u32x4 pl[KS2];
 #pragma unroll
@@ -411,7 +461,7 @@ __global__ __launch_bounds__(256) void k_attend(Geometry geo, SeqBatch sb,
       for (int s2 = 0; s2 < KS2; ++s2)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int t0 = TPG * g + 8 * s2 + 2 * jj;
+          const int t0 = 32 * s2 + 8 * g + 2 * jj;
           const uint32_t m = (t0 < valid ? 0x0000FFFFu : 0u) | (t0 + 1 < valid ? 0xFFFF0000u : 0u);
 #pragma unroll
           for (int dt = 0; dt < 8; ++dt) vf[dt][s2][jj] &= m;
@@ -445,15 +495,15 @@ __global__ __launch_bounds__(256) void k_attend(Geometry geo, SeqBatch sb,
   }
   __syncthreads();
   const int nsplit = geo.nsplit;
-  for (int e = threadIdx.x; e < G * kHeadDim; e += 256) {
+  for (int e = threadIdx.x; e < G * kHeadDim; e += NTH) {
     const int head = e / kHeadDim, d = e % kHeadDim;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][head]);
+    for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][head]);
     float L = 0.f, a = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < W; ++w) {
         const float mw = s_m[w][head];
         const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
         L += f * s_l[w][head];
@@ -475,28 +525,45 @@ __global__ __launch_bounds__(256) void k_attend(Geometry geo, SeqBatch sb,
 }
 
 // ---------------------------------------------------------------------------
-// combine split partials: one workgroup per (q head, sequence)
+// combine split partials: one workgroup per (q head, sequence).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_reduce_128(float v, bool is_max, float* s_red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float u = __shfl_xor(v, o, 64);
+    v = is_max ? fmaxf(v, u) : v + u;
+  }
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = is_max ? fmaxf(s_red[0], s_red[1]) : s_red[0] + s_red[1];
+  __syncthreads();
+  return v;
+}
+
 template <int DT>
 __global__ __launch_bounds__(128) void k_combine(Geometry geo, const float* __restrict__ partials,
                                                  uint16_t* __restrict__ out) {
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_red[2];
   const int hq = blockIdx.x, bi = blockIdx.y, d = threadIdx.x;
   const size_t row = (size_t)bi * geo.hq + hq;
   const int ns = geo.nsplit;
   const float* pp = partials + row * ns * (kHeadDim + 2);
   float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, pp[s * (kHeadDim + 2) + kHeadDim]);
-  float L = 0.f, a = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < ns; ++s) {
-      const float m = pp[s * (kHeadDim + 2) + kHeadDim];
-      if (m == -INFINITY) continue;
-      const float f = __builtin_amdgcn_exp2f(m - M);
-      L += f * pp[s * (kHeadDim + 2) + kHeadDim + 1];
-      a += f * pp[s * (kHeadDim + 2) + d];
-    }
+  for (int sp = d; sp < ns; sp += 128) M = fmaxf(M, pp[sp * (kHeadDim + 2) + kHeadDim]);
+  M = block_reduce_128(M, true, s_red);
+  float wl = 0.f;
+  for (int sp = d; sp < ns; sp += 128) {
+    const float m = pp[sp * (kHeadDim + 2) + kHeadDim];
+    const float w = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    s_w[sp] = w;
+    wl += w * pp[sp * (kHeadDim + 2) + kHeadDim + 1];
   }
-  out[row * kHeadDim + d] = from_f32<DT>(L > 0.f ? a / L : 0.f);
+  wl = block_reduce_128(wl, false, s_red);  // also orders the s_w writes
+  const float inv = wl > 0.f ? 1.f / wl : 0.f;
+  float a = 0.f;
+  for (int sp = 0; sp < ns; ++sp) a += s_w[sp] * pp[sp * (kHeadDim + 2) + d];
+  out[row * kHeadDim + d] = from_f32<DT>(a * inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -514,13 +581,13 @@ __global__ __launch_bounds__(256) void k_export(Geometry geo, SeqBatch sb, int T
   const int page = block_table(geo, seq)[blk];
   const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
   const size_t dst = (((size_t)bi * geo.hkv + h) * T + tok) * kHeadDim + 8 * c;
-  *(u32x4*)(ko + dst) = *(const u32x4*)((const uint16_t*)(slab + geo.k_off) + slot * kHeadDim + 8 * c);
+  *(u32x4*)(ko + dst) = *(const u32x4*)((const uint16_t*)(slab + geo.k_off) + k_elem(slot, 8 * c));
   const uint16_t* Vt = (const uint16_t*)(slab + geo.v_off);
   u32x4 w;
 #pragma unroll
   for (int e = 0; e < 4; ++e)
-    w[e] = (uint32_t)Vt[(8 * c + 2 * e) * geo.tb + slot] |
-           ((uint32_t)Vt[(8 * c + 2 * e + 1) * geo.tb + slot] << 16);
+    w[e] = (uint32_t)Vt[v_elem(geo.tb, slot, 8 * c + 2 * e)] |
+           ((uint32_t)Vt[v_elem(geo.tb, slot, 8 * c + 2 * e + 1)] << 16);
   *(u32x4*)(vo + dst) = w;
 }
 
@@ -528,8 +595,7 @@ __global__ __launch_bounds__(256) void k_export(Geometry geo, SeqBatch sb, int T
 __global__ __launch_bounds__(128) void k_export_summaries(Geometry geo, int seq, int nfull,
                                                           uint16_t* __restrict__ out) {
   const int j = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-  const int page = block_table(geo, seq)[j];
-  out[((size_t)h * nfull + j) * kHeadDim + d] = geo.summ[((size_t)page * geo.hkv + h) * kHeadDim + d];
+  out[((size_t)h * nfull + j) * kHeadDim + d] = summary_row(geo, seq, h, j)[d];
 }
 
 // ===========================================================================
@@ -576,17 +642,21 @@ static void score_dispatch(const Geometry& g, dim3 grid, const SeqBatch& b, cons
   }
 }
 
-hipError_t launch_score(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                        int max_cand, hipStream_t s) {
-  const int per_wg = (16 / g.hkv) * kScoreIters;
-  dim3 grid((max_cand + per_wg - 1) / per_wg, b.n);
-  if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s);
-  else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s);
-  return hipGetLastError();
+int select_chunks(const Geometry& g, int len) {
+  const int nb = len > 0 ? (len + g.tb - 1) / g.tb : 0;
+  const int nc = nb - g.nr - g.ns;
+  return ranked_select(g, nc) ? (nc + kSelChunk - 1) / kSelChunk : 0;
 }
 
-hipError_t launch_topk(const Geometry& g, const SeqBatch& b, const float* scores, int32_t* idx,
-                       hipStream_t s) {
+hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                         int32_t* idx, int max_chunks, hipStream_t s) {
+  if (max_chunks > 0) {
+    dim3 grid(max_chunks, g.hkv, b.n);
+    if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s);
+    else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   const size_t lds = (size_t)g.mbps * 5;
   hipLaunchKernelGGL(k_topk, dim3(g.hkv, b.n), dim3(256), lds, s, g, b, scores, idx);
   return hipGetLastError();
@@ -596,12 +666,14 @@ template <int DT, int TB>
 static void attend_dispatch(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
                             const int32_t* idx, float sl2, uint16_t* out, float* part,
                             hipStream_t s) {
+  constexpr int W = kWaves;
+  const dim3 blk(64 * W);
   switch (g.group) {
-    case 1: hipLaunchKernelGGL((k_attend<DT, TB, 1>), grid, dim3(256), 0, s, g, b, q, idx, sl2, out, part); break;
-    case 2: hipLaunchKernelGGL((k_attend<DT, TB, 2>), grid, dim3(256), 0, s, g, b, q, idx, sl2, out, part); break;
-    case 4: hipLaunchKernelGGL((k_attend<DT, TB, 4>), grid, dim3(256), 0, s, g, b, q, idx, sl2, out, part); break;
-    case 8: hipLaunchKernelGGL((k_attend<DT, TB, 8>), grid, dim3(256), 0, s, g, b, q, idx, sl2, out, part); break;
-    default: hipLaunchKernelGGL((k_attend<DT, TB, 16>), grid, dim3(256), 0, s, g, b, q, idx, sl2, out, part); break;
+    case 1: hipLaunchKernelGGL((k_attend<DT, TB, 1, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
+    case 2: hipLaunchKernelGGL((k_attend<DT, TB, 2, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
+    case 4: hipLaunchKernelGGL((k_attend<DT, TB, 4, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
+    case 8: hipLaunchKernelGGL((k_attend<DT, TB, 8, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
+    default: hipLaunchKernelGGL((k_attend<DT, TB, 16, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
   }
 }
 

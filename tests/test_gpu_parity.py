@@ -239,14 +239,50 @@ def test_attention_with_cache_update(gpu):
 
 
 def test_errors_are_status_codes(gpu):
+    """Misuse returns a status code and leaves the cache unchanged."""
     from bsattn import BsattnError
-    w = make_workload(3500, B=1, Hq=32, Hkv=8, T=64, Tb=64, dtype="f16", top_k=2)
-    cache = new_cache(w, mbps=2, num_pages=2)
+    w = make_workload(3500, B=2, Hq=32, Hkv=8, T=64, Tb=64, dtype="f16", top_k=2, lens=[64, 0])
+    cache = new_cache(w, mbps=4, num_pages=3)
     fill(cache, w, gpu)
-    big = to_dev(np.zeros((1, 8, 200, 128), np.uint16), "f16", gpu)
+    big = to_dev(np.zeros((1, 8, 300, 128), np.uint16), "f16", gpu)
     with pytest.raises(BsattnError) as e:
-        cache.append(big, big)  # would need 5 blocks > max_blocks_per_seq = 2
+        cache.append(big, big)  # 364 tokens > max_blocks_per_seq * block_size = 256
     assert e.value.code == -4
-    assert cache.offset == 64  # failed call changed nothing
-    with pytest.raises(BsattnError):
-        cache.append(big[:, :, :64], big[:, :, :64], seq_ids=[3])  # bad sequence id
+    assert cache.offset == 64  # the failed call changed nothing
+    small = big[:, :, :64].contiguous()
+    with pytest.raises(BsattnError) as e:
+        cache.append(small, small, seq_ids=[3])  # sequence id out of range
+    assert e.value.code == -4
+    mid = big[:, :, :192].contiguous()
+    with pytest.raises(BsattnError) as e:
+        cache.append(mid, mid, seq_ids=[1])  # needs 3 pages, 2 free
+    assert e.value.code == -3
+    assert cache.seqLen(1) == 0 and cache.freePages == 2
+
+
+def test_graph_replay_matches_eager(gpu):
+    """decode captured in a HIP graph: every replay, with eager work and
+    synchronizations in between, equals the eager result."""
+    import torch
+    w = make_workload(3600, B=4, Hq=32, Hkv=8, T=3000, Tb=64, dtype="bf16", top_k=8)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    q = to_dev(w.q[:, :, None, :], "bf16", gpu)
+    eager = cache.decode(q, w.scale)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        cache.decode(q, w.scale)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = cache.decode(q, w.scale)
+    for r in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {r} differs"
+        other = cache.decode(q, w.scale)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
