@@ -394,10 +394,35 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
   hipStream_t s = (hipStream_t)stream;
-  int32_t* idx = idx_out ? idx_out : c->idx_ws;
-  rc = do_select(c, q, seqs, idx, s);
-  if (rc) return rc;
-  return do_attend(c, q, seqs, idx, scale, out, s);
+  // the selection runs inside the attention kernel when every sequence has
+  // few enough candidate blocks; otherwise select, then attend
+  const int tb = c->d.block_size;
+  int max_nc = 0;
+  for (int sq : seqs) max_nc = std::max(max_nc, (c->len[sq] + tb - 1) / tb - c->geo.ns - c->geo.nr);
+  if (max_nc > fused_select_limit(c->geo.top_k)) {
+    int32_t* idx = idx_out ? idx_out : c->idx_ws;
+    rc = do_select(c, q, seqs, idx, s);
+    if (rc) return rc;
+    return do_attend(c, q, seqs, idx, scale, out, s);
+  }
+  const int n = (int)seqs.size();
+  for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
+    SeqBatch b{};
+    b.n = std::min(kMaxBatch, n - i0);
+    int max_chunks = 0;
+    for (int i = 0; i < b.n; ++i) {
+      b.ids[i] = seqs[i0 + i];
+      max_chunks = std::max(max_chunks, select_chunks(c->geo, c->len[b.ids[i]]));
+    }
+    const size_t qoff = (size_t)i0 * c->geo.hq * kHeadDim * 2;
+    HIP_TRY(launch_decode(c->geo, b, (const char*)q + qoff,
+                          c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps,
+                          idx_out ? idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max : nullptr,
+                          max_chunks, scale, (char*)out + qoff,
+                          c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2), s),
+            "decode launch");
+  }
+  return BSATTN_OK;
 }
 
 int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,

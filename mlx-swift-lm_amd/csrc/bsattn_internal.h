@@ -76,6 +76,13 @@ hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, fl
 hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q,
                          const int32_t* idx, float scale, void* out, float* partials,
                          hipStream_t s);
+// decode = scoring + attention with the top-K selection done inside the
+// attention kernel; valid while every sequence has at most
+// fused_select_limit(top_k) candidate blocks.  idx_out may be null.
+int fused_select_limit(int top_k);
+hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                         int32_t* idx_out, int max_chunks, float scale, void* out,
+                         float* partials, hipStream_t s);
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out,
                          void* v_out, hipStream_t s);
 hipError_t launch_export_quantized(const Geometry& g, const SeqBatch& b, int T,

@@ -212,37 +212,38 @@ __global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
   const int tid = threadIdx.x;
   const int chunk = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int seq = sb.ids[bi];
-  const int len = geo.meta[seq];
-  const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
-  const int c0 = geo.ns, c1 = nb - geo.nr;
-  if (!ranked_select(geo, c1 - c0)) return;
-  const int j0 = c0 + chunk * kSelChunk + (tid >> 4);
-  if (j0 >= c1) return;  // rows are 16-lane aligned, so whole rows leave
   const int c = tid & 15;
+  const int j0 = geo.ns + chunk * kSelChunk + (tid >> 4);
+  // summary rows below the block-table width are always in bounds, so the
+  // loads are issued before the sequence length is known
   const uint16_t* sbase = summary_row(geo, seq, h, 0) + 8 * c;
   u32x4 raw[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int j = j0 + 16 * p;
-    raw[p] = (j < c1) ? *(const u32x4*)(sbase + (size_t)j * kHeadDim) : u32x4{0u, 0u, 0u, 0u};
+    raw[p] = (j < geo.mbps) ? *(const u32x4*)(sbase + (size_t)j * kHeadDim) : u32x4{0u, 0u, 0u, 0u};
   }
   float qv[G][8];
   const uint16_t* qrow = q + ((size_t)bi * geo.hq + h * G) * kHeadDim + 8 * c;
 #pragma unroll
   for (int g = 0; g < G; ++g) unpack8<DT>(*(const u32x4*)(qrow + (size_t)g * kHeadDim), qv[g]);
+  const int len = geo.meta[seq];
+  const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
+  const int c1 = nb - geo.nr;
+  if (!ranked_select(geo, c1 - geo.ns)) return;
   float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int j = j0 + 16 * p;
-    if (j < c1) {
-      float s[8];
-      unpack8<DT>(raw[p], s);
+    if (j < c1) {  // rows are 16-lane aligned: a row enters or skips as a whole
+      float sv[8];
+      unpack8<DT>(raw[p], sv);
       float best = 0.0f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float acc = __fmul_rn(qv[g][0], s[0]);
+        float acc = __fmul_rn(qv[g][0], sv[0]);
 #pragma unroll
-        for (int e = 1; e < 8; ++e) acc = __fadd_rn(acc, __fmul_rn(qv[g][e], s[e]));
+        for (int e = 1; e < 8; ++e) acc = __fadd_rn(acc, __fmul_rn(qv[g][e], sv[e]));
         acc = __fadd_rn(acc, __shfl_xor(acc, 1, 64));
         acc = __fadd_rn(acc, __shfl_xor(acc, 2, 64));
         acc = __fadd_rn(acc, __shfl_xor(acc, 4, 64));
@@ -255,9 +256,94 @@ __global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
 }
 
 // ---------------------------------------------------------------------------
-// top-K select: one workgroup per (kv head, sequence).  MSB-first radix
-// select (4 x 8 bits) of the K-th largest key, ties by ascending index, then
-// compaction of forced + chosen blocks in ascending order.
+// wave-level top-K of one (sequence, kv head): the same selection as the
+// oracle (K largest keys, ties to the lower index), computed by one wave with
+// no LDS atomics and no workgroup barriers.  Lane l holds candidates
+// c0 + l + 64*k, k < S (S a power of two; padded keys are 0).  tau = the
+// K-th largest key is found bit by bit from the top: a candidate prefix
+// (always >= 1, so padded keys never count) stays if at least K keys are
+// >= it, counted with ballots.  Candidates c0 .. c0+nc-1, nc <= 64 * S,
+// nc > K > 0.  Writes the K chosen block indices, ascending, to sel_blk and
+// their pages (from bt) to sel_page when sel_page is not null.
+// ---------------------------------------------------------------------------
+constexpr int kSelKeysPerLane = 16;
+constexpr int kSelMaxK = 256;  // top_k limit of the in-kernel selection
+
+template <int S>
+__device__ __forceinline__ void wave_topk_s(const float* __restrict__ srow,
+                                            const int32_t* __restrict__ bt, int c0, int nc,
+                                            int K, int* sel_blk, int* sel_page) {
+  const int lane = threadIdx.x & 63;
+  uint32_t key[S];
+  int page[S];
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    const int i = lane + 64 * k;
+    const bool real = i < nc;
+    key[k] = real ? score_key(srow[c0 + i]) : 0u;
+    page[k] = (real && sel_page) ? bt[c0 + i] : 0;
+  }
+  uint32_t tau = 0u;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int k = 0; k < S; ++k) cnt += __popcll(__ballot(key[k] >= cand));
+    if (cnt >= K) tau = cand;
+  }
+  // keys > tau are taken; of the keys == tau, the krem lowest indices
+  int gt_total = 0;
+#pragma unroll
+  for (int k = 0; k < S; ++k) gt_total += __popcll(__ballot(key[k] > tau));
+  const int krem = K - gt_total;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int sel_before = 0, ties_before = 0;
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    const int i = lane + 64 * k;
+    const bool eq = i < nc && key[k] == tau;
+    const uint64_t eqm = __ballot(eq);
+    const bool take = key[k] > tau || (eq && ties_before + __popcll(eqm & below) < krem);
+    const uint64_t tm = __ballot(take);
+    if (take) {
+      const int pos = sel_before + __popcll(tm & below);
+      sel_blk[pos] = c0 + i;
+      if (sel_page) sel_page[pos] = page[k];
+    }
+    sel_before += __popcll(tm);
+    ties_before += __popcll(eqm);
+  }
+}
+
+// S = smallest power of two with 64 * S >= nc (nc <= 64 * kSelKeysPerLane)
+__device__ __forceinline__ void wave_topk(const float* __restrict__ srow,
+                                          const int32_t* __restrict__ bt, int c0, int nc, int K,
+                                          int* sel_blk, int* sel_page) {
+  if (nc <= 64) wave_topk_s<1>(srow, bt, c0, nc, K, sel_blk, sel_page);
+  else if (nc <= 128) wave_topk_s<2>(srow, bt, c0, nc, K, sel_blk, sel_page);
+  else if (nc <= 256) wave_topk_s<4>(srow, bt, c0, nc, K, sel_blk, sel_page);
+  else if (nc <= 512) wave_topk_s<8>(srow, bt, c0, nc, K, sel_blk, sel_page);
+  else wave_topk_s<16>(srow, bt, c0, nc, K, sel_blk, sel_page);
+}
+
+// Block in output slot p of the selection for nb blocks: sinks [0, ns),
+// then the K ranked candidates (sel), then recent [nb - nr, nb); when the
+// candidates do not outnumber K every block is kept.
+__device__ __forceinline__ int selected_block(int p, int nb, bool ranked, int ns, int nr, int K,
+                                              const int* sel) {
+  if (!ranked) return p < nb ? p : -1;
+  if (p < ns) return p;
+  if (p < ns + K) return sel[p - ns];
+  if (p < ns + K + nr) return nb - nr + (p - ns - K);
+  return -1;
+}
+
+// ---------------------------------------------------------------------------
+// top-K select: one workgroup per (kv head, sequence).  Up to
+// 64 * kSelKeysPerLane candidates: wave_topk.  More: MSB-first radix select
+// (4 x 8 bits) of the K-th largest key over the workgroup, ties by ascending
+// index, then compaction of forced + chosen blocks in ascending order.
 // dynamic LDS: keys[mbps] (u32) + flags[mbps] (u8).  grid (Hkv, n)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_topk(Geometry geo, SeqBatch sb,
@@ -275,9 +361,18 @@ __global__ __launch_bounds__(256) void k_topk(Geometry geo, SeqBatch sb,
   const int c0 = geo.ns, c1 = nb - geo.nr, nc = c1 - c0;
   const bool ranked = ranked_select(geo, nc);
   const float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
+  int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
+  if (ranked && nc <= 64 * kSelKeysPerLane && geo.top_k <= kSelMaxK) {
+    // one wave selects; no workgroup barriers inside the selection
+    __shared__ int s_sel[kSelMaxK];
+    if (tid < 64) wave_topk(srow, nullptr, c0, nc, geo.top_k, s_sel, nullptr);
+    __syncthreads();
+    for (int p = tid; p < geo.nsel_max; p += 256)
+      out[p] = selected_block(p, nb, true, geo.ns, geo.nr, geo.top_k, s_sel);
+    return;
+  }
   uint32_t* keys = smem;
   uint8_t* flags = (uint8_t*)(smem + geo.mbps);
-  int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
   if (ranked)
     for (int i = tid; i < nc; i += 256) keys[i] = score_key(srow[c0 + i]);
   for (int j = tid; j < nb; j += 256)
@@ -338,6 +433,34 @@ __global__ __launch_bounds__(256) void k_topk(Geometry geo, SeqBatch sb,
 }
 
 // ---------------------------------------------------------------------------
+// wave-level helpers
+// ---------------------------------------------------------------------------
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two floats -> packed fp16 / bf16 (v_cvt_pk_*_f32, round to nearest even)
+template <int DT>
+__device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
+  if constexpr (DT == 0) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
+// {x[l], x[l ^ 16]} and {x[l], x[l ^ 32]} on the VALU (v_permlane*_swap)
+__device__ __forceinline__ float max_over_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_over_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// ---------------------------------------------------------------------------
 // gathered attention.  Workgroup = W waves = W consecutive selected slots of
 // one (sequence, kv head); each wave does one block with MFMA 16x16x32:
 //   S^T[token][head] = K[token][:] . Q[head][:]       (A = K rows, B = Q^T)
@@ -347,19 +470,23 @@ __global__ __launch_bounds__(256) void k_topk(Geometry geo, SeqBatch sb,
 //  - the QK tile rows are ordered so that the S accumulator of lane (head n,
 //    group g) holds tokens tok_of(g, e), e = 0..Tb/4-1, which is the
 //    A-operand layout PV needs (no shuffles).
-// The tiles are stored fragment-major, so each K/V load is 1 KiB contiguous.
+// The tiles are stored fragment-major, so each K/V load is 1 KiB contiguous,
+// and every K/V load of a wave is issued before the first wait (a scheduling
+// barrier keeps the compiler from interleaving them with the MFMAs).
 // bf16: P is split into hi + lo bf16 parts (two MFMAs) for ~16-bit P.
-// Every K/V load of a wave is issued before the first wait (a scheduling
-// barrier keeps the compiler from interleaving them with the MFMAs), so
-// each wave pays one memory round trip.
+// SEL: the selection is computed here from the block scores (wave 0 runs
+// wave_topk for the sequence and kv head, loading the candidates' block-table
+// entries alongside their scores, and shares blocks and pages through LDS)
+// instead of being read from idx; split 0 then writes the selected indices
+// to idx (if not null).
 // With more than one split, each workgroup writes an unnormalised partial
-// (o, m, l) for k_combine.
-// grid (nsplit, Hkv, n)
+// (o, m, l) for k_combine.  grid (nsplit, Hkv, n)
 // ---------------------------------------------------------------------------
-template <int DT, int TB, int G, int W>
-__global__ __launch_bounds__(64 * W) void k_attend(Geometry geo, SeqBatch sb,
+template <int DT, int TB, int G, int W, bool SEL>
+__global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
                                                    const uint16_t* __restrict__ q,
-                                                   const int32_t* __restrict__ idx,
+                                                   int32_t* __restrict__ idx,
+                                                   const float* __restrict__ scores,
                                                    float sl2, uint16_t* __restrict__ out,
                                                    float* __restrict__ partials) {
   constexpr int NT = TB / 16;   // QK token tiles
@@ -368,17 +495,13 @@ __global__ __launch_bounds__(64 * W) void k_attend(Geometry geo, SeqBatch sb,
   constexpr int NTH = 64 * W;
   __shared__ float s_m[W][16], s_l[W][16];
   __shared__ float s_o[W][G][kHeadDim];
+  __shared__ int s_sel[SEL ? kSelMaxK : 1];
+  __shared__ int s_selp[SEL ? kSelMaxK : 1];
   const int split = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int seq = sb.ids[bi];
   const int slot = split * W + wave;
-  int j = -1;
-  if (slot < geo.nsel_max) j = idx[((size_t)bi * geo.hkv + h) * geo.nsel_max + slot];
-  j = uniform(j);
-  const int len = uniform(geo.meta[seq]);
-  // -1 and indices past the sequence's last block contribute nothing
-  if (j >= geo.mbps || (int64_t)j * TB >= len) j = -1;
   u32x4 qf[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
@@ -387,8 +510,42 @@ __global__ __launch_bounds__(64 * W) void k_attend(Geometry geo, SeqBatch sb,
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = *(const u32x4*)(src + 32 * s);
   }
+  const int len = uniform(geo.meta[seq]);
+  int j = -1, page = -1;
+  if constexpr (SEL) {
+    const int nb = len > 0 ? (len + TB - 1) / TB : 0;
+    const int c0 = geo.ns, nc = nb - geo.nr - c0, K = geo.top_k;
+    const bool ranked = nc > K;
+    const int32_t* bt = block_table(geo, seq);
+    // sink / recent / every-block slots are known from the length alone
+    const bool picked = ranked && K > 0 && slot >= geo.ns && slot < geo.ns + K;
+    if (!picked) {
+      j = selected_block(slot, nb, ranked, geo.ns, geo.nr, K, s_sel);
+      if (j >= 0) page = uniform(bt[j]);
+    }
+    if (ranked && K > 0) {  // one wave selects, the workgroup shares the result
+      if (wave == 0) wave_topk(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, bt, c0, nc, K, s_sel, s_selp);
+      __syncthreads();
+      if (picked) {
+        j = s_sel[slot - geo.ns];
+        page = s_selp[slot - geo.ns];
+      }
+    }
+    if (idx != nullptr && split == 0 && wave == 0) {
+      int32_t* row = idx + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
+      for (int p = lane; p < geo.nsel_max; p += 64)
+        row[p] = selected_block(p, nb, ranked, geo.ns, geo.nr, K, s_sel);
+    }
+  } else {
+    if (slot < geo.nsel_max) j = idx[((size_t)bi * geo.hkv + h) * geo.nsel_max + slot];
+    j = uniform(j);
+    // -1 and indices past the sequence's last block contribute nothing
+    if (j >= geo.mbps || (int64_t)j * TB >= len) j = -1;
+    if (j >= 0) page = uniform(block_table(geo, seq)[j]);
+  }
+  j = uniform(j);
+  page = uniform(page);
   if (j >= 0) {
-    const int page = uniform(block_table(geo, seq)[j]);
     const int valid = min(TB, len - j * TB);
     const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
     // fragment-major tiles: fragment f of lane l is 16 B at (f * 64 + l) * 16
@@ -413,31 +570,30 @@ __global__ __launch_bounds__(64 * W) void k_attend(Geometry geo, SeqBatch sb,
 #pragma unroll
       for (int s = 0; s < 4; ++s) acc[t] = mfma16x16x32<DT>(kf[t][s], qf[s], acc[t]);
     }
-    // softmax over this block (log2 domain)
+    // softmax over this block (log2 domain); lanes of padded heads (n >= G)
+    // see S = 0 and produce rows of O that are never stored
     float pv[EPL];
-    float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = 4 * t + i;
-        float x = acc[t][i] * sl2;
-        if (tok_of(g, e) >= valid) x = -INFINITY;
-        pv[e] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      for (int i = 0; i < 4; ++i) pv[4 * t + i] = acc[t][i] * sl2;
+    if (valid < TB) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e)
+        if (tok_of(g, e) >= valid) pv[e] = -INFINITY;
+    }
+    float mx = pv[0];
+#pragma unroll
+    for (int e = 1; e < EPL; ++e) mx = fmaxf(mx, pv[e]);
+    mx = max_over_groups(mx);
     float ps = 0.f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-      const float p = (n < G) ? __builtin_amdgcn_exp2f(pv[e] - mx) : 0.f;
-      pv[e] = p;
-      ps += p;
+      pv[e] = __builtin_amdgcn_exp2f(pv[e] - mx);
+      ps += pv[e];
     }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
-    // P operand (A): lane (head n, group g), k-step s2, element 2*jj (+1)
+    ps = sum_over_groups(ps);
+    // P operand (A): lane (head n, group g), k-step s2, elements 2*jj, 2*jj+1
     // -> tokens tok_of(g, 8*s2 + 2*jj (+1)) = 32*s2 + 8*g + 2*jj (+1)
     u32x4 pf[KS2];
     u32x4 pl[KS2];
@@ -446,14 +602,10 @@ __global__ __launch_bounds__(64 * W) void k_attend(Geometry geo, SeqBatch sb,
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const float p0 = pv[8 * s2 + 2 * jj], p1 = pv[8 * s2 + 2 * jj + 1];
-        if constexpr (DT == 0) {
-          pf[s2][jj] = pack2<0>(p0, p1);
-          pl[s2][jj] = 0u;
-        } else {
-          const uint16_t h0 = f32_to_bf16_rne(p0), h1 = f32_to_bf16_rne(p1);
-          pf[s2][jj] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-          pl[s2][jj] = pack2<1>(p0 - to_f32<1>(h0), p1 - to_f32<1>(h1));
-        }
+        const uint32_t hi = cvt_pk<DT>(p0, p1);
+        pf[s2][jj] = hi;
+        if constexpr (DT == 1)
+          pl[s2][jj] = cvt_pk<1>(p0 - __uint_as_float(hi << 16), p1 - __uint_as_float(hi & 0xFFFF0000u));
       }
     // zero V of tokens past the end of a partial block (stale page data)
     if (valid < TB) {
@@ -467,7 +619,7 @@ __global__ __launch_bounds__(64 * W) void k_attend(Geometry geo, SeqBatch sb,
           for (int dt = 0; dt < 8; ++dt) vf[dt][s2][jj] &= m;
         }
     }
-    // O = P . V
+    // O = P . V; lane (dim n, group g) holds O rows (heads) 4g .. 4g+3
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -476,10 +628,16 @@ __global__ __launch_bounds__(64 * W) void k_attend(Geometry geo, SeqBatch sb,
         o = mfma16x16x32<DT>(pf[s2], vf[dt][s2], o);
         if constexpr (DT == 1) o = mfma16x16x32<DT>(pl[s2], vf[dt][s2], o);
       }
+      if constexpr (G >= 4) {
+        if (4 * g < G) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int head = 4 * g + i;
-        if (head < G) s_o[wave][head][16 * dt + n] = o[i];
+          for (int i = 0; i < 4; ++i) s_o[wave][4 * g + i][16 * dt + n] = o[i];
+        }
+      } else {
+        if (g == 0) {
+#pragma unroll
+          for (int i = 0; i < G; ++i) s_o[wave][i][16 * dt + n] = o[i];
+        }
       }
     }
     if (g == 0 && n < G) {
@@ -662,33 +820,35 @@ hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, fl
   return hipGetLastError();
 }
 
-template <int DT, int TB>
+template <int DT, int TB, bool SEL>
 static void attend_dispatch(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
-                            const int32_t* idx, float sl2, uint16_t* out, float* part,
+                            int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
                             hipStream_t s) {
   constexpr int W = kWaves;
   const dim3 blk(64 * W);
   switch (g.group) {
-    case 1: hipLaunchKernelGGL((k_attend<DT, TB, 1, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
-    case 2: hipLaunchKernelGGL((k_attend<DT, TB, 2, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
-    case 4: hipLaunchKernelGGL((k_attend<DT, TB, 4, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
-    case 8: hipLaunchKernelGGL((k_attend<DT, TB, 8, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
-    default: hipLaunchKernelGGL((k_attend<DT, TB, 16, W>), grid, blk, 0, s, g, b, q, idx, sl2, out, part); break;
+    case 1: hipLaunchKernelGGL((k_attend<DT, TB, 1, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
+    case 2: hipLaunchKernelGGL((k_attend<DT, TB, 2, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
+    case 4: hipLaunchKernelGGL((k_attend<DT, TB, 4, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
+    case 8: hipLaunchKernelGGL((k_attend<DT, TB, 8, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
+    default: hipLaunchKernelGGL((k_attend<DT, TB, 16, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
   }
 }
 
-hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
-                         float scale, void* out, float* partials, hipStream_t s) {
+template <bool SEL>
+static hipError_t attend_impl(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
+                              const float* scores, float scale, void* out, float* partials,
+                              hipStream_t s) {
   const float sl2 = scale * 1.4426950408889634f;
   dim3 grid(g.nsplit, g.hkv, b.n);
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* oo = (uint16_t*)out;
   if (g.dtype == 0) {
-    if (g.tb == 64) attend_dispatch<0, 64>(g, grid, b, qq, idx, sl2, oo, partials, s);
-    else attend_dispatch<0, 32>(g, grid, b, qq, idx, sl2, oo, partials, s);
+    if (g.tb == 64) attend_dispatch<0, 64, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s);
+    else attend_dispatch<0, 32, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s);
   } else {
-    if (g.tb == 64) attend_dispatch<1, 64>(g, grid, b, qq, idx, sl2, oo, partials, s);
-    else attend_dispatch<1, 32>(g, grid, b, qq, idx, sl2, oo, partials, s);
+    if (g.tb == 64) attend_dispatch<1, 64, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s);
+    else attend_dispatch<1, 32, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || g.nsplit == 1) return e;
@@ -697,6 +857,26 @@ hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q, co
   else
     hipLaunchKernelGGL(k_combine<1>, dim3(g.hq, b.n), dim3(128), 0, s, g, partials, oo);
   return hipGetLastError();
+}
+
+hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
+                         float scale, void* out, float* partials, hipStream_t s) {
+  return attend_impl<false>(g, b, q, const_cast<int32_t*>(idx), nullptr, scale, out, partials, s);
+}
+
+int fused_select_limit(int top_k) { return top_k <= kSelMaxK ? 64 * kSelKeysPerLane : 0; }
+
+hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                         int32_t* idx_out, int max_chunks, float scale, void* out,
+                         float* partials, hipStream_t s) {
+  if (max_chunks > 0) {
+    dim3 grid(max_chunks, g.hkv, b.n);
+    if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s);
+    else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return attend_impl<true>(g, b, q, idx_out, scores, scale, out, partials, s);
 }
 
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out, void* v_out,
