@@ -13,9 +13,10 @@ per layer-step.  Steps are replayed from a HIP graph (captured once) so the
 timing is the GPU's, not the Python launcher's; the eager (ctypes per call)
 figure is reported alongside.
 
-roofline: the attention launch (bsattn_attend on precomputed indices), timed
-with HIP events on the launch stream over 36-layer graphs; algorithmic bytes
-per launch = selected K+V bytes + q + out + indices.
+roofline: the gather + attention kernel (k_attend, via bsattn_attend on
+precomputed indices), timed with HIP start/stop events attached to each of
+its dispatches on the launch stream (the library's profiling hook);
+algorithmic bytes per launch = selected K+V bytes + q + out + indices.
 cpu_baseline: the CPU oracle (single thread) doing the same layer-step
 (score given summaries, select, attend) on layer 0's data.
 """
@@ -52,6 +53,9 @@ def parse():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one plain 256 MiB device copy (a known-traffic dispatch "
+                         "for scaling hardware byte counters)")
     return ap.parse_args()
 
 
@@ -82,6 +86,19 @@ def algorithmic_bytes(nsel):
     idx = B * HKV * nsel * 4
     summ = B * HKV * (T // TB) * D * 2
     return gather + qo + idx, summ
+
+
+def recorded_traffic():
+    """HBM bytes per k_attend launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (copy-calibrated); None when it is absent."""
+    path = os.path.join(ROOT, "profiles", "k_attend_b8_ctx32k_bf16_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1]), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
 
 
 def cpu_baseline(cache, q, seconds):
@@ -169,30 +186,44 @@ def main():
     us_per_layer = ms_per_step * 1e3 / L
     log(f"[bench] graph: {us_per_layer:.2f} us/layer-step")
 
-    # roofline: attention launches alone, on precomputed indices
+    if args.copy_calibration:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] calibration copy: 256 MiB read + 256 MiB written")
+        del src, dst
+
+    # roofline: the gather + attention kernel alone, on precomputed indices.
+    # Eager bsattn_attend calls with the library's profiling on: each kernel
+    # dispatch carries its own HIP start/stop events on the launch stream.
     idx = [cache.selectBlocks(q) for cache, q in layers]
     torch.cuda.synchronize()
     nsel = int((idx[0] >= 0).sum(dim=2).max().item())
-    ga = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(ga):
+    for (cache, q), ii in zip(layers, idx):  # warm
+        cache.attend(q, ii, scale)
+    torch.cuda.synchronize()
+    for cache, _ in layers:
+        cache.profile(True)
+    reps = max(5, args.steps)
+    for _ in range(reps):
         for (cache, q), ii in zip(layers, idx):
             cache.attend(q, ii, scale)
-    for _ in range(3):
-        ga.replay()
     torch.cuda.synchronize()
-    reps = max(5, args.steps)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(reps):
-        ga.replay()
-    ev1.record()
-    ev1.synchronize()
-    attend_us = ev0.elapsed_time(ev1) * 1e3 / (reps * L)
+    tot_ms, launches, comb_ms = 0.0, 0, 0.0
+    for cache, _ in layers:
+        ms, n = cache.profileRead(bsattn._lib.KERNEL_ATTEND)
+        cms, _ = cache.profileRead(bsattn._lib.KERNEL_COMBINE)
+        tot_ms, launches, comb_ms = tot_ms + ms, launches + n, comb_ms + cms
+        cache.profile(False)
+    attend_us = tot_ms * 1e3 / launches
+    combine_us = comb_ms * 1e3 / launches
     attn_bytes, summ_bytes = algorithmic_bytes(nsel)
     achieved = attn_bytes / (attend_us * 1e-6) / 1e9
     layer_bytes = attn_bytes + summ_bytes
-    log(f"[bench] attend launch: {attend_us:.2f} us, {achieved:.0f} GB/s "
-        f"({100 * achieved / HBM_PEAK_GBPS:.1f}% of peak)")
+    log(f"[bench] attend kernel: {attend_us:.2f} us, {achieved:.0f} GB/s "
+        f"({100 * achieved / HBM_PEAK_GBPS:.1f}% of peak); combine {combine_us:.2f} us")
 
     cpu = None
     if not args.no_cpu and args.cpu_seconds > 0:
@@ -203,6 +234,7 @@ def main():
                          f"median of {n} layer-steps, 1 thread"}
         log(f"[bench] cpu oracle: {cpu_us:.0f} us/layer-step")
 
+    traffic, traffic_src = recorded_traffic()
     result = {
         "metric": METRIC,
         "value": round(us_per_layer, 3),
@@ -221,9 +253,10 @@ def main():
                    "block_size": TB, "top_k": TOP_K, "sink_blocks": NS, "recent_blocks": NR,
                    "selected_blocks": nsel, "layers": L, "step": "score + top-K + attend"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "attend launch (bsattn_attend)", "launch_us": round(attend_us, 3),
-                     "bytes_per_launch": attn_bytes},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "kernel": "k_attend (gather + attention)", "launch_us": round(attend_us, 3),
+                     "bytes_per_launch": attn_bytes, "combine_us": round(combine_us, 3)},
         "layer_step_GBps": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "eager_us_per_layer_step": round(eager_ms * 1e3 / L, 3),
         "cpu_baseline": cpu,

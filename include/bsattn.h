@@ -167,6 +167,23 @@ int bsattn_export_quantized(const bsattn_cache* cache, const int32_t* seq_ids,
 int bsattn_export_summaries(const bsattn_cache* cache, int32_t seq, void* out,
                             void* stream);
 
+/* Opt-in kernel timing (no reference counterpart; the reference times with
+ * wall-clock Date deltas, Libraries/MLXLMCommon/Evaluate.swift:1773-1777).
+ * While enabled, every eager launch of the handle's kernels carries HIP
+ * start/stop events attached to its dispatch (launches captured into a
+ * graph are not timed).  bsattn_profile_read waits for the recorded events
+ * and returns the summed kernel time and launch count of one kernel kind
+ * since profiling was last enabled.  Enabling (or disabling) resets the sums. */
+#define BSATTN_KERNEL_SCORE 0   /* block scoring */
+#define BSATTN_KERNEL_TOPK 1    /* top-K selection (bsattn_select) */
+#define BSATTN_KERNEL_ATTEND 2  /* gather + attention (selection fused in bsattn_decode) */
+#define BSATTN_KERNEL_COMBINE 3 /* split combine */
+#define BSATTN_KERNEL_APPEND 4  /* token append */
+#define BSATTN_KERNEL_SUMMARY 5 /* block summary refresh */
+int bsattn_profile_enable(bsattn_cache* cache, int32_t enable);
+int bsattn_profile_read(bsattn_cache* cache, int32_t kernel, double* total_ms,
+                        int64_t* launches);
+
 #ifdef __cplusplus
 }
 #endif

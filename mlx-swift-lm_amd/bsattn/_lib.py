@@ -40,7 +40,11 @@ EXPORTS = (
     "bsattn_export",
     "bsattn_export_quantized",
     "bsattn_export_summaries",
+    "bsattn_profile_enable",
+    "bsattn_profile_read",
 )
+
+KERNEL_SCORE, KERNEL_TOPK, KERNEL_ATTEND, KERNEL_COMBINE, KERNEL_APPEND, KERNEL_SUMMARY = range(6)
 
 
 class BsattnError(RuntimeError):
@@ -113,6 +117,9 @@ def lib() -> ctypes.CDLL:
         "bsattn_export": (ctypes.c_int, [P, PI32, i32, P, P, P]),
         "bsattn_export_quantized": (ctypes.c_int, [P, PI32, i32, P, P, P, P, P, P, P]),
         "bsattn_export_summaries": (ctypes.c_int, [P, i32, P, P]),
+        "bsattn_profile_enable": (ctypes.c_int, [P, i32]),
+        "bsattn_profile_read": (ctypes.c_int, [P, i32, ctypes.POINTER(ctypes.c_double),
+                                               ctypes.POINTER(ctypes.c_int64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -212,6 +212,17 @@ class BlockSparseKVCache:
                                   ctypes.c_float(scale), _ptr(out), idx_p, _stream(self.device)))
         return out
 
+    # -- kernel timing -------------------------------------------------------
+    def profile(self, enable: bool = True) -> None:
+        """Start (or stop) timing this cache's eager kernel launches; resets sums."""
+        check(lib().bsattn_profile_enable(self._h, 1 if enable else 0))
+
+    def profileRead(self, kernel: int):
+        """(total milliseconds, launches) of one kernel kind (bsattn KERNEL_*)."""
+        ms, n = ctypes.c_double(), ctypes.c_int64()
+        check(lib().bsattn_profile_read(self._h, kernel, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
     # -- KVCache protocol: state, trim, mask, copy -----------------------------
     @property
     def state(self) -> List[torch.Tensor]:

@@ -57,6 +57,12 @@ struct bsattn_cache {
   std::vector<int32_t> len;
   std::vector<std::vector<int32_t>> pages;
   std::vector<int32_t> free_pages;  // stack; back() is handed out next
+  // opt-in per-kernel timing (bsattn_profile_*)
+  bool profiling = false;
+  std::vector<hipEvent_t> event_pool;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending[kProfKinds];
+  double prof_ms[kProfKinds] = {};
+  int64_t prof_count[kProfKinds] = {};
 };
 
 namespace {
@@ -170,6 +176,70 @@ int reserve_pages(bsattn_cache* c, const std::vector<int32_t>& seqs, int L,
   return BSATTN_OK;
 }
 
+// Profiling slots for one C-ABI call: null unless profiling is on and the
+// stream is not being captured into a graph.
+Timing* prof_slots(bsattn_cache* c, hipStream_t s, Timing* tm) {
+  if (!c->profiling) return nullptr;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
+  for (int k = 0; k < kProfKinds; ++k) {
+    hipEvent_t ev[2];
+    for (auto& e : ev) {
+      if (!c->event_pool.empty()) {
+        e = c->event_pool.back();
+        c->event_pool.pop_back();
+      } else if (hipEventCreate(&e) != hipSuccess) {
+        e = nullptr;
+      }
+    }
+    tm[k].start = ev[0];
+    tm[k].stop = ev[1];
+    tm[k].used = false;
+  }
+  return tm;
+}
+
+void prof_collect(bsattn_cache* c, Timing* tm) {
+  if (!tm) return;
+  for (int k = 0; k < kProfKinds; ++k) {
+    if (tm[k].used && tm[k].start && tm[k].stop) {
+      c->pending[k].emplace_back(tm[k].start, tm[k].stop);
+    } else {
+      if (tm[k].start) c->event_pool.push_back(tm[k].start);
+      if (tm[k].stop) c->event_pool.push_back(tm[k].stop);
+    }
+  }
+}
+
+int prof_drain(bsattn_cache* c) {
+  for (int k = 0; k < kProfKinds; ++k) {
+    for (auto& pr : c->pending[k]) {
+      float ms = 0.f;
+      hipError_t e = hipEventSynchronize(pr.second);
+      if (e == hipSuccess) e = hipEventElapsedTime(&ms, pr.first, pr.second);
+      if (e != hipSuccess) return hip_fail(e, "profile events");
+      c->prof_ms[k] += ms;
+      c->prof_count[k] += 1;
+      c->event_pool.push_back(pr.first);
+      c->event_pool.push_back(pr.second);
+    }
+    c->pending[k].clear();
+  }
+  return BSATTN_OK;
+}
+
+void prof_release(bsattn_cache* c) {
+  for (int k = 0; k < kProfKinds; ++k) {
+    for (auto& pr : c->pending[k]) {
+      c->event_pool.push_back(pr.first);
+      c->event_pool.push_back(pr.second);
+    }
+    c->pending[k].clear();
+  }
+  for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
+  c->event_pool.clear();
+}
+
 }  // namespace
 
 extern "C" {
@@ -250,6 +320,7 @@ int bsattn_cache_destroy(bsattn_cache* c) {
   if (!c) return BSATTN_OK;
   DeviceGuard dg(c->d.device);
   (void)hipDeviceSynchronize();
+  prof_release(c);
   (void)hipFree(c->geo.pool);
   (void)hipFree(c->geo.summ);
   (void)hipFree(c->geo.meta);
@@ -315,8 +386,12 @@ int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* 
     sb.n = ab.n;
     const uint16_t* kk = (const uint16_t*)k + (size_t)i0 * row_elems;
     const uint16_t* vv = (const uint16_t*)v + (size_t)i0 * row_elems;
-    HIP_TRY(launch_append(c->geo, ab, kk, vv, s), "append launch");
-    if (max_count > 0) HIP_TRY(launch_summary(c->geo, sb, max_count, s), "summary launch");
+    Timing tm[kProfKinds];
+    Timing* prof = prof_slots(c, s, tm);
+    hipError_t e = launch_append(c->geo, ab, kk, vv, s, prof);
+    if (e == hipSuccess && max_count > 0) e = launch_summary(c->geo, sb, max_count, s, prof);
+    prof_collect(c, prof);
+    if (e != hipSuccess) return hip_fail(e, "append launch");
   }
   for (int s_ : seqs) c->len[s_] += n_tokens;
   return BSATTN_OK;
@@ -343,7 +418,11 @@ static int do_select(bsattn_cache* c, const void* q, const std::vector<int32_t>&
     const uint16_t* qq = (const uint16_t*)q + (size_t)i0 * c->geo.hq * kHeadDim;
     float* sc = c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps;
     int32_t* io = idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max;
-    HIP_TRY(launch_select(c->geo, b, qq, sc, io, max_chunks, s), "select launch");
+    Timing tm[kProfKinds];
+    Timing* prof = prof_slots(c, s, tm);
+    hipError_t e = launch_select(c->geo, b, qq, sc, io, max_chunks, s, prof);
+    prof_collect(c, prof);
+    if (e != hipSuccess) return hip_fail(e, "select launch");
   }
   return BSATTN_OK;
 }
@@ -357,11 +436,15 @@ static int do_attend(bsattn_cache* c, const void* q, const std::vector<int32_t>&
     b.n = std::min(kMaxBatch, n - i0);
     for (int i = 0; i < b.n; ++i) b.ids[i] = seqs[i0 + i];
     const size_t qoff = (size_t)i0 * c->geo.hq * kHeadDim * elem;
-    HIP_TRY(launch_attend(c->geo, b, (const char*)q + qoff,
-                          idx + (size_t)i0 * c->geo.hkv * c->geo.nsel_max, scale,
-                          (char*)out + qoff,
-                          c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2), s),
-            "attend launch");
+    Timing tm[kProfKinds];
+    Timing* prof = prof_slots(c, s, tm);
+    hipError_t e = launch_attend(c->geo, b, (const char*)q + qoff,
+                                 idx + (size_t)i0 * c->geo.hkv * c->geo.nsel_max, scale,
+                                 (char*)out + qoff,
+                                 c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2),
+                                 s, prof);
+    prof_collect(c, prof);
+    if (e != hipSuccess) return hip_fail(e, "attend launch");
   }
   return BSATTN_OK;
 }
@@ -415,12 +498,16 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
       max_chunks = std::max(max_chunks, select_chunks(c->geo, c->len[b.ids[i]]));
     }
     const size_t qoff = (size_t)i0 * c->geo.hq * kHeadDim * 2;
-    HIP_TRY(launch_decode(c->geo, b, (const char*)q + qoff,
-                          c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps,
-                          idx_out ? idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max : nullptr,
-                          max_chunks, scale, (char*)out + qoff,
-                          c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2), s),
-            "decode launch");
+    Timing tm[kProfKinds];
+    Timing* prof = prof_slots(c, s, tm);
+    hipError_t e = launch_decode(c->geo, b, (const char*)q + qoff,
+                                 c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps,
+                                 idx_out ? idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max : nullptr,
+                                 max_chunks, scale, (char*)out + qoff,
+                                 c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2),
+                                 s, prof);
+    prof_collect(c, prof);
+    if (e != hipSuccess) return hip_fail(e, "decode launch");
   }
   return BSATTN_OK;
 }
@@ -518,6 +605,30 @@ int bsattn_export_summaries(const bsattn_cache* c, int32_t seq, void* out, void*
   if (nfull == 0) return BSATTN_OK;
   DeviceGuard dg(c->d.device);
   HIP_TRY(launch_export_summaries(c->geo, seq, nfull, out, (hipStream_t)stream), "export summaries launch");
+  return BSATTN_OK;
+}
+
+int bsattn_profile_enable(bsattn_cache* c, int32_t enable) {
+  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  DeviceGuard dg(c->d.device);
+  int rc = prof_drain(c);
+  if (rc) return rc;
+  for (int k = 0; k < kProfKinds; ++k) {
+    c->prof_ms[k] = 0.0;
+    c->prof_count[k] = 0;
+  }
+  c->profiling = enable != 0;
+  return BSATTN_OK;
+}
+
+int bsattn_profile_read(bsattn_cache* c, int32_t kernel, double* total_ms, int64_t* launches) {
+  if (!c || !total_ms || !launches) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (kernel < 0 || kernel >= kProfKinds) return fail(BSATTN_ERR_INVALID, "unknown kernel id %d", kernel);
+  DeviceGuard dg(c->d.device);
+  int rc = prof_drain(c);
+  if (rc) return rc;
+  *total_ms = c->prof_ms[kernel];
+  *launches = c->prof_count[kernel];
   return BSATTN_OK;
 }
 

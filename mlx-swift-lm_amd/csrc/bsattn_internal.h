@@ -59,30 +59,42 @@ struct PatchBatch {
   int32_t val[kMaxPatch];
 };
 
+// Opt-in per-kernel profiling: a launcher given a Timing array records the
+// start/stop events of slot `kind` around that kernel's dispatch (when the
+// slot's events are set) and marks the slot used.
+enum ProfKind {
+  kProfScore = 0, kProfTopk = 1, kProfAttend = 2, kProfCombine = 3, kProfAppend = 4,
+  kProfSummary = 5, kProfKinds = 6
+};
+struct Timing {
+  hipEvent_t start = nullptr, stop = nullptr;
+  bool used = false;
+};
+
 // launchers (bsattn_kernels.hip); return hipError_t of the launch
 hipError_t launch_patch(const Geometry& g, const PatchBatch& pb, hipStream_t s);
 hipError_t launch_append(const Geometry& g, const AppendBatch& ab, const void* k,
-                         const void* v, hipStream_t s);
+                         const void* v, hipStream_t s, Timing* prof);
 hipError_t launch_append_quantized(const Geometry& g, const AppendBatch& ab,
                                    const uint32_t* kw, const void* ks, const void* kb,
                                    const uint32_t* vw, const void* vs, const void* vb,
                                    hipStream_t s);
 hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
-                          hipStream_t s);
+                          hipStream_t s, Timing* prof);
 int select_chunks(const Geometry& g, int len);
 // scoring workgroups per (sequence, kv head) for `len` tokens (0: no ranking)
 hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                         int32_t* idx, int max_chunks, hipStream_t s);
+                         int32_t* idx, int max_chunks, hipStream_t s, Timing* prof);
 hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q,
                          const int32_t* idx, float scale, void* out, float* partials,
-                         hipStream_t s);
+                         hipStream_t s, Timing* prof);
 // decode = scoring + attention with the top-K selection done inside the
 // attention kernel; valid while every sequence has at most
 // fused_select_limit(top_k) candidate blocks.  idx_out may be null.
 int fused_select_limit(int top_k);
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                          int32_t* idx_out, int max_chunks, float scale, void* out,
-                         float* partials, hipStream_t s);
+                         float* partials, hipStream_t s, Timing* prof);
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out,
                          void* v_out, hipStream_t s);
 hipError_t launch_export_quantized(const Geometry& g, const SeqBatch& b, int T,

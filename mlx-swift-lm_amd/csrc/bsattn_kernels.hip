@@ -14,6 +14,7 @@
 // the compiler cannot contract or reorder them; the order is the one the
 // oracle states (sequential token fold; 16 chunks of 8 dims, then an xor
 // butterfly 1, 2, 4, 8; max over the GQA group scanning upward).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -283,19 +284,32 @@ __device__ __forceinline__ void wave_topk_s(const float* __restrict__ srow,
     key[k] = real ? score_key(srow[c0 + i]) : 0u;
     page[k] = (real && sel_page) ? bt[c0 + i] : 0;
   }
+  // all compares of a step are issued before the first popcount: each
+  // scalar read of a VALU-written mask waits for the VALU pipeline, and
+  // grouping them pays that wait once per step instead of once per slot
   uint32_t tau = 0u;
 #pragma unroll 1
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = tau | (1u << bit);
+    uint64_t m[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k) m[k] = __ballot(key[k] >= cand);
+    __builtin_amdgcn_sched_barrier(0);
     int cnt = 0;
 #pragma unroll
-    for (int k = 0; k < S; ++k) cnt += __popcll(__ballot(key[k] >= cand));
+    for (int k = 0; k < S; ++k) cnt += __popcll(m[k]);
     if (cnt >= K) tau = cand;
   }
   // keys > tau are taken; of the keys == tau, the krem lowest indices
   int gt_total = 0;
+  {
+    uint64_t m[S];
 #pragma unroll
-  for (int k = 0; k < S; ++k) gt_total += __popcll(__ballot(key[k] > tau));
+    for (int k = 0; k < S; ++k) m[k] = __ballot(key[k] > tau);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < S; ++k) gt_total += __popcll(m[k]);
+  }
   const int krem = K - gt_total;
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   int sel_before = 0, ties_before = 0;
@@ -759,16 +773,30 @@ __global__ __launch_bounds__(128) void k_export_summaries(Geometry geo, int seq,
 // ===========================================================================
 // launchers
 // ===========================================================================
+// Launches `kernel`; with a profiling slot for its kind, the dispatch itself
+// records the slot's start/stop events (hipExtLaunchKernel).
+template <typename F, typename... Args>
+static void launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Timing* prof,
+                   int kind, Args... args) {
+  if (prof && prof[kind].start) {
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, prof[kind].start, prof[kind].stop,
+                          0u, args...);
+    prof[kind].used = true;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+  }
+}
+
 hipError_t launch_patch(const Geometry& g, const PatchBatch& pb, hipStream_t s) {
   hipLaunchKernelGGL(k_patch, dim3(1), dim3(256), 0, s, g.meta, pb);
   return hipGetLastError();
 }
 
 hipError_t launch_append(const Geometry& g, const AppendBatch& ab, const void* k, const void* v,
-                         hipStream_t s) {
+                         hipStream_t s, Timing* prof) {
   dim3 grid((ab.L + 15) / 16, g.hkv, ab.n);
-  hipLaunchKernelGGL(k_append, grid, dim3(256), 0, s, g, ab, (const uint16_t*)k,
-                     (const uint16_t*)v);
+  launch(k_append, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, (const uint16_t*)k,
+         (const uint16_t*)v);
   return hipGetLastError();
 }
 
@@ -779,24 +807,25 @@ hipError_t launch_append_quantized(const Geometry&, const AppendBatch&, const ui
 }
 
 hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
-                          hipStream_t s) {
+                          hipStream_t s, Timing* prof) {
   dim3 grid(max_count, g.hkv, sb.n);
   if (g.dtype == 0)
-    hipLaunchKernelGGL(k_summary<0>, grid, dim3(128), 0, s, g, sb);
+    launch(k_summary<0>, grid, dim3(128), 0, s, prof, kProfSummary, g, sb);
   else
-    hipLaunchKernelGGL(k_summary<1>, grid, dim3(128), 0, s, g, sb);
+    launch(k_summary<1>, grid, dim3(128), 0, s, prof, kProfSummary, g, sb);
   return hipGetLastError();
 }
 
 template <int DT>
 static void score_dispatch(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
-                           float* sc, hipStream_t s) {
+                           float* sc, hipStream_t s, Timing* prof) {
+  const dim3 blk(256);
   switch (g.group) {
-    case 1: hipLaunchKernelGGL((k_score<DT, 1>), grid, dim3(256), 0, s, g, b, q, sc); break;
-    case 2: hipLaunchKernelGGL((k_score<DT, 2>), grid, dim3(256), 0, s, g, b, q, sc); break;
-    case 4: hipLaunchKernelGGL((k_score<DT, 4>), grid, dim3(256), 0, s, g, b, q, sc); break;
-    case 8: hipLaunchKernelGGL((k_score<DT, 8>), grid, dim3(256), 0, s, g, b, q, sc); break;
-    default: hipLaunchKernelGGL((k_score<DT, 16>), grid, dim3(256), 0, s, g, b, q, sc); break;
+    case 1: launch(k_score<DT, 1>, grid, blk, 0, s, prof, kProfScore, g, b, q, sc); break;
+    case 2: launch(k_score<DT, 2>, grid, blk, 0, s, prof, kProfScore, g, b, q, sc); break;
+    case 4: launch(k_score<DT, 4>, grid, blk, 0, s, prof, kProfScore, g, b, q, sc); break;
+    case 8: launch(k_score<DT, 8>, grid, blk, 0, s, prof, kProfScore, g, b, q, sc); break;
+    default: launch(k_score<DT, 16>, grid, blk, 0, s, prof, kProfScore, g, b, q, sc); break;
   }
 }
 
@@ -807,76 +836,80 @@ int select_chunks(const Geometry& g, int len) {
 }
 
 hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                         int32_t* idx, int max_chunks, hipStream_t s) {
+                         int32_t* idx, int max_chunks, hipStream_t s, Timing* prof) {
   if (max_chunks > 0) {
     dim3 grid(max_chunks, g.hkv, b.n);
-    if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s);
-    else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s);
+    if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s, prof);
+    else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s, prof);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   const size_t lds = (size_t)g.mbps * 5;
-  hipLaunchKernelGGL(k_topk, dim3(g.hkv, b.n), dim3(256), lds, s, g, b, scores, idx);
+  launch(k_topk, dim3(g.hkv, b.n), dim3(256), lds, s, prof, kProfTopk, g, b, (const float*)scores,
+         idx);
   return hipGetLastError();
 }
 
 template <int DT, int TB, bool SEL>
 static void attend_dispatch(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
                             int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
-                            hipStream_t s) {
+                            hipStream_t s, Timing* prof) {
   constexpr int W = kWaves;
   const dim3 blk(64 * W);
+  const int kd = kProfAttend;
   switch (g.group) {
-    case 1: hipLaunchKernelGGL((k_attend<DT, TB, 1, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
-    case 2: hipLaunchKernelGGL((k_attend<DT, TB, 2, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
-    case 4: hipLaunchKernelGGL((k_attend<DT, TB, 4, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
-    case 8: hipLaunchKernelGGL((k_attend<DT, TB, 8, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
-    default: hipLaunchKernelGGL((k_attend<DT, TB, 16, W, SEL>), grid, blk, 0, s, g, b, q, idx, sc, sl2, out, part); break;
+    case 1: launch(k_attend<DT, TB, 1, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    case 2: launch(k_attend<DT, TB, 2, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    case 4: launch(k_attend<DT, TB, 4, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    case 8: launch(k_attend<DT, TB, 8, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    default: launch(k_attend<DT, TB, 16, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
   }
 }
 
 template <bool SEL>
 static hipError_t attend_impl(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
                               const float* scores, float scale, void* out, float* partials,
-                              hipStream_t s) {
+                              hipStream_t s, Timing* prof) {
   const float sl2 = scale * 1.4426950408889634f;
   dim3 grid(g.nsplit, g.hkv, b.n);
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* oo = (uint16_t*)out;
   if (g.dtype == 0) {
-    if (g.tb == 64) attend_dispatch<0, 64, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s);
-    else attend_dispatch<0, 32, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s);
+    if (g.tb == 64) attend_dispatch<0, 64, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+    else attend_dispatch<0, 32, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
   } else {
-    if (g.tb == 64) attend_dispatch<1, 64, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s);
-    else attend_dispatch<1, 32, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s);
+    if (g.tb == 64) attend_dispatch<1, 64, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+    else attend_dispatch<1, 32, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || g.nsplit == 1) return e;
+  const float* pc = partials;
   if (g.dtype == 0)
-    hipLaunchKernelGGL(k_combine<0>, dim3(g.hq, b.n), dim3(128), 0, s, g, partials, oo);
+    launch(k_combine<0>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, pc, oo);
   else
-    hipLaunchKernelGGL(k_combine<1>, dim3(g.hq, b.n), dim3(128), 0, s, g, partials, oo);
+    launch(k_combine<1>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, pc, oo);
   return hipGetLastError();
 }
 
 hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
-                         float scale, void* out, float* partials, hipStream_t s) {
-  return attend_impl<false>(g, b, q, const_cast<int32_t*>(idx), nullptr, scale, out, partials, s);
+                         float scale, void* out, float* partials, hipStream_t s, Timing* prof) {
+  return attend_impl<false>(g, b, q, const_cast<int32_t*>(idx), nullptr, scale, out, partials, s,
+                            prof);
 }
 
 int fused_select_limit(int top_k) { return top_k <= kSelMaxK ? 64 * kSelKeysPerLane : 0; }
 
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                          int32_t* idx_out, int max_chunks, float scale, void* out,
-                         float* partials, hipStream_t s) {
+                         float* partials, hipStream_t s, Timing* prof) {
   if (max_chunks > 0) {
     dim3 grid(max_chunks, g.hkv, b.n);
-    if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s);
-    else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s);
+    if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s, prof);
+    else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s, prof);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  return attend_impl<true>(g, b, q, idx_out, scores, scale, out, partials, s);
+  return attend_impl<true>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
 }
 
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out, void* v_out,

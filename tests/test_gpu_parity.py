@@ -286,3 +286,25 @@ def test_graph_replay_matches_eager(gpu):
         other = cache.decode(q, w.scale)  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
+
+
+def test_profiling_counts_launches(gpu):
+    """bsattn_profile_*: eager launches are timed per kernel kind."""
+    import torch
+    from bsattn import _lib
+    w = make_workload(3700, B=2, Hq=32, Hkv=8, T=4000, Tb=64, dtype="bf16", top_k=8)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    q = to_dev(w.q[:, :, None, :], "bf16", gpu)
+    cache.profile(True)
+    for _ in range(3):
+        idx = cache.selectBlocks(q)
+        cache.attend(q, idx, w.scale)
+    cache.decode(q, w.scale)
+    torch.cuda.synchronize()
+    ms, n = cache.profileRead(_lib.KERNEL_ATTEND)
+    assert n == 4 and ms > 0
+    assert cache.profileRead(_lib.KERNEL_TOPK)[1] == 3
+    assert cache.profileRead(_lib.KERNEL_SCORE)[1] == 4
+    cache.profile(False)
+    assert cache.profileRead(_lib.KERNEL_ATTEND) == (0.0, 0)
