@@ -145,9 +145,70 @@ class BlockSparseKVCache:
 
     def update(self, keys: torch.Tensor, values: torch.Tensor):
         """KVCache.update (KVCache.swift:328-371): append, then return all
-        cached keys/values [B, Hkv, offset, D]."""
+        cached keys/values [B, Hkv, offset, D].  A quantized cache traps like
+        QuantizedKVCache.update (KVCache.swift:891-896): use updateQuantized."""
+        if self.bits:
+            raise RuntimeError("`update` was called on a quantized BlockSparseKVCache. "
+                               "Use `updateQuantized` instead.")
         self.append(keys, values)
         return self.export(list(range(keys.shape[0])))
+
+    # -- quantized caches (QuantizedKVCache, KVCache.swift:728-988) -----------
+    def _require_quantized(self) -> None:
+        if not self.bits:
+            raise RuntimeError("not a quantized cache (bits 0)")
+
+    def quantizedShapes(self, B: int, L: int):
+        """Shapes of (weights, scales, biases) in the MLX layout for B
+        sequences of L tokens: [B, Hkv, L, D*bits/32] uint32 (stored as
+        int32) and [B, Hkv, L, D/groupSize] fp16."""
+        d = self.desc
+        return ((B, d.num_kv_heads, L, d.head_dim * d.kv_bits // 32),
+                (B, d.num_kv_heads, L, d.head_dim // d.group_size))
+
+    def appendQuantized(self, keys, values, seq_ids: Optional[Sequence[int]] = None) -> None:
+        """Appends already-quantized tokens: keys / values are (weights,
+        scales, biases) tuples in the MLX layout (quantizedShapes)."""
+        self._require_quantized()
+        (kw, ks, kb), (vw, vs, vb) = keys, values
+        B, L = kw.shape[0], kw.shape[2]
+        wshape, sshape = self.quantizedShapes(B, L)
+        for name, t, shape, dt in (("keys.weights", kw, wshape, torch.int32), ("keys.scales", ks, sshape, torch.float16),
+                                   ("keys.biases", kb, sshape, torch.float16), ("values.weights", vw, wshape, torch.int32),
+                                   ("values.scales", vs, sshape, torch.float16), ("values.biases", vb, sshape, torch.float16)):
+            if tuple(t.shape) != shape or t.dtype != dt or t.device != self.device or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous {dt} tensor {shape} on {self.device}, "
+                                 f"got {t.dtype} {tuple(t.shape)}")
+        check(lib().bsattn_append_quantized(self._h, _ptr(kw), _ptr(ks), _ptr(kb), _ptr(vw), _ptr(vs),
+                                            _ptr(vb), i32_array(seq_ids), B, L, _stream(self.device)))
+
+    def exportQuantized(self, seq_ids: Sequence[int]):
+        """((kw, ks, kb), (vw, vs, vb)) of the listed sequences, MLX layout."""
+        self._require_quantized()
+        B = len(seq_ids)
+        T = self.seqLen(seq_ids[0])
+        wshape, sshape = self.quantizedShapes(B, T)
+        kw, ks, kb, vw, vs, vb = (
+            torch.empty(shape, dtype=dt, device=self.device)
+            for shape, dt in [(wshape, torch.int32), (sshape, torch.float16), (sshape, torch.float16)] * 2)
+        if T > 0:
+            check(lib().bsattn_export_quantized(self._h, i32_array(seq_ids), B, _ptr(kw), _ptr(ks), _ptr(kb),
+                                                _ptr(vw), _ptr(vs), _ptr(vb), _stream(self.device)))
+        return (kw, ks, kb), (vw, vs, vb)
+
+    def updateQuantized(self, keys: torch.Tensor, values: torch.Tensor):
+        """QuantizedKVCache.updateQuantized (KVCache.swift:816-889): quantize
+        and append fp16 keys / values [B, Hkv, L, D], then return the
+        quantized tuples of all cached tokens."""
+        self._require_quantized()
+        self.append(keys, values)
+        return self.exportQuantized(list(range(keys.shape[0])))
+
+    def getQuantizedState(self):
+        """QuantizedKVCache.getQuantizedState (KVCache.swift:797-806)."""
+        self._require_quantized()
+        n = self.batchSize()
+        return self.exportQuantized(list(range(n))) if n else None
 
     def export(self, seq_ids: Sequence[int]):
         B = len(seq_ids)
@@ -226,18 +287,30 @@ class BlockSparseKVCache:
     # -- KVCache protocol: state, trim, mask, copy -----------------------------
     @property
     def state(self) -> List[torch.Tensor]:
+        """[keys, values] (KVCacheSimple, KVCache.swift:373-384) or, for a
+        quantized cache, [kw, ks, kb, vw, vs, vb] (QuantizedKVCache,
+        KVCache.swift:906-925)."""
         n = self.batchSize()
         if n == 0:
             return []
+        if self.bits:
+            (kw, ks, kb), (vw, vs, vb) = self.exportQuantized(list(range(n)))
+            return [kw, ks, kb, vw, vs, vb]
         return list(self.export(list(range(n))))
 
     @state.setter
     def state(self, arrays: List[torch.Tensor]) -> None:
-        if len(arrays) != 2:
-            raise ValueError("BlockSparseKVCache state must have exactly 2 arrays (keys, values)")
-        k, v = arrays
+        want = 6 if self.bits else 2
+        if len(arrays) != want:
+            raise ValueError(f"BlockSparseKVCache state must have exactly {want} arrays")
         self.reset(list(range(self.desc.max_seqs)))
-        if k.shape[2] > 0:
+        if arrays[0].shape[2] == 0:
+            return
+        if self.bits:
+            a = [t.contiguous() for t in arrays]
+            self.appendQuantized((a[0], a[1], a[2]), (a[3], a[4], a[5]))
+        else:
+            k, v = arrays
             self.append(k.contiguous(), v.contiguous())
 
     @property

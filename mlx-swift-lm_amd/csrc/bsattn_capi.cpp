@@ -94,7 +94,14 @@ int validate_desc(const bsattn_desc& d) {
     return fail(BSATTN_ERR_INVALID, "block_size %d unsupported (32 or 64)", d.block_size);
   if (d.dtype != BSATTN_F16 && d.dtype != BSATTN_BF16)
     return fail(BSATTN_ERR_INVALID, "dtype %d unknown", d.dtype);
-  if (d.kv_bits != 0) return fail(BSATTN_ERR_INVALID, "kv_bits %d: quantized caches not available in this build", d.kv_bits);
+  if (d.kv_bits != 0) {
+    if (d.kv_bits != 4 && d.kv_bits != 8)
+      return fail(BSATTN_ERR_INVALID, "kv_bits %d unsupported (0, 4 or 8)", d.kv_bits);
+    if (d.dtype != BSATTN_F16)
+      return fail(BSATTN_ERR_INVALID, "quantized caches take fp16 queries, keys and values");
+    if (d.group_size != 64)
+      return fail(BSATTN_ERR_INVALID, "group_size %d unsupported (64)", d.group_size);
+  }
   if (d.top_k < 0 || d.sink_blocks < 0) return fail(BSATTN_ERR_INVALID, "top_k and sink_blocks must be >= 0");
   if (d.recent_blocks < 1) return fail(BSATTN_ERR_INVALID, "recent_blocks must be >= 1 (the partial block is never scored)");
   if (d.max_blocks_per_seq < 1 || d.max_blocks_per_seq > 12288)
@@ -275,11 +282,12 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   g.nsplit = (g.nsel_max + kWaves - 1) / kWaves;
   g.mbps = d.max_blocks_per_seq;
   g.bt_off = d.max_seqs;
-  // slab: K tile [Tb][D] then V tile [D][Tb], 16-bit elements
+  // slab: K tile then V tile (16-bit elements, or b-bit codes), then for
+  // quantized caches 16 B of scales / biases per token
   g.k_off = 0;
-  g.v_off = (int64_t)d.block_size * kHeadDim * 2;
-  g.slab_bytes = 2 * g.v_off;
-  g.ks_off = g.kb_off = g.vs_off = g.vb_off = 0;
+  g.v_off = (int64_t)d.block_size * kHeadDim * (d.kv_bits ? d.kv_bits : 16) / 8;
+  g.sb_off = 2 * g.v_off;
+  g.slab_bytes = g.sb_off + (d.kv_bits ? (int64_t)d.block_size * 16 : 0);
   c->pool_bytes = (size_t)c->num_pages * g.hkv * g.slab_bytes;
   c->summ_bytes = (size_t)d.max_seqs * g.hkv * g.mbps * kHeadDim * 2;
   c->meta_words = (size_t)d.max_seqs * (1 + d.max_blocks_per_seq);
@@ -348,16 +356,17 @@ int bsattn_seq_len(const bsattn_cache* c, int32_t seq, int32_t* out_len) {
   return BSATTN_OK;
 }
 
-int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* seq_ids,
-                  int32_t n_seqs, int32_t n_tokens, void* stream) {
-  if (!c || !k || !v) return fail(BSATTN_ERR_INVALID, "null argument");
-  if (c->d.kv_bits != 0) return fail(BSATTN_ERR_INVALID, "quantize-on-append is not available; use bsattn_append_quantized");
+// Shared append flow: reserve pages, patch lengths / block tables, then per
+// batch of sequences launch `kernels(batch, first row)` (token writes) and the
+// summaries of the blocks that become full.
+extern "C++" template <typename F>
+int append_impl(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
+                       hipStream_t s, F kernels) {
   if (n_tokens < 1) return fail(BSATTN_ERR_INVALID, "n_tokens must be >= 1 (got %d)", n_tokens);
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
-  hipStream_t s = (hipStream_t)stream;
   std::vector<std::pair<int32_t, int32_t>> patches;
   rc = reserve_pages(c, seqs, n_tokens, patches);
   if (rc) return rc;
@@ -365,7 +374,6 @@ int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* 
   for (int s_ : seqs) patches.emplace_back(s_, c->len[s_] + n_tokens);
   rc = flush_patches(c, patches, s);
   if (rc) return rc;
-  const size_t row_elems = (size_t)c->geo.hkv * n_tokens * kHeadDim;
   for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
     AppendBatch ab{};
     SummaryBatch sb{};
@@ -384,11 +392,9 @@ int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* 
       max_count = std::max(max_count, last - first);
     }
     sb.n = ab.n;
-    const uint16_t* kk = (const uint16_t*)k + (size_t)i0 * row_elems;
-    const uint16_t* vv = (const uint16_t*)v + (size_t)i0 * row_elems;
     Timing tm[kProfKinds];
     Timing* prof = prof_slots(c, s, tm);
-    hipError_t e = launch_append(c->geo, ab, kk, vv, s, prof);
+    hipError_t e = kernels(ab, (size_t)i0, prof);
     if (e == hipSuccess && max_count > 0) e = launch_summary(c->geo, sb, max_count, s, prof);
     prof_collect(c, prof);
     if (e != hipSuccess) return hip_fail(e, "append launch");
@@ -397,11 +403,35 @@ int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* 
   return BSATTN_OK;
 }
 
-int bsattn_append_quantized(bsattn_cache* c, const uint32_t*, const void*, const void*,
-                            const uint32_t*, const void*, const void*, const int32_t*, int32_t,
-                            int32_t, void*) {
-  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
-  return fail(BSATTN_ERR_INVALID, "quantized caches are not available in this build");
+int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* seq_ids,
+                  int32_t n_seqs, int32_t n_tokens, void* stream) {
+  if (!c || !k || !v) return fail(BSATTN_ERR_INVALID, "null argument");
+  hipStream_t s = (hipStream_t)stream;
+  const size_t row = (size_t)c->geo.hkv * n_tokens * kHeadDim;  // elements per sequence
+  const bool quant = c->d.kv_bits != 0;
+  return append_impl(c, seq_ids, n_seqs, n_tokens, s, [&](const AppendBatch& ab, size_t i0, Timing* prof) {
+    const uint16_t* kk = (const uint16_t*)k + i0 * row;
+    const uint16_t* vv = (const uint16_t*)v + i0 * row;
+    return quant ? launch_append_q16(c->geo, ab, kk, vv, s, prof)
+                 : launch_append(c->geo, ab, kk, vv, s, prof);
+  });
+}
+
+int bsattn_append_quantized(bsattn_cache* c, const uint32_t* k_w, const void* k_s, const void* k_b,
+                            const uint32_t* v_w, const void* v_s, const void* v_b,
+                            const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
+                            void* stream) {
+  if (!c || !k_w || !k_s || !k_b || !v_w || !v_s || !v_b) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (c->d.kv_bits == 0) return fail(BSATTN_ERR_INVALID, "not a quantized cache (kv_bits 0): use bsattn_append");
+  hipStream_t s = (hipStream_t)stream;
+  const size_t rows = (size_t)c->geo.hkv * n_tokens;  // token rows per sequence
+  const size_t words = kHeadDim * c->d.kv_bits / 32, groups = kHeadDim / c->d.group_size;
+  return append_impl(c, seq_ids, n_seqs, n_tokens, s, [&](const AppendBatch& ab, size_t i0, Timing* prof) {
+    const size_t wo = i0 * rows * words, go = i0 * rows * groups;
+    return launch_append_quantized(c->geo, ab, k_w + wo, (const uint16_t*)k_s + go,
+                                   (const uint16_t*)k_b + go, v_w + wo, (const uint16_t*)v_s + go,
+                                   (const uint16_t*)v_b + go, s, prof);
+  });
 }
 
 static int do_select(bsattn_cache* c, const void* q, const std::vector<int32_t>& seqs,
@@ -592,10 +622,32 @@ int bsattn_export(const bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs,
   return BSATTN_OK;
 }
 
-int bsattn_export_quantized(const bsattn_cache* c, const int32_t*, int32_t, uint32_t*, void*, void*,
-                            uint32_t*, void*, void*, void*) {
-  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
-  return fail(BSATTN_ERR_INVALID, "quantized caches are not available in this build");
+int bsattn_export_quantized(const bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs,
+                            uint32_t* k_w, void* k_s, void* k_b, uint32_t* v_w, void* v_s,
+                            void* v_b, void* stream) {
+  if (!c || !k_w || !k_s || !k_b || !v_w || !v_s || !v_b) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (c->d.kv_bits == 0) return fail(BSATTN_ERR_INVALID, "not a quantized cache (kv_bits 0): use bsattn_export");
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  const int T = c->len[seqs[0]];
+  for (int sq : seqs)
+    if (c->len[sq] != T) return fail(BSATTN_ERR_INVALID, "listed sequences hold different token counts");
+  if (T == 0) return BSATTN_OK;
+  DeviceGuard dg(c->d.device);
+  const size_t rows = (size_t)c->geo.hkv * T;
+  const size_t words = kHeadDim * c->d.kv_bits / 32, groups = kHeadDim / c->d.group_size;
+  for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
+    SeqBatch b{};
+    b.n = std::min(kMaxBatch, n_seqs - i0);
+    for (int i = 0; i < b.n; ++i) b.ids[i] = seqs[i0 + i];
+    const size_t wo = (size_t)i0 * rows * words, go = (size_t)i0 * rows * groups;
+    HIP_TRY(launch_export_quantized(c->geo, b, T, k_w + wo, (uint16_t*)k_s + go, (uint16_t*)k_b + go,
+                                    v_w + wo, (uint16_t*)v_s + go, (uint16_t*)v_b + go,
+                                    (hipStream_t)stream),
+            "export launch");
+  }
+  return BSATTN_OK;
 }
 
 int bsattn_export_summaries(const bsattn_cache* c, int32_t seq, void* out, void* stream) {

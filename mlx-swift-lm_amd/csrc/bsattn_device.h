@@ -1,0 +1,418 @@
+// bsattn_device.h -- device-side helpers shared by the 16-bit kernels
+// (bsattn_kernels.hip) and the affine-quantized kernels (bsattn_quant.hip):
+// element conversions, the MFMA wrapper, fragment-major tile addressing,
+// the wave-level top-K selection and cross-lane-group reductions.
+#pragma once
+
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bsattn_internal.h"
+
+namespace bsattn {
+
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------
+// element conversions (dtype 0 = fp16, 1 = bf16); RNE on the way down
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ float to_f32(uint16_t b) {
+  if constexpr (DT == 0) return (float)__builtin_bit_cast(_Float16, b);
+  else return __uint_as_float((uint32_t)b << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u);
+  return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t from_f32(float f) {
+  if constexpr (DT == 0) return __builtin_bit_cast(uint16_t, (_Float16)f);
+  else return f32_to_bf16_rne(f);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)from_f32<DT>(lo) | ((uint32_t)from_f32<DT>(hi) << 16);
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == 0)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ const int32_t* block_table(const Geometry& g, int seq) {
+  return g.meta + g.bt_off + (size_t)seq * g.mbps;
+}
+
+// ---------------------------------------------------------------------------
+// fragment-major tile addressing (element offsets inside a K or V tile)
+//  K: fragment (t, s) for QK token tile t and k-step s; lane (m, g) holds
+//     dims 32*s + 8*g .. +7 of token tok_of(m / 4, 4*t + m % 4).
+//  V: fragment (dt, s2) for dim tile dt and PV k-step s2; lane (n, g) holds
+//     tokens 32*s2 + 8*g .. +7 of dim 16*dt + n.
+// tok_of(g, e) = 32*(e/8) + 8*g + e%8 is the token whose score lands in
+// accumulator entry e of lane group g (see k_attend).
+// ---------------------------------------------------------------------------
+__host__ __device__ inline int tok_of(int g, int e) { return 32 * (e >> 3) + 8 * g + (e & 7); }
+
+__host__ __device__ inline int k_elem(int tok, int d) {
+  const int e = 8 * (tok >> 5) + (tok & 7);  // accumulator entry of the token
+  const int t = e >> 2, m = 4 * ((tok >> 3) & 3) + (e & 3);
+  const int s = d >> 5, g = (d >> 3) & 3;
+  return (((t * 4 + s) * 64 + m + 16 * g) << 3) + (d & 7);
+}
+
+__host__ __device__ inline int v_elem(int tb, int tok, int d) {
+  const int ks2 = tb >> 5;
+  const int s2 = tok >> 5, g = (tok >> 3) & 3;
+  const int dt = d >> 4, n = d & 15;
+  return (((dt * ks2 + s2) * 64 + n + 16 * g) << 3) + (tok & 7);
+}
+
+// ---------------------------------------------------------------------------
+// metadata patch: meta[idx[i]] = val[i]
+__device__ __forceinline__ uint16_t* summary_row(const Geometry& g, int seq, int h, int j) {
+  return g.summ + (((size_t)seq * g.hkv + h) * g.mbps + j) * kHeadDim;
+}
+
+__device__ __forceinline__ uint32_t score_key(float s) {
+  if (__builtin_isnan(s)) return 0u;
+  if (s == 0.0f) s = 0.0f;
+  const uint32_t b = __float_as_uint(s);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// ---------------------------------------------------------------------------
+// wave-level top-K of one (sequence, kv head): the same selection as the
+// oracle (K largest keys, ties to the lower index), computed by one wave with
+// no LDS atomics and no workgroup barriers.  Lane l holds candidates
+// c0 + l + 64*k, k < S (S a power of two; padded keys are 0).  tau = the
+// K-th largest key is found bit by bit from the top: a candidate prefix
+// (always >= 1, so padded keys never count) stays if at least K keys are
+// >= it, counted with ballots.  Candidates c0 .. c0+nc-1, nc <= 64 * S,
+// nc > K > 0.  Writes the K chosen block indices, ascending, to sel_blk and
+// their pages (from bt) to sel_page when sel_page is not null.
+// ---------------------------------------------------------------------------
+constexpr int kSelKeysPerLane = 16;
+constexpr int kSelMaxK = 256;  // top_k limit of the in-kernel selection
+
+template <int S>
+__device__ __forceinline__ void wave_topk_s(const float* __restrict__ srow,
+                                            const int32_t* __restrict__ bt, int c0, int nc,
+                                            int K, int* sel_blk, int* sel_page) {
+  const int lane = threadIdx.x & 63;
+  uint32_t key[S];
+  int page[S];
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    const int i = lane + 64 * k;
+    const bool real = i < nc;
+    key[k] = real ? score_key(srow[c0 + i]) : 0u;
+    page[k] = (real && sel_page) ? bt[c0 + i] : 0;
+  }
+  // all compares of a step are issued before the first popcount: each
+  // scalar read of a VALU-written mask waits for the VALU pipeline, and
+  // grouping them pays that wait once per step instead of once per slot
+  uint32_t tau = 0u;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    uint64_t m[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k) m[k] = __ballot(key[k] >= cand);
+    __builtin_amdgcn_sched_barrier(0);
+    int cnt = 0;
+#pragma unroll
+    for (int k = 0; k < S; ++k) cnt += __popcll(m[k]);
+    if (cnt >= K) tau = cand;
+  }
+  // keys > tau are taken; of the keys == tau, the krem lowest indices
+  int gt_total = 0;
+  {
+    uint64_t m[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k) m[k] = __ballot(key[k] > tau);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < S; ++k) gt_total += __popcll(m[k]);
+  }
+  const int krem = K - gt_total;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int sel_before = 0, ties_before = 0;
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    const int i = lane + 64 * k;
+    const bool eq = i < nc && key[k] == tau;
+    const uint64_t eqm = __ballot(eq);
+    const bool take = key[k] > tau || (eq && ties_before + __popcll(eqm & below) < krem);
+    const uint64_t tm = __ballot(take);
+    if (take) {
+      const int pos = sel_before + __popcll(tm & below);
+      sel_blk[pos] = c0 + i;
+      if (sel_page) sel_page[pos] = page[k];
+    }
+    sel_before += __popcll(tm);
+    ties_before += __popcll(eqm);
+  }
+}
+
+// S = smallest power of two with 64 * S >= nc (nc <= 64 * kSelKeysPerLane)
+__device__ __forceinline__ void wave_topk(const float* __restrict__ srow,
+                                          const int32_t* __restrict__ bt, int c0, int nc, int K,
+                                          int* sel_blk, int* sel_page) {
+  if (nc <= 64) wave_topk_s<1>(srow, bt, c0, nc, K, sel_blk, sel_page);
+  else if (nc <= 128) wave_topk_s<2>(srow, bt, c0, nc, K, sel_blk, sel_page);
+  else if (nc <= 256) wave_topk_s<4>(srow, bt, c0, nc, K, sel_blk, sel_page);
+  else if (nc <= 512) wave_topk_s<8>(srow, bt, c0, nc, K, sel_blk, sel_page);
+  else wave_topk_s<16>(srow, bt, c0, nc, K, sel_blk, sel_page);
+}
+
+// Block in output slot p of the selection for nb blocks: sinks [0, ns),
+// then the K ranked candidates (sel), then recent [nb - nr, nb); when the
+// candidates do not outnumber K every block is kept.
+__device__ __forceinline__ int selected_block(int p, int nb, bool ranked, int ns, int nr, int K,
+                                              const int* sel) {
+  if (!ranked) return p < nb ? p : -1;
+  if (p < ns) return p;
+  if (p < ns + K) return sel[p - ns];
+  if (p < ns + K + nr) return nb - nr + (p - ns - K);
+  return -1;
+}
+
+// ---------------------------------------------------------------------------
+// wave-level helpers
+// ---------------------------------------------------------------------------
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two floats -> packed fp16 / bf16 (v_cvt_pk_*_f32, round to nearest even)
+template <int DT>
+__device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
+  if constexpr (DT == 0) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
+// {x[l], x[l ^ 16]} and {x[l], x[l ^ 32]} on the VALU (v_permlane*_swap)
+__device__ __forceinline__ float max_over_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_over_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// ---------------------------------------------------------------------------
+// affine-quantized slab (b = 4 or 8 bits; Tb tokens), byte offsets:
+//   K codes  [Tb * 128 * b / 8]: per 16-token QK tile t, b/4 fragments of
+//            1 KiB; lane (m, g) of the tile's fragments holds, for k-step s,
+//            the 8 codes of dims 32*s + 8*g .. +7 of the tile's row m token
+//            (int4: one word per k-step, all four in one fragment; int8:
+//            two words per k-step, k-steps 2f, 2f+1 in fragment f);
+//   V codes  [same]: fragments (dim-tile group, PV k-step s2); lane (n, g)
+//            holds, per 16-dim tile dt, the codes of tokens 32*s2 + 8*g .. +7
+//            of dim 16*dt + n (int4: one word per dt, four dt per fragment;
+//            int8: two words per dt, two dt per fragment);
+//   scale / bias [Tb][8 x fp16]: (k scale g0, g1, k bias g0, g1, v scale g0,
+//            g1, v bias g0, g1) of a token, at entry sb_entry(tok): lane group
+//            g reads its Tb/4 tokens tok_of(g, e) as one contiguous run.
+// Inside a 32-bit word, int4 element e (dim or token order) sits in nibble
+// q_nib(e), so that (w >> 4k) & 0x000F000F holds elements 2k and 2k+1; int8
+// element e sits in byte e.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline int q_nib(int e) { return (e >> 1) + 4 * (e & 1); }
+
+// byte offset of the code of (tok, d) in the K-code tile; *shift = its bit
+// offset inside that byte
+__host__ __device__ inline int kq_byte(int bits, int tok, int d, int* shift) {
+  const int ea = 8 * (tok >> 5) + (tok & 7);
+  const int t = ea >> 2, m = 4 * ((tok >> 3) & 3) + (ea & 3);
+  const int s = d >> 5, g = (d >> 3) & 3, e = d & 7;
+  const int lane = m + 16 * g;
+  if (bits == 4) {
+    const int nb = q_nib(e);
+    *shift = 4 * (nb & 1);
+    return (t * 64 + lane) * 16 + 4 * s + (nb >> 1);
+  }
+  *shift = 0;
+  return ((t * 2 + (s >> 1)) * 64 + lane) * 16 + 4 * (2 * (s & 1) + (e >> 2)) + (e & 3);
+}
+
+__host__ __device__ inline int vq_byte(int bits, int tb, int tok, int d, int* shift) {
+  const int ks2 = tb >> 5, s2 = tok >> 5, g = (tok >> 3) & 3, e = tok & 7;
+  const int dt = d >> 4, lane = (d & 15) + 16 * g;
+  if (bits == 4) {
+    const int nb = q_nib(e);
+    *shift = 4 * (nb & 1);
+    return (((dt >> 2) * ks2 + s2) * 64 + lane) * 16 + 4 * (dt & 3) + (nb >> 1);
+  }
+  *shift = 0;
+  return (((dt >> 1) * ks2 + s2) * 64 + lane) * 16 + 4 * (2 * (dt & 1) + (e >> 2)) + (e & 3);
+}
+
+__host__ __device__ inline int sb_entry(int tb, int tok) {
+  return ((tok >> 3) & 3) * (tb >> 2) + 8 * (tok >> 5) + (tok & 7);
+}
+
+// ---------------------------------------------------------------------------
+// attention workgroup plumbing shared by the 16-bit and quantized kernels.
+// A workgroup is W waves = W consecutive selected slots of one (sequence,
+// kv head); wave w of split `split` handles slot split * W + w.
+// ---------------------------------------------------------------------------
+// Block (j) and physical page of this wave's slot, -1 when the slot is empty.
+// SEL: the selection is computed here from the block scores (wave 0 runs
+// wave_topk for the sequence and kv head, loading the candidates' block-table
+// entries alongside their scores, and shares blocks and pages through
+// s_sel / s_selp); forced slots load their page before the selection is
+// known.  Split 0 then writes the selected indices to idx (if not null).
+// Otherwise the block comes from idx; -1 and indices past the sequence's
+// last block contribute nothing.  Contains a workgroup barrier when SEL.
+template <int TB, int W, bool SEL>
+__device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, int seq, int len,
+                                            int split, int wave, int lane,
+                                            int32_t* __restrict__ idx,
+                                            const float* __restrict__ scores, int* s_sel,
+                                            int* s_selp, int& j_out, int& page_out) {
+  const int slot = split * W + wave;
+  int j = -1, page = -1;
+  if constexpr (SEL) {
+    const int nb = len > 0 ? (len + TB - 1) / TB : 0;
+    const int c0 = geo.ns, nc = nb - geo.nr - c0, K = geo.top_k;
+    const bool ranked = nc > K;
+    const int32_t* bt = block_table(geo, seq);
+    // sink / recent / every-block slots are known from the length alone
+    const bool picked = ranked && K > 0 && slot >= geo.ns && slot < geo.ns + K;
+    if (!picked) {
+      j = selected_block(slot, nb, ranked, geo.ns, geo.nr, K, s_sel);
+      if (j >= 0) page = uniform(bt[j]);
+    }
+    if (ranked && K > 0) {  // one wave selects, the workgroup shares the result
+      if (wave == 0) wave_topk(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, bt, c0, nc, K, s_sel, s_selp);
+      __syncthreads();
+      if (picked) {
+        j = s_sel[slot - geo.ns];
+        page = s_selp[slot - geo.ns];
+      }
+    }
+    if (idx != nullptr && split == 0 && wave == 0) {
+      int32_t* row = idx + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
+      for (int p = lane; p < geo.nsel_max; p += 64)
+        row[p] = selected_block(p, nb, ranked, geo.ns, geo.nr, K, s_sel);
+    }
+  } else {
+    if (slot < geo.nsel_max) j = idx[((size_t)bi * geo.hkv + h) * geo.nsel_max + slot];
+    j = uniform(j);
+    if (j >= geo.mbps || (int64_t)j * TB >= len) j = -1;
+    if (j >= 0) page = uniform(block_table(geo, seq)[j]);
+  }
+  j_out = uniform(j);
+  page_out = uniform(page);
+}
+
+// Stores one 16-dim tile of this wave's O (MFMA accumulator layout: lane
+// (dim n, group g) holds heads 4g .. 4g+3) into s_o[head][dim].
+template <int G>
+__device__ __forceinline__ void store_o_tile(float (*s_o)[kHeadDim], int dt, int n, int g,
+                                             const f32x4& o) {
+  if constexpr (G >= 4) {
+    if (4 * g < G) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_o[4 * g + i][16 * dt + n] = o[i];
+    }
+  } else {
+    if (g == 0) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) s_o[i][16 * dt + n] = o[i];
+    }
+  }
+}
+
+// Per-wave (m, l, o) of an empty slot.
+template <int G>
+__device__ __forceinline__ void store_empty(float* s_m, float* s_l, float (*s_o)[kHeadDim],
+                                            int lane) {
+  if (lane < G) {
+    s_m[lane] = -INFINITY;
+    s_l[lane] = 0.f;
+  }
+  for (int e = lane; e < G * kHeadDim; e += 64) s_o[e / kHeadDim][e % kHeadDim] = 0.f;
+}
+
+// Merges the W waves' (m, l, o) (after a workgroup barrier) and writes the
+// normalised output (one split) or the unnormalised partial (o, m, l) for
+// k_combine.
+template <int DT, int G, int W>
+__device__ __forceinline__ void attend_merge(const Geometry& geo, int bi, int h, int split,
+                                             const float (*s_m)[16], const float (*s_l)[16],
+                                             const float (*s_o)[G][kHeadDim],
+                                             uint16_t* __restrict__ out,
+                                             float* __restrict__ partials) {
+  const int nsplit = geo.nsplit;
+  for (int e = threadIdx.x; e < G * kHeadDim; e += 64 * W) {
+    const int head = e / kHeadDim, d = e % kHeadDim;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][head]);
+    float L = 0.f, a = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float mw = s_m[w][head];
+        const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+        L += f * s_l[w][head];
+        a += f * s_o[w][head][d];
+      }
+    }
+    const size_t row = (size_t)bi * geo.hq + h * G + head;
+    if (nsplit == 1) {
+      out[row * kHeadDim + d] = from_f32<DT>(L > 0.f ? a / L : 0.f);
+    } else {
+      float* pp = partials + (row * nsplit + split) * (kHeadDim + 2);
+      pp[d] = a;
+      if (d == 0) {
+        pp[kHeadDim] = M;
+        pp[kHeadDim + 1] = L;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host-side launch helper
+// ---------------------------------------------------------------------------
+// Launches `kernel`; with a profiling slot for its kind, the dispatch itself
+// records the slot's start/stop events (hipExtLaunchKernel).
+template <typename F, typename... Args>
+static void launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Timing* prof,
+                   int kind, Args... args) {
+  if (prof && prof[kind].start) {
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, prof[kind].start, prof[kind].stop,
+                          0u, args...);
+    prof[kind].used = true;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+  }
+}
+
+}  // namespace bsattn

@@ -28,8 +28,9 @@ struct Geometry {
   int32_t mbps;               // block-table width
   int32_t bt_off;             // offset of the block table inside meta
   int64_t slab_bytes;         // bytes of one (page, kv head) slab
-  // byte offsets inside a slab
-  int64_t k_off, v_off, ks_off, kb_off, vs_off, vb_off;
+  // byte offsets inside a slab: K tile (or K codes), V tile (or V codes),
+  // per-token scales / biases (quantized caches only)
+  int64_t k_off, v_off, sb_off;
   uint8_t* pool;              // [num_pages][hkv] slabs
   uint16_t* summ;             // [max_seqs][hkv][mbps][D], by logical block
   int32_t* meta;              // [max_seqs] lengths, then [max_seqs][mbps] pages
@@ -75,10 +76,19 @@ struct Timing {
 hipError_t launch_patch(const Geometry& g, const PatchBatch& pb, hipStream_t s);
 hipError_t launch_append(const Geometry& g, const AppendBatch& ab, const void* k,
                          const void* v, hipStream_t s, Timing* prof);
+// quantized caches (bsattn_quant.hip): append from fp16 (quantize on append)
+// or from the MLX layout; block summaries of dequantized keys; attention
+hipError_t launch_append_q16(const Geometry& g, const AppendBatch& ab, const void* k,
+                             const void* v, hipStream_t s, Timing* prof);
 hipError_t launch_append_quantized(const Geometry& g, const AppendBatch& ab,
                                    const uint32_t* kw, const void* ks, const void* kb,
                                    const uint32_t* vw, const void* vs, const void* vb,
-                                   hipStream_t s);
+                                   hipStream_t s, Timing* prof);
+hipError_t launch_summary_q(const Geometry& g, const SummaryBatch& sb, int max_count,
+                            hipStream_t s, Timing* prof);
+hipError_t launch_attend_q(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
+                           const float* scores, bool fused_select, float sl2, void* out,
+                           float* partials, hipStream_t s, Timing* prof);
 hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
                           hipStream_t s, Timing* prof);
 int select_chunks(const Geometry& g, int len);

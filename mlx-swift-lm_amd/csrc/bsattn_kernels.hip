@@ -18,52 +18,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "bsattn_internal.h"
+#include "bsattn_device.h"
 
 namespace bsattn {
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-// ---------------------------------------------------------------------------
-// element conversions (dtype 0 = fp16, 1 = bf16); RNE on the way down
-// ---------------------------------------------------------------------------
-template <int DT>
-__device__ __forceinline__ float to_f32(uint16_t b) {
-  if constexpr (DT == 0) return (float)__builtin_bit_cast(_Float16, b);
-  else return __uint_as_float((uint32_t)b << 16);
-}
-
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u);
-  return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
-}
-
-template <int DT>
-__device__ __forceinline__ uint16_t from_f32(float f) {
-  if constexpr (DT == 0) return __builtin_bit_cast(uint16_t, (_Float16)f);
-  else return f32_to_bf16_rne(f);
-}
-
-template <int DT>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)from_f32<DT>(lo) | ((uint32_t)from_f32<DT>(hi) << 16);
-}
-
-template <int DT>
-__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
-  if constexpr (DT == 0)
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // 256-thread inclusive scan; s_tmp holds 4 ints.
 __device__ __forceinline__ int block_scan_incl(int v, int* s_tmp, int* total) {
@@ -88,37 +45,6 @@ __device__ __forceinline__ int block_scan_incl(int v, int* s_tmp, int* total) {
   return off + x;
 }
 
-__device__ __forceinline__ const int32_t* block_table(const Geometry& g, int seq) {
-  return g.meta + g.bt_off + (size_t)seq * g.mbps;
-}
-
-// ---------------------------------------------------------------------------
-// fragment-major tile addressing (element offsets inside a K or V tile)
-//  K: fragment (t, s) for QK token tile t and k-step s; lane (m, g) holds
-//     dims 32*s + 8*g .. +7 of token tok_of(m / 4, 4*t + m % 4).
-//  V: fragment (dt, s2) for dim tile dt and PV k-step s2; lane (n, g) holds
-//     tokens 32*s2 + 8*g .. +7 of dim 16*dt + n.
-// tok_of(g, e) = 32*(e/8) + 8*g + e%8 is the token whose score lands in
-// accumulator entry e of lane group g (see k_attend).
-// ---------------------------------------------------------------------------
-__host__ __device__ inline int tok_of(int g, int e) { return 32 * (e >> 3) + 8 * g + (e & 7); }
-
-__host__ __device__ inline int k_elem(int tok, int d) {
-  const int e = 8 * (tok >> 5) + (tok & 7);  // accumulator entry of the token
-  const int t = e >> 2, m = 4 * ((tok >> 3) & 3) + (e & 3);
-  const int s = d >> 5, g = (d >> 3) & 3;
-  return (((t * 4 + s) * 64 + m + 16 * g) << 3) + (d & 7);
-}
-
-__host__ __device__ inline int v_elem(int tb, int tok, int d) {
-  const int ks2 = tb >> 5;
-  const int s2 = tok >> 5, g = (tok >> 3) & 3;
-  const int dt = d >> 4, n = d & 15;
-  return (((dt * ks2 + s2) * 64 + n + 16 * g) << 3) + (tok & 7);
-}
-
-// ---------------------------------------------------------------------------
-// metadata patch: meta[idx[i]] = val[i]
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_patch(int32_t* meta, PatchBatch pb) {
   const int t = threadIdx.x;
@@ -160,10 +86,6 @@ __global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
 // Summaries are stored by logical block: summ[seq][kv head][block][D].
 // grid (max_count, Hkv, n)
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint16_t* summary_row(const Geometry& g, int seq, int h, int j) {
-  return g.summ + (((size_t)seq * g.hkv + h) * g.mbps + j) * kHeadDim;
-}
-
 template <int DT>
 __global__ __launch_bounds__(128) void k_summary(Geometry geo, SummaryBatch sb) {
   const int bi = blockIdx.z, h = blockIdx.y;
@@ -186,13 +108,6 @@ __global__ __launch_bounds__(128) void k_summary(Geometry geo, SummaryBatch sb) 
 // up front with no indirection.  grid (chunks, Hkv, n)
 // ---------------------------------------------------------------------------
 constexpr int kSelChunk = 64;
-
-__device__ __forceinline__ uint32_t score_key(float s) {
-  if (__builtin_isnan(s)) return 0u;
-  if (s == 0.0f) s = 0.0f;
-  const uint32_t b = __float_as_uint(s);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
 
 template <int DT>
 __device__ __forceinline__ void unpack8(const u32x4 raw, float* out) {
@@ -254,103 +169,6 @@ __global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
       if (c == 0) srow[j] = best;
     }
   }
-}
-
-// ---------------------------------------------------------------------------
-// wave-level top-K of one (sequence, kv head): the same selection as the
-// oracle (K largest keys, ties to the lower index), computed by one wave with
-// no LDS atomics and no workgroup barriers.  Lane l holds candidates
-// c0 + l + 64*k, k < S (S a power of two; padded keys are 0).  tau = the
-// K-th largest key is found bit by bit from the top: a candidate prefix
-// (always >= 1, so padded keys never count) stays if at least K keys are
-// >= it, counted with ballots.  Candidates c0 .. c0+nc-1, nc <= 64 * S,
-// nc > K > 0.  Writes the K chosen block indices, ascending, to sel_blk and
-// their pages (from bt) to sel_page when sel_page is not null.
-// ---------------------------------------------------------------------------
-constexpr int kSelKeysPerLane = 16;
-constexpr int kSelMaxK = 256;  // top_k limit of the in-kernel selection
-
-template <int S>
-__device__ __forceinline__ void wave_topk_s(const float* __restrict__ srow,
-                                            const int32_t* __restrict__ bt, int c0, int nc,
-                                            int K, int* sel_blk, int* sel_page) {
-  const int lane = threadIdx.x & 63;
-  uint32_t key[S];
-  int page[S];
-#pragma unroll
-  for (int k = 0; k < S; ++k) {
-    const int i = lane + 64 * k;
-    const bool real = i < nc;
-    key[k] = real ? score_key(srow[c0 + i]) : 0u;
-    page[k] = (real && sel_page) ? bt[c0 + i] : 0;
-  }
-  // all compares of a step are issued before the first popcount: each
-  // scalar read of a VALU-written mask waits for the VALU pipeline, and
-  // grouping them pays that wait once per step instead of once per slot
-  uint32_t tau = 0u;
-#pragma unroll 1
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = tau | (1u << bit);
-    uint64_t m[S];
-#pragma unroll
-    for (int k = 0; k < S; ++k) m[k] = __ballot(key[k] >= cand);
-    __builtin_amdgcn_sched_barrier(0);
-    int cnt = 0;
-#pragma unroll
-    for (int k = 0; k < S; ++k) cnt += __popcll(m[k]);
-    if (cnt >= K) tau = cand;
-  }
-  // keys > tau are taken; of the keys == tau, the krem lowest indices
-  int gt_total = 0;
-  {
-    uint64_t m[S];
-#pragma unroll
-    for (int k = 0; k < S; ++k) m[k] = __ballot(key[k] > tau);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < S; ++k) gt_total += __popcll(m[k]);
-  }
-  const int krem = K - gt_total;
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  int sel_before = 0, ties_before = 0;
-#pragma unroll
-  for (int k = 0; k < S; ++k) {
-    const int i = lane + 64 * k;
-    const bool eq = i < nc && key[k] == tau;
-    const uint64_t eqm = __ballot(eq);
-    const bool take = key[k] > tau || (eq && ties_before + __popcll(eqm & below) < krem);
-    const uint64_t tm = __ballot(take);
-    if (take) {
-      const int pos = sel_before + __popcll(tm & below);
-      sel_blk[pos] = c0 + i;
-      if (sel_page) sel_page[pos] = page[k];
-    }
-    sel_before += __popcll(tm);
-    ties_before += __popcll(eqm);
-  }
-}
-
-// S = smallest power of two with 64 * S >= nc (nc <= 64 * kSelKeysPerLane)
-__device__ __forceinline__ void wave_topk(const float* __restrict__ srow,
-                                          const int32_t* __restrict__ bt, int c0, int nc, int K,
-                                          int* sel_blk, int* sel_page) {
-  if (nc <= 64) wave_topk_s<1>(srow, bt, c0, nc, K, sel_blk, sel_page);
-  else if (nc <= 128) wave_topk_s<2>(srow, bt, c0, nc, K, sel_blk, sel_page);
-  else if (nc <= 256) wave_topk_s<4>(srow, bt, c0, nc, K, sel_blk, sel_page);
-  else if (nc <= 512) wave_topk_s<8>(srow, bt, c0, nc, K, sel_blk, sel_page);
-  else wave_topk_s<16>(srow, bt, c0, nc, K, sel_blk, sel_page);
-}
-
-// Block in output slot p of the selection for nb blocks: sinks [0, ns),
-// then the K ranked candidates (sel), then recent [nb - nr, nb); when the
-// candidates do not outnumber K every block is kept.
-__device__ __forceinline__ int selected_block(int p, int nb, bool ranked, int ns, int nr, int K,
-                                              const int* sel) {
-  if (!ranked) return p < nb ? p : -1;
-  if (p < ns) return p;
-  if (p < ns + K) return sel[p - ns];
-  if (p < ns + K + nr) return nb - nr + (p - ns - K);
-  return -1;
 }
 
 // ---------------------------------------------------------------------------
@@ -447,34 +265,6 @@ __global__ __launch_bounds__(256) void k_topk(Geometry geo, SeqBatch sb,
 }
 
 // ---------------------------------------------------------------------------
-// wave-level helpers
-// ---------------------------------------------------------------------------
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// two floats -> packed fp16 / bf16 (v_cvt_pk_*_f32, round to nearest even)
-template <int DT>
-__device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
-  if constexpr (DT == 0) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
-  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
-}
-
-// {x[l], x[l ^ 16]} and {x[l], x[l ^ 32]} on the VALU (v_permlane*_swap)
-__device__ __forceinline__ float max_over_groups(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float sum_over_groups(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-// ---------------------------------------------------------------------------
 // gathered attention.  Workgroup = W waves = W consecutive selected slots of
 // one (sequence, kv head); each wave does one block with MFMA 16x16x32:
 //   S^T[token][head] = K[token][:] . Q[head][:]       (A = K rows, B = Q^T)
@@ -506,7 +296,6 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   constexpr int NT = TB / 16;   // QK token tiles
   constexpr int EPL = TB / 4;   // scores per lane
   constexpr int KS2 = TB / 32;  // PV k-steps
-  constexpr int NTH = 64 * W;
   __shared__ float s_m[W][16], s_l[W][16];
   __shared__ float s_o[W][G][kHeadDim];
   __shared__ int s_sel[SEL ? kSelMaxK : 1];
@@ -515,7 +304,6 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int seq = sb.ids[bi];
-  const int slot = split * W + wave;
   u32x4 qf[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
@@ -525,40 +313,8 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
     for (int s = 0; s < 4; ++s) qf[s] = *(const u32x4*)(src + 32 * s);
   }
   const int len = uniform(geo.meta[seq]);
-  int j = -1, page = -1;
-  if constexpr (SEL) {
-    const int nb = len > 0 ? (len + TB - 1) / TB : 0;
-    const int c0 = geo.ns, nc = nb - geo.nr - c0, K = geo.top_k;
-    const bool ranked = nc > K;
-    const int32_t* bt = block_table(geo, seq);
-    // sink / recent / every-block slots are known from the length alone
-    const bool picked = ranked && K > 0 && slot >= geo.ns && slot < geo.ns + K;
-    if (!picked) {
-      j = selected_block(slot, nb, ranked, geo.ns, geo.nr, K, s_sel);
-      if (j >= 0) page = uniform(bt[j]);
-    }
-    if (ranked && K > 0) {  // one wave selects, the workgroup shares the result
-      if (wave == 0) wave_topk(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, bt, c0, nc, K, s_sel, s_selp);
-      __syncthreads();
-      if (picked) {
-        j = s_sel[slot - geo.ns];
-        page = s_selp[slot - geo.ns];
-      }
-    }
-    if (idx != nullptr && split == 0 && wave == 0) {
-      int32_t* row = idx + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
-      for (int p = lane; p < geo.nsel_max; p += 64)
-        row[p] = selected_block(p, nb, ranked, geo.ns, geo.nr, K, s_sel);
-    }
-  } else {
-    if (slot < geo.nsel_max) j = idx[((size_t)bi * geo.hkv + h) * geo.nsel_max + slot];
-    j = uniform(j);
-    // -1 and indices past the sequence's last block contribute nothing
-    if (j >= geo.mbps || (int64_t)j * TB >= len) j = -1;
-    if (j >= 0) page = uniform(block_table(geo, seq)[j]);
-  }
-  j = uniform(j);
-  page = uniform(page);
+  int j, page;
+  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, scores, s_sel, s_selp, j, page);
   if (j >= 0) {
     const int valid = min(TB, len - j * TB);
     const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
@@ -642,58 +398,17 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
         o = mfma16x16x32<DT>(pf[s2], vf[dt][s2], o);
         if constexpr (DT == 1) o = mfma16x16x32<DT>(pl[s2], vf[dt][s2], o);
       }
-      if constexpr (G >= 4) {
-        if (4 * g < G) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) s_o[wave][4 * g + i][16 * dt + n] = o[i];
-        }
-      } else {
-        if (g == 0) {
-#pragma unroll
-          for (int i = 0; i < G; ++i) s_o[wave][i][16 * dt + n] = o[i];
-        }
-      }
+      store_o_tile<G>(s_o[wave], dt, n, g, o);
     }
     if (g == 0 && n < G) {
       s_m[wave][n] = mx;
       s_l[wave][n] = ps;
     }
   } else {
-    if (lane < G) {
-      s_m[wave][lane] = -INFINITY;
-      s_l[wave][lane] = 0.f;
-    }
-    for (int e = lane; e < G * kHeadDim; e += 64) s_o[wave][e / kHeadDim][e % kHeadDim] = 0.f;
+    store_empty<G>(s_m[wave], s_l[wave], s_o[wave], lane);
   }
   __syncthreads();
-  const int nsplit = geo.nsplit;
-  for (int e = threadIdx.x; e < G * kHeadDim; e += NTH) {
-    const int head = e / kHeadDim, d = e % kHeadDim;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][head]);
-    float L = 0.f, a = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        const float mw = s_m[w][head];
-        const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-        L += f * s_l[w][head];
-        a += f * s_o[w][head][d];
-      }
-    }
-    const size_t row = (size_t)bi * geo.hq + h * G + head;
-    if (nsplit == 1) {
-      out[row * kHeadDim + d] = from_f32<DT>(L > 0.f ? a / L : 0.f);
-    } else {
-      float* pp = partials + (row * nsplit + split) * (kHeadDim + 2);
-      pp[d] = a;
-      if (d == 0) {
-        pp[kHeadDim] = M;
-        pp[kHeadDim + 1] = L;
-      }
-    }
-  }
+  attend_merge<DT, G, W>(geo, bi, h, split, s_m, s_l, s_o, out, partials);
 }
 
 // ---------------------------------------------------------------------------
@@ -773,20 +488,6 @@ __global__ __launch_bounds__(128) void k_export_summaries(Geometry geo, int seq,
 // ===========================================================================
 // launchers
 // ===========================================================================
-// Launches `kernel`; with a profiling slot for its kind, the dispatch itself
-// records the slot's start/stop events (hipExtLaunchKernel).
-template <typename F, typename... Args>
-static void launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Timing* prof,
-                   int kind, Args... args) {
-  if (prof && prof[kind].start) {
-    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, prof[kind].start, prof[kind].stop,
-                          0u, args...);
-    prof[kind].used = true;
-  } else {
-    hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
-  }
-}
-
 hipError_t launch_patch(const Geometry& g, const PatchBatch& pb, hipStream_t s) {
   hipLaunchKernelGGL(k_patch, dim3(1), dim3(256), 0, s, g.meta, pb);
   return hipGetLastError();
@@ -800,14 +501,9 @@ hipError_t launch_append(const Geometry& g, const AppendBatch& ab, const void* k
   return hipGetLastError();
 }
 
-hipError_t launch_append_quantized(const Geometry&, const AppendBatch&, const uint32_t*,
-                                   const void*, const void*, const uint32_t*, const void*,
-                                   const void*, hipStream_t) {
-  return hipErrorNotSupported;
-}
-
 hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
                           hipStream_t s, Timing* prof) {
+  if (g.kv_bits != 0) return launch_summary_q(g, sb, max_count, s, prof);
   dim3 grid(max_count, g.hkv, sb.n);
   if (g.dtype == 0)
     launch(k_summary<0>, grid, dim3(128), 0, s, prof, kProfSummary, g, sb);
@@ -874,7 +570,10 @@ static hipError_t attend_impl(const Geometry& g, const SeqBatch& b, const void* 
   dim3 grid(g.nsplit, g.hkv, b.n);
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* oo = (uint16_t*)out;
-  if (g.dtype == 0) {
+  if (g.kv_bits != 0) {
+    hipError_t e = launch_attend_q(g, b, q, idx, scores, SEL, sl2, out, partials, s, prof);
+    if (e != hipSuccess) return e;
+  } else if (g.dtype == 0) {
     if (g.tb == 64) attend_dispatch<0, 64, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
     else attend_dispatch<0, 32, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
   } else {
@@ -917,11 +616,6 @@ hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_ou
   dim3 grid((T + 15) / 16, g.hkv, b.n);
   hipLaunchKernelGGL(k_export, grid, dim3(256), 0, s, g, b, T, (uint16_t*)k_out, (uint16_t*)v_out);
   return hipGetLastError();
-}
-
-hipError_t launch_export_quantized(const Geometry&, const SeqBatch&, int, uint32_t*, void*, void*,
-                                   uint32_t*, void*, void*, hipStream_t) {
-  return hipErrorNotSupported;
 }
 
 hipError_t launch_export_summaries(const Geometry& g, int seq, int nfull, void* out,

@@ -1,0 +1,578 @@
+// bsattn_quant.hip -- gfx950 kernels of the block-sparse decode path over an
+// MLX-style affine-quantized KV cache (b = 4 or 8 bits, group 64 along the
+// head dim, fp16 scale and bias per group: w = scale * code + bias).
+//
+// The slab layout (bsattn_device.h) stores the codes in the order the
+// attention kernel's MFMA operands need them, so every gather load is a
+// contiguous 1 KiB fragment, and the scales / biases of a lane group's
+// tokens as one contiguous run.  Dequantisation is fused into the MFMAs:
+//   - a code c becomes the exact fp16 value OFF + UNIT * c (int4: 1 + c/16,
+//     int8: 1024 + c) with two bit operations per pair, no conversion;
+//   - QK per group g of 64 dims: raw_g = sum_d q_d (OFF + UNIT c_d), so
+//     sum_d q_d c_d = (raw_g - OFF * Q_g) / UNIT with Q_g = sum_d q_d (one
+//     MFMA against an all-ones operand), and
+//     s = sum_g k_scale_g * sum_d q_d c_d + k_bias_g * Q_g;
+//   - PV per group: P_g = p * v_scale_g (fp16) is the A operand against the
+//     codes; the same P_g and p * v_bias_g against an all-ones operand give
+//     sum_t P_g and sum_t p v_bias_g in the accumulator layout of O, so
+//     o = (raw - OFF * sum P_g) / UNIT + sum p v_bias_g needs no shuffles.
+// Summaries of a quantized cache are fp16 means of the dequantized keys
+// (fmaf(scale, code, bias), sequential fold), so scoring and selection are
+// the 16-bit kernels' own.
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bsattn_device.h"
+
+namespace bsattn {
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+__device__ __forceinline__ float lo_f(uint32_t w) { return h2f(w & 0xFFFFu); }
+__device__ __forceinline__ float hi_f(uint32_t w) { return h2f(w >> 16); }
+
+// int4 word (element e in nibble q_nib(e)) -> 8 fp16 values 1 + c/16, in
+// element order: pair k = elements 2k, 2k+1 = nibbles k, k+4
+__device__ __forceinline__ u32x4 nib_to_f16(uint32_t w) {
+  constexpr uint32_t M = 0x03C003C0u, ONE = 0x3C003C00u;
+  return u32x4{((w << 6) & M) | ONE, ((w << 2) & M) | ONE, ((w >> 2) & M) | ONE,
+               ((w >> 6) & M) | ONE};
+}
+
+// two int8 words (element e in byte e) -> 8 fp16 values 1024 + c: each
+// byte becomes the low byte of an fp16 whose high byte is 0x64
+__device__ __forceinline__ u32x4 byte_to_f16(uint32_t lo, uint32_t hi) {
+  constexpr uint32_t H = 0x64646464u;
+  return u32x4{__builtin_amdgcn_perm(H, lo, 0x04010400u), __builtin_amdgcn_perm(H, lo, 0x04030402u),
+               __builtin_amdgcn_perm(H, hi, 0x04010400u), __builtin_amdgcn_perm(H, hi, 0x04030402u)};
+}
+
+template <int KB>
+struct QCode {
+  static constexpr float OFF = KB == 4 ? 1.0f : 1024.0f;  // value of code 0
+  static constexpr float INV_UNIT = KB == 4 ? 16.0f : 1.0f;  // 1 / value step
+  static constexpr int KF = KB / 4;                          // K fragments per token tile
+  static constexpr int DPF = 16 / KB;                        // dim tiles per V fragment
+  static constexpr int WPR = kHeadDim * KB / 32;             // MLX words per token row
+};
+
+// A operand of QK token tile t, k-step s, from the tile's K fragments
+template <int KB>
+__device__ __forceinline__ u32x4 k_operand(const u32x4* kf, int s) {
+  if constexpr (KB == 4) return nib_to_f16(kf[0][s]);
+  else return byte_to_f16(kf[s >> 1][2 * (s & 1)], kf[s >> 1][2 * (s & 1) + 1]);
+}
+
+// B operand of PV dim tile dt, k-step s2, from the V fragments
+template <int KB, int KS2>
+__device__ __forceinline__ u32x4 v_operand(const u32x4* vf, int dt, int s2) {
+  constexpr int DPF = QCode<KB>::DPF;
+  const u32x4& f = vf[(dt / DPF) * KS2 + s2];
+  if constexpr (KB == 4) return nib_to_f16(f[dt & 3]);
+  else return byte_to_f16(f[2 * (dt & 1)], f[2 * (dt & 1) + 1]);
+}
+
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// quantize 8 consecutive dims of one row (lane c of the 16 lanes holding the
+// row; lanes c & ~7 .. +7 hold one 64-dim group), exactly as the affine
+// codec: min / max of the group (the first of equal values, as a scan in dim
+// order keeps), scale = fp16((max - min) / (2^b - 1)) (1 if that is 0),
+// bias = fp16(min), code = clamp(rint((x - bias) / scale), 0, 2^b - 1).
+// ---------------------------------------------------------------------------
+template <int KB>
+__device__ __forceinline__ void quantize8(const uint16_t* __restrict__ src, int c, uint8_t* codes,
+                                          uint16_t* scale_out, uint16_t* bias_out) {
+  const u32x4 raw = *(const u32x4*)src;
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = (e & 1) ? hi_f(raw[e >> 1]) : lo_f(raw[e >> 1]);
+  float mn = x[0], mx = x[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) {
+    if (x[e] < mn) mn = x[e];
+    if (x[e] > mx) mx = x[e];
+  }
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1) {
+    const float pmn = __shfl_xor(mn, off, 64), pmx = __shfl_xor(mx, off, 64);
+    if (c & off) {  // the partner holds the lower dims and wins ties
+      mn = (mn < pmn) ? mn : pmn;
+      mx = (mx > pmx) ? mx : pmx;
+    } else {
+      mn = (pmn < mn) ? pmn : mn;
+      mx = (pmx > mx) ? pmx : mx;
+    }
+  }
+  constexpr float nbins = (float)((1 << KB) - 1);
+  _Float16 s16 = (_Float16)__fdiv_rn(__fsub_rn(mx, mn), nbins);
+  if ((float)s16 == 0.0f) s16 = (_Float16)1.0f;
+  const _Float16 b16 = (_Float16)mn;
+  const float sf = (float)s16, bf = (float)b16;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float qv = __builtin_rintf(__fdiv_rn(__fsub_rn(x[e], bf), sf));
+    qv = qv < 0.0f ? 0.0f : qv;
+    qv = qv > nbins ? nbins : qv;
+    codes[e] = (uint8_t)qv;
+  }
+  if ((c & 7) == 0) {
+    *scale_out = __builtin_bit_cast(uint16_t, s16);
+    *bias_out = __builtin_bit_cast(uint16_t, b16);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// append: workgroup x covers the 8-aligned positions [P0, P0 + 8),
+// P0 = 8 * (old_len / 8 + x), of one (sequence, kv head); the tokens
+// appended there are [max(P0, old), min(P0 + 8, old + L)).  Stage 1 puts
+// their codes and scales / biases in LDS (quantizing fp16 input, or
+// unpacking the MLX layout: element i of a row in word i / (32/b), bits
+// b * (i % (32/b)) up, LSB first; scales / biases [.., D / 64]); stage 2
+// writes whole 32-bit words: K words belong to one token, a V word to one dim
+// and the 8 (int4) or 4 (int8) tokens of this group, merged with the codes
+// already there when the group is only partly new.
+// grid (L / 8 + 2, Hkv, n), 128 threads
+// ---------------------------------------------------------------------------
+template <int KB, bool QUANTIZE>
+__global__ __launch_bounds__(128) void k_append_q(Geometry geo, AppendBatch ab,
+                                                  const uint16_t* __restrict__ k16,
+                                                  const uint16_t* __restrict__ v16,
+                                                  const uint32_t* __restrict__ kw,
+                                                  const uint16_t* __restrict__ ks,
+                                                  const uint16_t* __restrict__ kb,
+                                                  const uint32_t* __restrict__ vw,
+                                                  const uint16_t* __restrict__ vs,
+                                                  const uint16_t* __restrict__ vb) {
+  constexpr int WPR = QCode<KB>::WPR;
+  __shared__ uint8_t s_kc[8][kHeadDim];
+  __shared__ uint8_t s_vc[8][kHeadDim];
+  __shared__ uint32_t s_sb[8][4];
+  const int bi = blockIdx.z, h = blockIdx.y;
+  const int old = ab.old_len[bi], L = ab.L;
+  const int P0 = 8 * (old / 8 + (int)blockIdx.x);
+  const int lo = max(P0, old), hi = min(P0 + 8, old + L);
+  if (lo >= hi) return;
+  const int seq = ab.seq[bi];
+  const int tid = threadIdx.x;
+  {
+    const int i = tid >> 4, c = tid & 15;  // token P0 + i, dims 8c .. 8c+7
+    const int pos = P0 + i;
+    if (pos >= lo && pos < hi) {
+      const size_t row = ((size_t)bi * geo.hkv + h) * L + (pos - old);
+      uint16_t* sbh = (uint16_t*)s_sb[i];
+      if constexpr (QUANTIZE) {
+        const int grp = c >> 3;
+        quantize8<KB>(k16 + row * kHeadDim + 8 * c, c, &s_kc[i][8 * c], sbh + grp, sbh + 2 + grp);
+        quantize8<KB>(v16 + row * kHeadDim + 8 * c, c, &s_vc[i][8 * c], sbh + 4 + grp, sbh + 6 + grp);
+      } else {
+        if constexpr (KB == 4) {
+          const uint32_t a = kw[row * WPR + c], b = vw[row * WPR + c];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            s_kc[i][8 * c + e] = (uint8_t)((a >> (4 * e)) & 15u);
+            s_vc[i][8 * c + e] = (uint8_t)((b >> (4 * e)) & 15u);
+          }
+        } else {
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            const uint32_t a = kw[row * WPR + 2 * c + w], b = vw[row * WPR + 2 * c + w];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              s_kc[i][8 * c + 4 * w + e] = (uint8_t)(a >> (8 * e));
+              s_vc[i][8 * c + 4 * w + e] = (uint8_t)(b >> (8 * e));
+            }
+          }
+        }
+        if (c < 2) {
+          sbh[c] = ks[row * 2 + c];
+          sbh[2 + c] = kb[row * 2 + c];
+          sbh[4 + c] = vs[row * 2 + c];
+          sbh[6 + c] = vb[row * 2 + c];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int blk = P0 / geo.tb, slot0 = P0 - blk * geo.tb;
+  const int page = block_table(geo, seq)[blk];
+  uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
+  uint8_t* Kc = slab + geo.k_off;
+  uint8_t* Vc = slab + geo.v_off;
+  // K: 8 tokens x WPR words
+  for (int u = tid; u < 8 * WPR; u += 128) {
+    const int i = u / WPR, wd = u - i * WPR;
+    const int pos = P0 + i;
+    if (pos < lo || pos >= hi) continue;
+    int sh;
+    uint32_t word = 0u;
+    if constexpr (KB == 4) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) word |= (uint32_t)s_kc[i][8 * wd + e] << (4 * q_nib(e));
+      *(uint32_t*)(Kc + kq_byte(4, slot0 + i, 8 * wd, &sh)) = word;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) word |= (uint32_t)s_kc[i][4 * wd + e] << (8 * e);
+      *(uint32_t*)(Kc + kq_byte(8, slot0 + i, 4 * wd, &sh)) = word;
+    }
+  }
+  // V: thread = dim; words of this group's tokens
+  {
+    const int d = tid;
+    constexpr int TPW = 32 / KB;  // tokens per word
+#pragma unroll
+    for (int w = 0; w < 8 / TPW; ++w) {
+      const int t0 = P0 + w * TPW;
+      if (t0 + TPW <= lo || t0 >= hi) continue;
+      int sh;
+      uint32_t* dst = (uint32_t*)(Vc + vq_byte(KB, geo.tb, slot0 + w * TPW, d, &sh));
+      const bool whole = t0 >= lo && t0 + TPW <= hi;
+      uint32_t word = whole ? 0u : *dst;
+#pragma unroll
+      for (int e = 0; e < TPW; ++e) {
+        const int pos = t0 + e;
+        if (pos < lo || pos >= hi) continue;
+        const int at = KB == 4 ? 4 * q_nib(e) : 8 * e;
+        const uint32_t mask = ((1u << KB) - 1u) << at;
+        word = (word & ~mask) | ((uint32_t)s_vc[pos - P0][d] << at);
+      }
+      *dst = word;
+    }
+  }
+  // scales / biases: 16 B per token
+  if (tid < 8) {
+    const int pos = P0 + tid;
+    if (pos >= lo && pos < hi) {
+      u32x4* dst = (u32x4*)(slab + geo.sb_off) + sb_entry(geo.tb, slot0 + tid);
+      *dst = u32x4{s_sb[tid][0], s_sb[tid][1], s_sb[tid][2], s_sb[tid][3]};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// block summary of a quantized block: thread per dim, sequential fp32 fold
+// of the dequantized keys fmaf(scale, code, bias) from token 0, times 1/Tb,
+// to fp16.  grid (max_count, Hkv, n)
+// ---------------------------------------------------------------------------
+template <int KB>
+__global__ __launch_bounds__(128) void k_summary_q(Geometry geo, SummaryBatch sb) {
+  const int bi = blockIdx.z, h = blockIdx.y;
+  if ((int)blockIdx.x >= sb.count[bi]) return;
+  const int seq = sb.seq[bi];
+  const int j = sb.first[bi] + blockIdx.x;
+  const int page = block_table(geo, seq)[j];
+  const int d = threadIdx.x, grp = d >> 6;
+  const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
+  const uint8_t* Kc = slab + geo.k_off;
+  const uint16_t* Sb = (const uint16_t*)(slab + geo.sb_off);
+  float acc = 0.0f;
+  for (int t = 0; t < geo.tb; ++t) {
+    int sh;
+    const int code = (Kc[kq_byte(KB, t, d, &sh)] >> sh) & ((1 << KB) - 1);
+    const uint16_t* f = Sb + 8 * sb_entry(geo.tb, t);
+    const float w = __builtin_fmaf(h2f(f[grp]), (float)code, h2f(f[2 + grp]));
+    acc = (t == 0) ? w : __fadd_rn(acc, w);
+  }
+  summary_row(geo, seq, h, j)[d] =
+      __builtin_bit_cast(uint16_t, (_Float16)__fmul_rn(acc, 1.0f / (float)geo.tb));
+}
+
+// ---------------------------------------------------------------------------
+// gathered attention over quantized blocks: the 16-bit kernel's structure
+// (one block per wave, W waves per workgroup, selection fused when SEL,
+// split partials merged by k_combine), with the dequantisation folded into
+// the MFMAs as described at the top of this file.  q / out are fp16.
+// grid (nsplit, Hkv, n)
+// ---------------------------------------------------------------------------
+template <int TB, int G, int W, bool SEL, int KB>
+__global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch sb,
+                                                     const uint16_t* __restrict__ q,
+                                                     int32_t* __restrict__ idx,
+                                                     const float* __restrict__ scores,
+                                                     float sl2, uint16_t* __restrict__ out,
+                                                     float* __restrict__ partials) {
+  using QC = QCode<KB>;
+  constexpr int NT = TB / 16;   // QK token tiles
+  constexpr int EPL = TB / 4;   // scores per lane
+  constexpr int KS2 = TB / 32;  // PV k-steps
+  constexpr int KF = QC::KF;
+  constexpr int NVF = (8 / QC::DPF) * KS2;  // V fragments
+  __shared__ float s_m[W][16], s_l[W][16];
+  __shared__ float s_o[W][G][kHeadDim];
+  __shared__ int s_sel[SEL ? kSelMaxK : 1];
+  __shared__ int s_selp[SEL ? kSelMaxK : 1];
+  const int split = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int seq = sb.ids[bi];
+  u32x4 qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
+  if (n < G) {
+    const uint16_t* src = q + ((size_t)bi * geo.hq + h * G + n) * kHeadDim + 8 * g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = *(const u32x4*)(src + 32 * s);
+  }
+  const int len = uniform(geo.meta[seq]);
+  int j, page;
+  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, scores, s_sel, s_selp, j, page);
+  if (j >= 0) {
+    const int valid = min(TB, len - j * TB);
+    const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
+    const u32x4* Kf = (const u32x4*)(slab + geo.k_off) + lane;
+    const u32x4* Vf = (const u32x4*)(slab + geo.v_off) + lane;
+    const u32x4* Sf = (const u32x4*)(slab + geo.sb_off) + g * EPL;
+    u32x4 kf[NT][KF];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int f = 0; f < KF; ++f) kf[t][f] = __builtin_nontemporal_load(Kf + (t * KF + f) * 64);
+    u32x4 vf[NVF];
+#pragma unroll
+    for (int i = 0; i < NVF; ++i) vf[i] = __builtin_nontemporal_load(Vf + i * 64);
+    u32x4 sbv[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) sbv[e] = Sf[e];
+    __builtin_amdgcn_sched_barrier(0);
+    const u32x4 ones = u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+    // Q_g = sum of q over dim group g, for head n (every accumulator entry)
+    f32x4 qs0 = mfma_f16(ones, qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
+    qs0 = mfma_f16(ones, qf[1], qs0);
+    f32x4 qs1 = mfma_f16(ones, qf[2], f32x4{0.f, 0.f, 0.f, 0.f});
+    qs1 = mfma_f16(ones, qf[3], qs1);
+    const float q0 = qs0[0], q1 = qs1[0];
+    const float q0c = q0 * (QC::OFF * QC::INV_UNIT), q1c = q1 * (QC::OFF * QC::INV_UNIT);
+    // raw_g = K-codes-as-fp16 . Q^T per dim group
+    float pv[EPL];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 r0 = f32x4{0.f, 0.f, 0.f, 0.f}, r1 = r0;
+      r0 = mfma_f16(k_operand<KB>(kf[t], 0), qf[0], r0);
+      r0 = mfma_f16(k_operand<KB>(kf[t], 1), qf[1], r0);
+      r1 = mfma_f16(k_operand<KB>(kf[t], 2), qf[2], r1);
+      r1 = mfma_f16(k_operand<KB>(kf[t], 3), qf[3], r1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4& f = sbv[4 * t + i];
+        const float d0 = __builtin_fmaf(r0[i], QC::INV_UNIT, -q0c);  // sum_d q_d c_d, group 0
+        const float d1 = __builtin_fmaf(r1[i], QC::INV_UNIT, -q1c);
+        float sc = lo_f(f[0]) * d0;
+        sc = __builtin_fmaf(lo_f(f[1]), q0, sc);
+        sc = __builtin_fmaf(hi_f(f[0]), d1, sc);
+        sc = __builtin_fmaf(hi_f(f[1]), q1, sc);
+        pv[4 * t + i] = sc * sl2;
+      }
+    }
+    if (valid < TB) {
+      // tokens past the end: no score, and no stale scale / bias reaches PV
+#pragma unroll
+      for (int e = 0; e < EPL; ++e)
+        if (tok_of(g, e) >= valid) {
+          pv[e] = -INFINITY;
+          sbv[e] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    float mx = pv[0];
+#pragma unroll
+    for (int e = 1; e < EPL; ++e) mx = fmaxf(mx, pv[e]);
+    mx = max_over_groups(mx);
+    float ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      pv[e] = __builtin_amdgcn_exp2f(pv[e] - mx);
+      ps += pv[e];
+    }
+    ps = sum_over_groups(ps);
+    // A operands: P_g = p * v_scale_g and p * v_bias_g per dim group
+    u32x4 pa0[KS2], pa1[KS2], pb0[KS2], pb1[KS2];
+#pragma unroll
+    for (int s2 = 0; s2 < KS2; ++s2)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int e0 = 8 * s2 + 2 * jj, e1 = e0 + 1;
+        const float p0 = pv[e0], p1 = pv[e1];
+        const u32x4 &f0 = sbv[e0], &f1 = sbv[e1];
+        pa0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[2]), p1 * lo_f(f1[2]));
+        pa1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[2]), p1 * hi_f(f1[2]));
+        pb0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[3]), p1 * lo_f(f1[3]));
+        pb1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[3]), p1 * hi_f(f1[3]));
+      }
+    // sum_t P_g and sum_t p v_bias_g, in O's accumulator layout
+    f32x4 ps0 = f32x4{0.f, 0.f, 0.f, 0.f}, ps1 = ps0, vb0 = ps0, vb1 = ps0;
+#pragma unroll
+    for (int s2 = 0; s2 < KS2; ++s2) {
+      ps0 = mfma_f16(pa0[s2], ones, ps0);
+      ps1 = mfma_f16(pa1[s2], ones, ps1);
+      vb0 = mfma_f16(pb0[s2], ones, vb0);
+      vb1 = mfma_f16(pb1[s2], ones, vb1);
+    }
+    // O = P_g . V codes, corrected per dim group
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s2 = 0; s2 < KS2; ++s2) o = mfma_f16(dt < 4 ? pa0[s2] : pa1[s2], v_operand<KB, KS2>(vf, dt, s2), o);
+      const f32x4& psg = dt < 4 ? ps0 : ps1;
+      const f32x4& vbg = dt < 4 ? vb0 : vb1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(o[i] - QC::OFF * psg[i], QC::INV_UNIT, vbg[i]);
+      store_o_tile<G>(s_o[wave], dt, n, g, o);
+    }
+    if (g == 0 && n < G) {
+      s_m[wave][n] = mx;
+      s_l[wave][n] = ps;
+    }
+  } else {
+    store_empty<G>(s_m[wave], s_l[wave], s_o[wave], lane);
+  }
+  __syncthreads();
+  attend_merge<0, G, W>(geo, bi, h, split, s_m, s_l, s_o, out, partials);
+}
+
+// ---------------------------------------------------------------------------
+// export in the MLX layout: kw / vw [n, Hkv, T, D*b/32] uint32 (LSB first),
+// scales / biases [n, Hkv, T, D/64] fp16.  grid (ceil(T/16), Hkv, n)
+// ---------------------------------------------------------------------------
+template <int KB>
+__global__ __launch_bounds__(256) void k_export_q(Geometry geo, SeqBatch sb, int T,
+                                                  uint32_t* __restrict__ kw, uint16_t* __restrict__ ks,
+                                                  uint16_t* __restrict__ kb, uint32_t* __restrict__ vw,
+                                                  uint16_t* __restrict__ vs, uint16_t* __restrict__ vb) {
+  constexpr int WPR = QCode<KB>::WPR;
+  constexpr int EPW = 32 / KB;  // elements per MLX word
+  const int bi = blockIdx.z, h = blockIdx.y;
+  const int tok = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int c = threadIdx.x & 15;
+  if (tok >= T) return;
+  const int seq = sb.ids[bi];
+  const int blk = tok / geo.tb, slot = tok - blk * geo.tb;
+  const int page = block_table(geo, seq)[blk];
+  const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
+  const size_t row = ((size_t)bi * geo.hkv + h) * T + tok;
+  constexpr uint32_t mask = (1u << KB) - 1u;
+#pragma unroll
+  for (int w = 0; w < WPR / 16; ++w) {
+    const int wd = (WPR / 16) * c + w;
+    uint32_t a = 0u, b = 0u;
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) {
+      const int d = wd * EPW + e;
+      int sh;
+      a |= ((uint32_t)(slab[geo.k_off + kq_byte(KB, slot, d, &sh)] >> sh) & mask) << (KB * e);
+      b |= ((uint32_t)(slab[geo.v_off + vq_byte(KB, geo.tb, slot, d, &sh)] >> sh) & mask) << (KB * e);
+    }
+    kw[row * WPR + wd] = a;
+    vw[row * WPR + wd] = b;
+  }
+  if (c < 2) {
+    const uint16_t* f = (const uint16_t*)(slab + geo.sb_off) + 8 * sb_entry(geo.tb, slot);
+    ks[row * 2 + c] = f[c];
+    kb[row * 2 + c] = f[2 + c];
+    vs[row * 2 + c] = f[4 + c];
+    vb[row * 2 + c] = f[6 + c];
+  }
+}
+
+// ===========================================================================
+// launchers
+// ===========================================================================
+hipError_t launch_append_q16(const Geometry& g, const AppendBatch& ab, const void* k,
+                             const void* v, hipStream_t s, Timing* prof) {
+  const dim3 grid(ab.L / 8 + 2, g.hkv, ab.n);
+  const uint16_t *k16 = (const uint16_t*)k, *v16 = (const uint16_t*)v;
+  if (g.kv_bits == 4)
+    launch(k_append_q<4, true>, grid, dim3(128), 0, s, prof, kProfAppend, g, ab, k16, v16,
+             (const uint32_t*)nullptr, (const uint16_t*)nullptr, (const uint16_t*)nullptr,
+             (const uint32_t*)nullptr, (const uint16_t*)nullptr, (const uint16_t*)nullptr);
+  else
+    launch(k_append_q<8, true>, grid, dim3(128), 0, s, prof, kProfAppend, g, ab, k16, v16,
+             (const uint32_t*)nullptr, (const uint16_t*)nullptr, (const uint16_t*)nullptr,
+             (const uint32_t*)nullptr, (const uint16_t*)nullptr, (const uint16_t*)nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_append_quantized(const Geometry& g, const AppendBatch& ab, const uint32_t* kw,
+                                   const void* ks, const void* kb, const uint32_t* vw,
+                                   const void* vs, const void* vb, hipStream_t s, Timing* prof) {
+  const dim3 grid(ab.L / 8 + 2, g.hkv, ab.n);
+  const uint16_t* nul = nullptr;
+  if (g.kv_bits == 4)
+    launch(k_append_q<4, false>, grid, dim3(128), 0, s, prof, kProfAppend, g, ab, nul, nul, kw,
+             (const uint16_t*)ks, (const uint16_t*)kb, vw, (const uint16_t*)vs, (const uint16_t*)vb);
+  else
+    launch(k_append_q<8, false>, grid, dim3(128), 0, s, prof, kProfAppend, g, ab, nul, nul, kw,
+             (const uint16_t*)ks, (const uint16_t*)kb, vw, (const uint16_t*)vs, (const uint16_t*)vb);
+  return hipGetLastError();
+}
+
+hipError_t launch_summary_q(const Geometry& g, const SummaryBatch& sb, int max_count,
+                            hipStream_t s, Timing* prof) {
+  const dim3 grid(max_count, g.hkv, sb.n);
+  if (g.kv_bits == 4) launch(k_summary_q<4>, grid, dim3(128), 0, s, prof, kProfSummary, g, sb);
+  else launch(k_summary_q<8>, grid, dim3(128), 0, s, prof, kProfSummary, g, sb);
+  return hipGetLastError();
+}
+
+template <int TB, bool SEL, int KB>
+static void attend_q_group(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
+                           int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
+                           hipStream_t s, Timing* prof) {
+  constexpr int W = kWaves;
+  const dim3 blk(64 * W);
+  const int kd = kProfAttend;
+  switch (g.group) {
+    case 1: launch(k_attend_q<TB, 1, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    case 2: launch(k_attend_q<TB, 2, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    case 4: launch(k_attend_q<TB, 4, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    case 8: launch(k_attend_q<TB, 8, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    default: launch(k_attend_q<TB, 16, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+  }
+}
+
+template <bool SEL>
+static void attend_q_sel(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
+                         int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
+                         hipStream_t s, Timing* prof) {
+  if (g.kv_bits == 4) {
+    if (g.tb == 64) attend_q_group<64, SEL, 4>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
+    else attend_q_group<32, SEL, 4>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
+  } else {
+    if (g.tb == 64) attend_q_group<64, SEL, 8>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
+    else attend_q_group<32, SEL, 8>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
+  }
+}
+
+hipError_t launch_attend_q(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
+                           const float* scores, bool fused_select, float sl2, void* out,
+                           float* partials, hipStream_t s, Timing* prof) {
+  const dim3 grid(g.nsplit, g.hkv, b.n);
+  const uint16_t* qq = (const uint16_t*)q;
+  uint16_t* oo = (uint16_t*)out;
+  if (fused_select) attend_q_sel<true>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+  else attend_q_sel<false>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+  return hipGetLastError();
+}
+
+hipError_t launch_export_quantized(const Geometry& g, const SeqBatch& b, int T, uint32_t* kw,
+                                   void* ks, void* kb, uint32_t* vw, void* vs, void* vb,
+                                   hipStream_t s) {
+  const dim3 grid((T + 15) / 16, g.hkv, b.n);
+  if (g.kv_bits == 4)
+    hipLaunchKernelGGL(k_export_q<4>, grid, dim3(256), 0, s, g, b, T, kw, (uint16_t*)ks,
+                       (uint16_t*)kb, vw, (uint16_t*)vs, (uint16_t*)vb);
+  else
+    hipLaunchKernelGGL(k_export_q<8>, grid, dim3(256), 0, s, g, b, T, kw, (uint16_t*)ks,
+                       (uint16_t*)kb, vw, (uint16_t*)vs, (uint16_t*)vb);
+  return hipGetLastError();
+}
+
+}  // namespace bsattn

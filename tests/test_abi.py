@@ -61,6 +61,9 @@ def _desc(**kw):
     (dict(dtype=7), "dtype"),
     (dict(max_blocks_per_seq=0), "max_blocks_per_seq"),
     (dict(max_seqs=0), "max_seqs"),
+    (dict(kv_bits=3, dtype=0), "kv_bits"),
+    (dict(kv_bits=4), "fp16"),
+    (dict(kv_bits=8, dtype=0, group_size=32), "group_size"),
 ])
 def test_create_rejects_bad_geometry(bad, msg):
     import bsattn
@@ -80,4 +83,6 @@ def test_null_arguments_are_errors():
     assert L.bsattn_decode(None, None, None, 1, ctypes.c_float(1.0), None, None, None) == -1
     assert L.bsattn_select(None, None, None, 1, None, None) == -1
     assert L.bsattn_cache_info(None, None) == -1
+    assert L.bsattn_append_quantized(None, None, None, None, None, None, None, None, 1, 1, None) == -1
+    assert L.bsattn_export_quantized(None, None, 1, None, None, None, None, None, None, None) == -1
     assert L.bsattn_cache_destroy(None) == 0

@@ -13,49 +13,13 @@ import sys
 import numpy as np
 import pytest
 
-from common import (Workload, from_dev, make_workload, oracle_decode, oracle_summaries,
-                    output_error, to_dev, torch_dtype)
+from common import (Workload, fill, from_dev, log, make_workload, new_cache, oracle_decode,
+                    oracle_summaries, output_error, to_dev, torch_dtype)
 import oracle as O
 
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
-
-
-def log(msg):
-    print(msg, flush=True)
-    sys.stdout.flush()
-
-
-def new_cache(w: Workload, mbps=None, num_pages=0):
-    from bsattn import BlockSparseKVCache
-    mbps = mbps or (max(w.lens) + w.Tb - 1) // w.Tb + 2
-    return BlockSparseKVCache(max_seqs=w.B, num_q_heads=w.Hq, num_kv_heads=w.Hkv, head_dim=w.D,
-                              block_size=w.Tb, dtype=torch_dtype(w.dtype), top_k=w.top_k,
-                              sink_blocks=w.ns, recent_blocks=w.nr, max_blocks_per_seq=mbps,
-                              num_pages=num_pages, device=0)
-
-
-def fill(cache, w: Workload, device, chunk=None, seed=7):
-    """Append every sequence's tokens; with `chunk`, round-robin in random-size
-    chunks so the sequences' pages interleave in the pool."""
-    if chunk is None:
-        for b in range(w.B):
-            if w.lens[b]:
-                cache.append(to_dev(w.keys[b][None], w.dtype, device),
-                             to_dev(w.values[b][None], w.dtype, device), seq_ids=[b])
-        return
-    rng = np.random.default_rng(seed)
-    pos = [0] * w.B
-    while any(pos[b] < w.lens[b] for b in range(w.B)):
-        for b in rng.permutation(w.B):
-            if pos[b] >= w.lens[b]:
-                continue
-            n = int(min(w.lens[b] - pos[b], rng.integers(1, chunk + 1)))
-            k = np.ascontiguousarray(w.keys[b][:, pos[b]:pos[b] + n][None])
-            v = np.ascontiguousarray(w.values[b][:, pos[b]:pos[b] + n][None])
-            cache.append(to_dev(k, w.dtype, device), to_dev(v, w.dtype, device), seq_ids=[int(b)])
-            pos[b] += n
 
 
 def run_and_check(cache, w: Workload, device, check_summaries=True):
