@@ -1,22 +1,35 @@
 """Block-sparse decode attention benchmark on one MI355X.
 
-Workload (the headline configuration): B=8 sequences, Hq=32, Hkv=8, D=128,
-32768 tokens each in 64-token blocks (512 blocks), bf16 K/V ~ N(0,1) with 1%
-of key positions per (sequence, kv head) scaled x8, top-32 + sink + recent
-(34 blocks selected), softmax scale 1/sqrt(128).  36 distinct layer caches
-(one per layer, ~1.1 GB each) so the working set is far above the 256 MB
-Infinity Cache.
+Default workload (the headline configuration, --config c2): B=8 sequences,
+Hq=32, Hkv=8, D=128, 32768 tokens each in 64-token blocks (512 blocks), bf16
+K/V ~ N(0,1) with 1% of key positions per (sequence, kv head) scaled x8,
+top-32 + sink + recent (34 blocks selected), softmax scale 1/sqrt(128).  36
+distinct layer caches (one per layer, ~1.1 GB each) so the working set is far
+above the 256 MB Infinity Cache.
 
-A step = one decode step through all 36 layers: per layer, block scoring +
+A step = one decode step through all layers: per layer, block scoring +
 top-K select + gathered attention (bsattn_decode).  `value` = microseconds
 per layer-step.  Steps are replayed from a HIP graph (captured once) so the
 timing is the GPU's, not the Python launcher's; the eager (ctypes per call)
 figure is reported alongside.
 
-roofline: the gather + attention kernel (k_attend, via bsattn_attend on
-precomputed indices), timed with HIP start/stop events attached to each of
-its dispatches on the launch stream (the library's profiling hook);
-algorithmic bytes per launch = selected K+V bytes + q + out + indices.
+Other workloads (one JSON line each, not the headline):
+  --config c3  int4 affine KV (group 64, fp16 scale / bias): B=4, Hq=32,
+               Hkv=8, 131072 tokens, 64-token blocks, top-64 + sink + recent;
+  --config c5  int8 affine KV, wide GQA: B=8, Hq=64, Hkv=4 (G=16), 262144
+               tokens, 32-token blocks, top-128 + sink + 4 recent; adds the
+               per-head recall of the selection against exact dense
+               attention mass on two sequences of layer 0;
+  --config c4  decode loop with appends: B=32, fp16, lengths U[8192, 65536],
+               pages of the sequences interleaved in the pool, 256 steps of
+               (append one token per sequence, score + top-32 + attend);
+               eager, since every append changes host-side page tables.
+
+roofline: the gather + attention kernel (k_attend / k_attend_q via
+bsattn_attend on precomputed indices), timed with HIP start/stop events
+attached to each of its dispatches on the launch stream (the library's
+profiling hook); algorithmic bytes per launch = selected K+V bytes (codes and
+scales / biases for quantized caches) + q + out + indices.
 cpu_baseline: the CPU oracle (single thread) doing the same layer-step
 (score given summaries, select, attend) on layer 0's data.
 """
@@ -28,17 +41,56 @@ import math
 import os
 import sys
 import time
+from dataclasses import dataclass
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "mlx-swift-lm_amd"))
 
-METRIC = "block-sparse decode attn µs/layer-step + achieved HBM GB/s (% of peak), 32k ctx"
 HBM_PEAK_GBPS = 8000.0
+D = 128
 
-B, HQ, HKV, D, T, TB = 8, 32, 8, 128, 32768, 64
-TOP_K, NS, NR = 32, 1, 1
-LAYERS = 36
-SALIENT = 0.01
+
+@dataclass
+class Config:
+    key: str
+    metric: str
+    B: int
+    HQ: int
+    HKV: int
+    T: int
+    TB: int
+    dtype: str      # "bf16" / "f16"
+    bits: int       # 0: 16-bit K/V; 4 / 8: affine codes
+    top_k: int
+    ns: int
+    nr: int
+    salient: float
+    layers: int
+    traffic_file: str
+
+    @property
+    def G(self):
+        return self.HQ // self.HKV
+
+    @property
+    def bytes_tok(self):
+        """HBM bytes of one token's K + V in one kv head."""
+        if self.bits == 0:
+            return 2 * D * 2
+        return 2 * D * self.bits // 8 + 16   # codes + (k, v) x (scale, bias) x 2 groups fp16
+
+
+CONFIGS = {
+    "c2": Config("c2", "block-sparse decode attn µs/layer-step + achieved HBM GB/s (% of peak), 32k ctx",
+                 8, 32, 8, 32768, 64, "bf16", 0, 32, 1, 1, 0.01, 36,
+                 "k_attend_b8_ctx32k_bf16_traffic.md"),
+    "c3": Config("c3", "block-sparse decode attn µs/layer-step, int4 affine KV, 131k ctx",
+                 4, 32, 8, 131072, 64, "f16", 4, 64, 1, 1, 0.0, 36,
+                 "k_attend_q_b4_ctx128k_int4_traffic.md"),
+    "c5": Config("c5", "block-sparse decode attn µs/layer-step, int8 affine KV, GQA 16, 262k ctx",
+                 8, 64, 4, 262144, 32, "f16", 8, 128, 1, 4, 0.0, 12,
+                 "k_attend_q_b8_ctx256k_int8_traffic.md"),
+}
 
 
 def log(msg):
@@ -48,50 +100,61 @@ def log(msg):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--layers", type=int, default=0, help="layer caches (0: the config's)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-recall", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 256 MiB device copy (a known-traffic dispatch "
                          "for scaling hardware byte counters)")
     return ap.parse_args()
 
 
-def make_layer(layer, dev, torch, bsattn):
+def torch_dtype(torch, cfg):
+    return torch.bfloat16 if cfg.dtype == "bf16" else torch.float16
+
+
+def make_layer(cfg: Config, layer, dev, torch, bsattn):
     g = torch.Generator(device=dev)
-    g.manual_seed(1001 * 1000 + layer)
-    cache = bsattn.BlockSparseKVCache(max_seqs=B, num_q_heads=HQ, num_kv_heads=HKV, head_dim=D,
-                                      block_size=TB, dtype=torch.bfloat16, top_k=TOP_K,
-                                      sink_blocks=NS, recent_blocks=NR,
-                                      max_blocks_per_seq=T // TB + 2, device=dev.index)
-    n_sal = int(round(SALIENT * T))
-    for b in range(B):  # one sequence at a time keeps the temporaries small
-        mult = torch.ones(HKV, T, device=dev)
-        pos = torch.rand(HKV, T, device=dev, generator=g).argsort(dim=1)[:, :n_sal]
-        mult.scatter_(1, pos, 8.0)
-        k = (torch.randn(HKV, T, D, device=dev, generator=g) * mult[..., None]).to(torch.bfloat16)
-        v = torch.randn(HKV, T, D, device=dev, generator=g).to(torch.bfloat16)
+    seeds = {"c2": 1001, "c3": 1003, "c5": 1005}
+    g.manual_seed(seeds[cfg.key] * 1000 + layer)
+    dt = torch_dtype(torch, cfg)
+    cache = bsattn.BlockSparseKVCache(max_seqs=cfg.B, num_q_heads=cfg.HQ, num_kv_heads=cfg.HKV,
+                                      head_dim=D, block_size=cfg.TB, dtype=dt, kv_bits=cfg.bits,
+                                      top_k=cfg.top_k, sink_blocks=cfg.ns, recent_blocks=cfg.nr,
+                                      max_blocks_per_seq=cfg.T // cfg.TB + 2, device=dev.index)
+    n_sal = int(round(cfg.salient * cfg.T))
+    for b in range(cfg.B):  # one sequence at a time keeps the temporaries small
+        if n_sal:
+            mult = torch.ones(cfg.HKV, cfg.T, device=dev)
+            pos = torch.rand(cfg.HKV, cfg.T, device=dev, generator=g).argsort(dim=1)[:, :n_sal]
+            mult.scatter_(1, pos, 8.0)
+            k = (torch.randn(cfg.HKV, cfg.T, D, device=dev, generator=g) * mult[..., None]).to(dt)
+            del mult, pos
+        else:
+            k = torch.randn(cfg.HKV, cfg.T, D, device=dev, generator=g).to(dt)
+        v = torch.randn(cfg.HKV, cfg.T, D, device=dev, generator=g).to(dt)
         cache.append(k[None].contiguous(), v[None].contiguous(), seq_ids=[b])
-        del k, v, mult, pos
-    q = torch.randn(B, HQ, 1, D, device=dev, generator=g).to(torch.bfloat16)
+        del k, v
+    q = torch.randn(cfg.B, cfg.HQ, 1, D, device=dev, generator=g).to(dt)
     return cache, q
 
 
-def algorithmic_bytes(nsel):
-    bytes_tok = 2 * D * 2                      # K + V row, bf16
-    gather = B * HKV * nsel * TB * bytes_tok
-    qo = B * HQ * D * 2 * 2
-    idx = B * HKV * nsel * 4
-    summ = B * HKV * (T // TB) * D * 2
+def algorithmic_bytes(cfg: Config, nsel):
+    gather = cfg.B * cfg.HKV * nsel * cfg.TB * cfg.bytes_tok
+    qo = cfg.B * cfg.HQ * D * 2 * 2
+    idx = cfg.B * cfg.HKV * nsel * 4
+    summ = cfg.B * cfg.HKV * (cfg.T // cfg.TB) * D * 2
     return gather + qo + idx, summ
 
 
-def recorded_traffic():
-    """HBM bytes per k_attend launch from the committed rocprofv3 FETCH_SIZE /
+def recorded_traffic(cfg: Config):
+    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (copy-calibrated); None when it is absent."""
-    path = os.path.join(ROOT, "profiles", "k_attend_b8_ctx32k_bf16_traffic.md")
+    path = os.path.join(ROOT, "profiles", cfg.traffic_file)
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -101,54 +164,101 @@ def recorded_traffic():
     return None, None
 
 
-def cpu_baseline(cache, q, seconds):
+def host16(t, torch, np):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def cpu_baseline(cfg: Config, cache, q, seconds):
     """Oracle layer-step on layer 0's data: per (sequence, kv head) score all
-    candidate summaries, select, attend.  Single thread."""
+    candidate summaries, select, attend (over dequantized blocks for a
+    quantized cache).  Single thread; repeated for about `seconds`."""
     import numpy as np
     import torch
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    k, v = cache.export(list(range(B)))
-    kh = k.view(torch.int16).cpu().numpy().view(np.uint16)
-    vh = v.view(torch.int16).cpu().numpy().view(np.uint16)
-    qh = q.view(torch.int16).cpu().numpy().view(np.uint16).reshape(B, HQ, D)
-    summ = [cache.exportSummaries(b).view(torch.int16).cpu().numpy().view(np.uint16) for b in range(B)]
-    G = HQ // HKV
-    scale = 1.0 / math.sqrt(D)
+    ids = list(range(cfg.B))
+    if cfg.bits:
+        (kw, ks, kb), (vw, vs, vb) = cache.exportQuantized(ids)
+        u32 = lambda t: t.cpu().numpy().view(np.uint32)
+        kq = (u32(kw), host16(ks, torch, np), host16(kb, torch, np))
+        vq = (u32(vw), host16(vs, torch, np), host16(vb, torch, np))
+    else:
+        k, v = cache.export(ids)
+        kh, vh = host16(k, torch, np), host16(v, torch, np)
+    qh = host16(q, torch, np).reshape(cfg.B, cfg.HQ, D)
+    summ = [host16(cache.exportSummaries(b), torch, np) for b in ids]
+    G, scale = cfg.G, 1.0 / math.sqrt(D)
     times = []
     t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(times) < 2:
         t0 = time.perf_counter()
-        for b in range(B):
-            for h in range(HKV):
+        for b in ids:
+            for h in range(cfg.HKV):
                 qq = qh[b, h * G:(h + 1) * G]
-                sc = O.score_blocks(qq, summ[b][h], "bf16")
-                idx, n = O.select(sc, T, TB, NS, NR, TOP_K)
-                O.attend(qq, kh[b, h], vh[b, h], TB, idx[:n], scale, "bf16")
+                sc = O.score_blocks(qq, summ[b][h], cfg.dtype)
+                idx, n = O.select(sc, cfg.T, cfg.TB, cfg.ns, cfg.nr, cfg.top_k)
+                if cfg.bits:
+                    O.attend_q(qq, tuple(a[b, h] for a in kq), tuple(a[b, h] for a in vq), cfg.TB,
+                               cfg.bits, 64, idx[:n], scale)
+                else:
+                    O.attend(qq, kh[b, h], vh[b, h], cfg.TB, idx[:n], scale, cfg.dtype)
         times.append(time.perf_counter() - t0)
     times.sort()
     return times[len(times) // 2] * 1e6, len(times)
 
 
-def main():
-    args = parse()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this benchmark runs on one GPU only: the block-sparse decode "
-                                   "path is a single-GPU kernel set (see DESIGN.md for how it "
-                                   "would shard); run with --gpus 1"}))
-        sys.exit(2)
+def recall_report(cfg: Config, cache, q, idx, seqs):
+    """Per-head recall of the selected blocks against exact dense attention
+    mass (fp64, over the dequantized keys): for each (sequence, kv head) the
+    true top-K candidate blocks by mass summed over the GQA group, recall =
+    |selected ∩ true top-K| / K, captured = selected blocks' share of the
+    mass; per q head, the captured share of its own mass."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    scale = 1.0 / math.sqrt(D)
+    qh = host16(q, torch, np).reshape(cfg.B, cfg.HQ, D)
+    idx = idx.cpu().numpy()
+    nb = -(-cfg.T // cfg.TB)
+    cand = np.arange(cfg.ns, nb - cfg.nr)
+    rec, cap_kv, cap_q = [], [], []
+    for b in seqs:
+        (kw, ks, kb), _ = cache.exportQuantized([b])
+        for h in range(cfg.HKV):
+            keys = O.dequantize(kw[0, h].cpu().numpy().view(np.uint32), host16(ks[0, h], torch, np),
+                                host16(kb[0, h], torch, np), cfg.bits, 64)
+            mass = np.stack([O.block_mass(qh[b, h * cfg.G + g], keys, cfg.TB, scale)
+                             for g in range(cfg.G)])          # [G, nb]
+            sel = idx[b, h][idx[b, h] >= 0]
+            tot = mass.sum(axis=0)
+            true_top = cand[np.argsort(-tot[cand], kind="stable")[:cfg.top_k]]
+            chosen = np.intersect1d(sel, cand)
+            rec.append(len(np.intersect1d(chosen, true_top)) / cfg.top_k)
+            cap_kv.append(tot[sel].sum() / cfg.G)
+            cap_q.extend(mass[:, sel].sum(axis=1).tolist())
+    r = lambda a: round(float(a), 4)
+    return {"sequences": list(seqs), "kv_heads": cfg.HKV, "q_heads_per_kv": cfg.G,
+            "recall_mean": r(np.mean(rec)), "recall_min": r(np.min(rec)),
+            "captured_mass_kv_mean": r(np.mean(cap_kv)), "captured_mass_kv_min": r(np.min(cap_kv)),
+            "captured_mass_q_mean": r(np.mean(cap_q)), "captured_mass_q_min": r(np.min(cap_q)),
+            "note": "mass = exact softmax(q.k * scale) over all tokens of the dequantized keys; "
+                    "true top-K ranks candidate blocks (not sink / recent) by mass summed over "
+                    "the group's q heads"}
+
+
+def bench_layers(args, cfg: Config):
     import torch
     import bsattn
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    L = args.layers
+    L = args.layers or cfg.layers
     t0 = time.time()
-    layers = [make_layer(i, dev, torch, bsattn) for i in range(L)]
+    layers = [make_layer(cfg, i, dev, torch, bsattn) for i in range(L)]
     torch.cuda.synchronize()
-    log(f"[bench] built {L} layer caches in {time.time() - t0:.1f}s "
+    log(f"[bench] {cfg.key}: built {L} layer caches in {time.time() - t0:.1f}s "
         f"({layers[0][0].poolBytes / 2**30:.2f} GiB each)")
     scale = 1.0 / math.sqrt(D)
-    outs = [torch.empty_like(q) for _, q in layers]
 
     def step():
         for (cache, q) in layers:
@@ -195,6 +305,25 @@ def main():
         log("[bench] calibration copy: 256 MiB read + 256 MiB written")
         del src, dst
 
+    # kernel times of one decode layer-step (eager, profiled)
+    for cache, _ in layers:
+        cache.profile(True)
+    for _ in range(max(3, args.steps // 4)):
+        step()
+    torch.cuda.synchronize()
+    kinds = {"score": bsattn._lib.KERNEL_SCORE, "topk": bsattn._lib.KERNEL_TOPK,
+             "attend": bsattn._lib.KERNEL_ATTEND, "combine": bsattn._lib.KERNEL_COMBINE}
+    decode_kernels = {}
+    for name, kind in kinds.items():
+        tot, n = 0.0, 0
+        for cache, _ in layers:
+            ms, c = cache.profileRead(kind)
+            tot, n = tot + ms, n + c
+        if n:
+            decode_kernels[name] = round(tot * 1e3 / n, 3)
+    for cache, _ in layers:
+        cache.profile(False)
+
     # roofline: the gather + attention kernel alone, on precomputed indices.
     # Eager bsattn_attend calls with the library's profiling on: each kernel
     # dispatch carries its own HIP start/stop events on the launch stream.
@@ -219,24 +348,31 @@ def main():
         cache.profile(False)
     attend_us = tot_ms * 1e3 / launches
     combine_us = comb_ms * 1e3 / launches
-    attn_bytes, summ_bytes = algorithmic_bytes(nsel)
+    attn_bytes, summ_bytes = algorithmic_bytes(cfg, nsel)
     achieved = attn_bytes / (attend_us * 1e-6) / 1e9
     layer_bytes = attn_bytes + summ_bytes
     log(f"[bench] attend kernel: {attend_us:.2f} us, {achieved:.0f} GB/s "
         f"({100 * achieved / HBM_PEAK_GBPS:.1f}% of peak); combine {combine_us:.2f} us")
 
+    recall = None
+    if cfg.key == "c5" and not args.no_recall:
+        t0 = time.time()
+        recall = recall_report(cfg, layers[0][0], layers[0][1], idx[0], seqs=[0, 1])
+        log(f"[bench] recall ({time.time() - t0:.0f}s): {recall}")
+
     cpu = None
     if not args.no_cpu and args.cpu_seconds > 0:
-        cpu_us, n = cpu_baseline(layers[0][0], layers[0][1], args.cpu_seconds)
+        cpu_us, n = cpu_baseline(cfg, layers[0][0], layers[0][1], args.cpu_seconds)
         cpu = {"value": round(cpu_us, 1), "unit": "us/layer-step", "cores": 1, "kind": "port",
-               "sample": f"layer 0 of the same workload (8 seq x 8 kv heads x 32768 tokens), "
-                         f"oracle score+select+attend per (seq, kv head) given summaries, "
+               "sample": f"layer 0 of the same workload ({cfg.B} seq x {cfg.HKV} kv heads x {cfg.T} "
+                         f"tokens), oracle score+select+attend per (seq, kv head) given summaries, "
                          f"median of {n} layer-steps, 1 thread"}
         log(f"[bench] cpu oracle: {cpu_us:.0f} us/layer-step")
 
-    traffic, traffic_src = recorded_traffic()
+    traffic, traffic_src = recorded_traffic(cfg)
+    kv = cfg.dtype if cfg.bits == 0 else f"int{cfg.bits} affine, group 64, fp16 scale/bias"
     result = {
-        "metric": METRIC,
+        "metric": cfg.metric,
         "value": round(us_per_layer, 3),
         "unit": "us/layer-step",
         "n_gpus": 1,
@@ -246,22 +382,130 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: torch RNG on device, bf16 K/V ~ N(0,1), 1% of key positions x8, random-init q",
+        "dtype": cfg.dtype if cfg.bits == 0 else f"{cfg.dtype} (int{cfg.bits} KV)",
+        "data": "synthetic: torch RNG on device, K/V ~ N(0,1)"
+                + (f", {cfg.salient:.0%} of key positions x8" if cfg.salient else "")
+                + ", random-init q",
         "config": {"workload": f"block-sparse decode layer-step x{L} distinct layer caches",
-                   "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": T,
-                   "block_size": TB, "top_k": TOP_K, "sink_blocks": NS, "recent_blocks": NR,
-                   "selected_blocks": nsel, "layers": L, "step": "score + top-K + attend"},
+                   "batch": cfg.B, "q_heads": cfg.HQ, "kv_heads": cfg.HKV, "head_dim": D,
+                   "context": cfg.T, "block_size": cfg.TB, "kv": kv, "top_k": cfg.top_k,
+                   "sink_blocks": cfg.ns, "recent_blocks": cfg.nr, "selected_blocks": nsel,
+                   "layers": L, "step": "score + top-K + attend"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "k_attend (gather + attention)", "launch_us": round(attend_us, 3),
+                     "kernel": "k_attend (gather + attention)" if cfg.bits == 0 else
+                               "k_attend_q (gather + fused dequant + attention)",
+                     "launch_us": round(attend_us, 3),
                      "bytes_per_launch": attn_bytes, "combine_us": round(combine_us, 3)},
+        "decode_kernels_us": decode_kernels,
         "layer_step_GBps": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "eager_us_per_layer_step": round(eager_ms * 1e3 / L, 3),
         "cpu_baseline": cpu,
     }
+    if recall is not None:
+        result["recall"] = recall
     print(json.dumps(result), flush=True)
+
+
+def bench_loop(args):
+    """Config 4: decode loop with appends, eager (page tables change every step)."""
+    import numpy as np
+    import torch
+    import bsattn
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, HQ, HKV, TB, K, STEPS = 32, 32, 8, 64, 32, 256
+    steps = args.steps if args.steps != 20 else STEPS
+    rng = np.random.default_rng(4)
+    lens = rng.integers(8192, 65536 + 1, size=B)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4004)
+    mbps = (int(lens.max()) + steps) // TB + 2
+    pages = int(sum(-(-(int(n) + steps) // TB) for n in lens)) + B
+    cache = bsattn.BlockSparseKVCache(max_seqs=B, num_q_heads=HQ, num_kv_heads=HKV, head_dim=D,
+                                      block_size=TB, dtype=torch.float16, top_k=K, sink_blocks=1,
+                                      recent_blocks=1, max_blocks_per_seq=mbps, num_pages=pages,
+                                      device=0)
+    # prefill in random-size chunks, sequences in random order each round, so
+    # every sequence's pages are scattered through the pool
+    t0 = time.time()
+    pos = np.zeros(B, np.int64)
+    while (pos < lens).any():
+        for b in rng.permutation(B):
+            if pos[b] >= lens[b]:
+                continue
+            n = int(min(lens[b] - pos[b], rng.integers(256, 4096)))
+            k = torch.randn(1, HKV, n, D, device=dev, generator=g).half()
+            v = torch.randn(1, HKV, n, D, device=dev, generator=g).half()
+            cache.append(k, v, seq_ids=[int(b)])
+            pos[b] += n
+    torch.cuda.synchronize()
+    log(f"[bench] c4: prefilled {B} sequences ({int(lens.sum())} tokens) in {time.time() - t0:.1f}s")
+    kn = torch.randn(steps + args.warmup, B, HKV, 1, D, device=dev, generator=g).half()
+    vn = torch.randn(steps + args.warmup, B, HKV, 1, D, device=dev, generator=g).half()
+    qs = torch.randn(steps + args.warmup, B, HQ, 1, D, device=dev, generator=g).half()
+    scale = 1.0 / math.sqrt(D)
+    for i in range(args.warmup):
+        cache.append(kn[i], vn[i])
+        cache.decode(qs[i], scale)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, args.warmup + steps):
+        cache.append(kn[i], vn[i])
+        cache.decode(qs[i], scale)
+    torch.cuda.synchronize()
+    us_step = (time.perf_counter() - t0) * 1e6 / steps
+    # kernel time per step: the same steps again (trimmed back first), profiled
+    cache.trim(steps, list(range(B)))
+    cache.profile(True)
+    for i in range(args.warmup, args.warmup + steps):
+        cache.append(kn[i], vn[i])
+        cache.decode(qs[i], scale)
+    torch.cuda.synchronize()
+    kern = {}
+    total = 0.0
+    names = {"append": bsattn._lib.KERNEL_APPEND, "summary": bsattn._lib.KERNEL_SUMMARY,
+             "score": bsattn._lib.KERNEL_SCORE, "topk": bsattn._lib.KERNEL_TOPK,
+             "attend": bsattn._lib.KERNEL_ATTEND, "combine": bsattn._lib.KERNEL_COMBINE}
+    for name, kind in names.items():
+        ms, n = cache.profileRead(kind)
+        if n:
+            kern[name] = {"us_per_step": round(ms * 1e3 / steps, 3), "launches": n}
+            total += ms * 1e3 / steps
+    cache.profile(False)
+    log(f"[bench] c4: {us_step:.2f} us/step eager, kernels {total:.2f} us/step")
+    nsel = K + 2
+    gather = int(B * HKV * nsel * TB * 2 * D * 2)
+    result = {
+        "metric": "block-sparse decode loop with appends µs/step, B=32 variable lengths",
+        "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic: torch RNG on device, K/V/q ~ N(0,1); lengths from numpy seed 4",
+        "config": {"workload": "decode loop: append 1 token per sequence, score + top-K + attend",
+                   "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
+                   "lengths": [int(x) for x in lens], "block_size": TB, "top_k": K,
+                   "sink_blocks": 1, "recent_blocks": 1, "pages": pages,
+                   "timing": "eager wall clock per step (ctypes launches included)"},
+        "kernels_us_per_step": kern, "kernel_us_per_step_total": round(total, 3),
+        "gather_bytes_per_step": gather,
+        "gather_GBps_at_kernel_time": round(gather / (total * 1e-6) / 1e9, 1) if total else None,
+    }
+    print(json.dumps(result), flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU only: the block-sparse decode "
+                                   "path is a single-GPU kernel set (see DESIGN.md for how it "
+                                   "would shard); run with --gpus 1"}))
+        sys.exit(2)
+    if args.config == "c4":
+        bench_loop(args)
+    else:
+        bench_layers(args, CONFIGS[args.config])
 
 
 if __name__ == "__main__":
