@@ -54,6 +54,7 @@ struct bsattn_cache {
   float* scores = nullptr;    // [max_seqs][hkv][mbps]
   int32_t* idx_ws = nullptr;  // [max_seqs][hkv][nsel_max]
   float* partials = nullptr;  // [max_seqs][hq][nsplit][D + 2]
+  float* err_ws = nullptr;    // [max_seqs][hkv][mfma_err_stride]: MFMA score bounds
   std::vector<int32_t> len;
   std::vector<std::vector<int32_t>> pages;
   std::vector<int32_t> free_pages;  // stack; back() is handed out next
@@ -298,6 +299,7 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
     (void)hipFree(c->scores);
     (void)hipFree(c->idx_ws);
     (void)hipFree(c->partials);
+    (void)hipFree(c->err_ws);
     delete c;
     return code;
   };
@@ -311,6 +313,8 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
     return cleanup(hip_fail(e, "hipMalloc(indices)"));
   if ((e = hipMalloc((void**)&c->partials, (size_t)d.max_seqs * g.hq * g.nsplit * (kHeadDim + 2) * 4)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMalloc(partials)"));
+  if ((e = hipMalloc((void**)&c->err_ws, (size_t)d.max_seqs * g.hkv * mfma_err_stride(g) * 4)) != hipSuccess)
+    return cleanup(hip_fail(e, "hipMalloc(bounds)"));
   // zeroed pages: never-written token slots hold finite values
   if ((e = hipMemset(g.pool, 0, c->pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(pool)"));
   if ((e = hipMemset(g.summ, 0, c->summ_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(summaries)"));
@@ -335,6 +339,7 @@ int bsattn_cache_destroy(bsattn_cache* c) {
   (void)hipFree(c->scores);
   (void)hipFree(c->idx_ws);
   (void)hipFree(c->partials);
+  (void)hipFree(c->err_ws);
   delete c;
   return BSATTN_OK;
 }
@@ -440,17 +445,18 @@ static int do_select(bsattn_cache* c, const void* q, const std::vector<int32_t>&
   for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
     SeqBatch b{};
     b.n = std::min(kMaxBatch, n - i0);
-    int max_chunks = 0;
+    int max_nc = 0;
     for (int i = 0; i < b.n; ++i) {
       b.ids[i] = seqs[i0 + i];
-      max_chunks = std::max(max_chunks, select_chunks(c->geo, c->len[b.ids[i]]));
+      max_nc = std::max(max_nc, candidates(c->geo, c->len[b.ids[i]]));
     }
     const uint16_t* qq = (const uint16_t*)q + (size_t)i0 * c->geo.hq * kHeadDim;
     float* sc = c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps;
     int32_t* io = idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max;
     Timing tm[kProfKinds];
     Timing* prof = prof_slots(c, s, tm);
-    hipError_t e = launch_select(c->geo, b, qq, sc, io, max_chunks, s, prof);
+    float* err = c->err_ws + (size_t)i0 * c->geo.hkv * mfma_err_stride(c->geo);
+    hipError_t e = launch_select(c->geo, b, qq, sc, err, io, max_nc, s, prof);
     prof_collect(c, prof);
     if (e != hipSuccess) return hip_fail(e, "select launch");
   }
@@ -522,10 +528,10 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
     SeqBatch b{};
     b.n = std::min(kMaxBatch, n - i0);
-    int max_chunks = 0;
+    int max_nc = 0;
     for (int i = 0; i < b.n; ++i) {
       b.ids[i] = seqs[i0 + i];
-      max_chunks = std::max(max_chunks, select_chunks(c->geo, c->len[b.ids[i]]));
+      max_nc = std::max(max_nc, candidates(c->geo, c->len[b.ids[i]]));
     }
     const size_t qoff = (size_t)i0 * c->geo.hq * kHeadDim * 2;
     Timing tm[kProfKinds];
@@ -533,7 +539,7 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
     hipError_t e = launch_decode(c->geo, b, (const char*)q + qoff,
                                  c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps,
                                  idx_out ? idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max : nullptr,
-                                 max_chunks, scale, (char*)out + qoff,
+                                 max_nc, scale, (char*)out + qoff,
                                  c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2),
                                  s, prof);
     prof_collect(c, prof);

@@ -98,6 +98,33 @@ __device__ __forceinline__ uint32_t score_key(float s) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+template <int DT>
+__device__ __forceinline__ void unpack8(const u32x4 raw, float* out) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    out[e] = to_f32<DT>((uint16_t)((e & 1) ? (raw[e >> 1] >> 16) : (raw[e >> 1] & 0xFFFFu)));
+}
+
+// Candidates are ranked only when they outnumber top_k.
+__host__ __device__ inline bool ranked_select(const Geometry& g, int nc) {
+  return nc > g.top_k && g.top_k > 0;
+}
+
+// Canonical dot product of one 128-dim pair held by 16 consecutive lanes
+// (lane c = chunk c: dims 8c .. 8c+7): left fold of the chunk's 8 products,
+// then the pairwise tree over chunks as an xor butterfly 1, 2, 4, 8.  Every
+// one of the 16 lanes returns the same bits.
+__device__ __forceinline__ float canonical_dot16(const float* a, const float* b) {
+  float acc = __fmul_rn(a[0], b[0]);
+#pragma unroll
+  for (int e = 1; e < 8; ++e) acc = __fadd_rn(acc, __fmul_rn(a[e], b[e]));
+  acc = __fadd_rn(acc, __shfl_xor(acc, 1, 64));
+  acc = __fadd_rn(acc, __shfl_xor(acc, 2, 64));
+  acc = __fadd_rn(acc, __shfl_xor(acc, 4, 64));
+  acc = __fadd_rn(acc, __shfl_xor(acc, 8, 64));
+  return acc;
+}
+
 // ---------------------------------------------------------------------------
 // wave-level top-K of one (sequence, kv head): the same selection as the
 // oracle (K largest keys, ties to the lower index), computed by one wave with

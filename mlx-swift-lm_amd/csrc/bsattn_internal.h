@@ -91,10 +91,18 @@ hipError_t launch_attend_q(const Geometry& g, const SeqBatch& b, const void* q, 
                            float* partials, hipStream_t s, Timing* prof);
 hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
                           hipStream_t s, Timing* prof);
-int select_chunks(const Geometry& g, int len);
-// scoring workgroups per (sequence, kv head) for `len` tokens (0: no ranking)
+// candidate blocks (neither sink nor recent) of a sequence of `len` tokens
+int candidates(const Geometry& g, int len);
+// scoring + top-K for a batch whose largest candidate count is max_nc;
+// err: bound workspace of mfma_err_stride(g) floats per (sequence, kv head)
 hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                         int32_t* idx, int max_chunks, hipStream_t s, Timing* prof);
+                         float* err, int32_t* idx, int max_nc, hipStream_t s, Timing* prof);
+int mfma_err_stride(const Geometry& g);
+// block-wide selection (bsattn_select.hip); scores_ready: exact scores are
+// in `scores`, else (group >= 8) MFMA scores with the band rescored exactly
+hipError_t launch_select_large(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                               float* err, int max_nc, int32_t* idx, hipStream_t s, Timing* prof,
+                               bool scores_ready);
 hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q,
                          const int32_t* idx, float scale, void* out, float* partials,
                          hipStream_t s, Timing* prof);
@@ -103,7 +111,7 @@ hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q,
 // fused_select_limit(top_k) candidate blocks.  idx_out may be null.
 int fused_select_limit(int top_k);
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                         int32_t* idx_out, int max_chunks, float scale, void* out,
+                         int32_t* idx_out, int max_nc, float scale, void* out,
                          float* partials, hipStream_t s, Timing* prof);
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out,
                          void* v_out, hipStream_t s);

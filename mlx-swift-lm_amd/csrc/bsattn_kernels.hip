@@ -22,29 +22,6 @@
 
 namespace bsattn {
 
-// 256-thread inclusive scan; s_tmp holds 4 ints.
-__device__ __forceinline__ int block_scan_incl(int v, int* s_tmp, int* total) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  if (lane == 63) s_tmp[w] = x;
-  __syncthreads();
-  int off = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int t = s_tmp[i];
-    off += (i < w) ? t : 0;
-    tot += t;
-  }
-  __syncthreads();
-  if (total) *total = tot;
-  return off + x;
-}
-
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_patch(int32_t* meta, PatchBatch pb) {
   const int t = threadIdx.x;
@@ -109,17 +86,6 @@ __global__ __launch_bounds__(128) void k_summary(Geometry geo, SummaryBatch sb) 
 // ---------------------------------------------------------------------------
 constexpr int kSelChunk = 64;
 
-template <int DT>
-__device__ __forceinline__ void unpack8(const u32x4 raw, float* out) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    out[e] = to_f32<DT>((uint16_t)((e & 1) ? (raw[e >> 1] >> 16) : (raw[e >> 1] & 0xFFFFu)));
-}
-
-__host__ __device__ inline bool ranked_select(const Geometry& g, int nc) {
-  return nc > g.top_k && g.top_k > 0;
-}
-
 template <int DT, int G>
 __global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
                                                const uint16_t* __restrict__ q,
@@ -157,13 +123,7 @@ __global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
       float best = 0.0f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float acc = __fmul_rn(qv[g][0], sv[0]);
-#pragma unroll
-        for (int e = 1; e < 8; ++e) acc = __fadd_rn(acc, __fmul_rn(qv[g][e], sv[e]));
-        acc = __fadd_rn(acc, __shfl_xor(acc, 1, 64));
-        acc = __fadd_rn(acc, __shfl_xor(acc, 2, 64));
-        acc = __fadd_rn(acc, __shfl_xor(acc, 4, 64));
-        acc = __fadd_rn(acc, __shfl_xor(acc, 8, 64));
+        const float acc = canonical_dot16(qv[g], sv);
         if (g == 0 || acc > best) best = acc;
       }
       if (c == 0) srow[j] = best;
@@ -172,96 +132,26 @@ __global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
 }
 
 // ---------------------------------------------------------------------------
-// top-K select: one workgroup per (kv head, sequence).  Up to
-// 64 * kSelKeysPerLane candidates: wave_topk.  More: MSB-first radix select
-// (4 x 8 bits) of the K-th largest key over the workgroup, ties by ascending
-// index, then compaction of forced + chosen blocks in ascending order.
-// dynamic LDS: keys[mbps] (u32) + flags[mbps] (u8).  grid (Hkv, n)
+// top-K select for batches whose candidate sets fit one wave (at most
+// 64 * kSelKeysPerLane candidates, top_k <= kSelMaxK): one workgroup per
+// (kv head, sequence), one wave selects.  Larger sets go to k_select
+// (bsattn_select.hip).  grid (Hkv, n)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_topk(Geometry geo, SeqBatch sb,
-                                              const float* __restrict__ scores,
-                                              int32_t* __restrict__ idx_out) {
-  extern __shared__ uint32_t smem[];
-  __shared__ uint32_t hist[256];
-  __shared__ int s_tmp[4];
-  __shared__ int s_sel[2];
-  const int tid = threadIdx.x;
+__global__ __launch_bounds__(64) void k_topk(Geometry geo, SeqBatch sb,
+                                             const float* __restrict__ scores,
+                                             int32_t* __restrict__ idx_out) {
+  __shared__ int s_sel[kSelMaxK];
+  const int lane = threadIdx.x;
   const int h = blockIdx.x, bi = blockIdx.y;
   const int seq = sb.ids[bi];
   const int len = geo.meta[seq];
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
-  const int c0 = geo.ns, c1 = nb - geo.nr, nc = c1 - c0;
+  const int c0 = geo.ns, nc = nb - geo.nr - c0;
   const bool ranked = ranked_select(geo, nc);
-  const float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
   int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
-  if (ranked && nc <= 64 * kSelKeysPerLane && geo.top_k <= kSelMaxK) {
-    // one wave selects; no workgroup barriers inside the selection
-    __shared__ int s_sel[kSelMaxK];
-    if (tid < 64) wave_topk(srow, nullptr, c0, nc, geo.top_k, s_sel, nullptr);
-    __syncthreads();
-    for (int p = tid; p < geo.nsel_max; p += 256)
-      out[p] = selected_block(p, nb, true, geo.ns, geo.nr, geo.top_k, s_sel);
-    return;
-  }
-  uint32_t* keys = smem;
-  uint8_t* flags = (uint8_t*)(smem + geo.mbps);
-  if (ranked)
-    for (int i = tid; i < nc; i += 256) keys[i] = score_key(srow[c0 + i]);
-  for (int j = tid; j < nb; j += 256)
-    flags[j] = (j < geo.ns || j >= nb - geo.nr || (nc > 0 && !ranked)) ? 1 : 0;
-  __syncthreads();
-  if (ranked) {
-    uint32_t prefix = 0u, mask = 0u;
-    int krem = geo.top_k;
-    for (int sh = 24; sh >= 0; sh -= 8) {
-      hist[tid] = 0u;
-      __syncthreads();
-      for (int i = tid; i < nc; i += 256) {
-        const uint32_t key = keys[i];
-        if (((key ^ prefix) & mask) == 0u) atomicAdd(&hist[(key >> sh) & 255u], 1u);
-      }
-      __syncthreads();
-      const int cnt = (int)hist[255 - tid];
-      const int incl = block_scan_incl(cnt, s_tmp, nullptr);
-      if (incl >= krem && incl - cnt < krem) {
-        s_sel[0] = 255 - tid;
-        s_sel[1] = incl - cnt;
-      }
-      __syncthreads();
-      prefix |= (uint32_t)s_sel[0] << sh;
-      mask |= 0xFFu << sh;
-      krem -= s_sel[1];
-      __syncthreads();
-    }
-    const uint32_t tau = prefix;
-    const int per = (nc + 255) / 256;
-    const int lo = min(tid * per, nc), hi = min(lo + per, nc);
-    int nties = 0;
-    for (int i = lo; i < hi; ++i) {
-      const uint32_t key = keys[i];
-      if (key > tau) flags[c0 + i] = 1;
-      else if (key == tau) ++nties;
-    }
-    int rank = block_scan_incl(nties, s_tmp, nullptr) - nties;
-    for (int i = lo; i < hi; ++i)
-      if (keys[i] == tau) {
-        if (rank < krem) flags[c0 + i] = 1;
-        ++rank;
-      }
-  }
-  __syncthreads();
-  const int per = (nb + 255) / 256;
-  const int lo = min(tid * per, nb), hi = min(lo + per, nb);
-  int cnt = 0;
-  for (int j = lo; j < hi; ++j) cnt += flags[j];
-  int total = 0;
-  int pos = block_scan_incl(cnt, s_tmp, &total) - cnt;
-  for (int j = lo; j < hi; ++j)
-    if (flags[j]) {
-      if (pos < geo.nsel_max) out[pos] = j;
-      ++pos;
-    }
-  for (int p = total + tid; p < geo.nsel_max; p += 256) out[p] = -1;
+  if (ranked) wave_topk(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, nullptr, c0, nc, geo.top_k, s_sel, nullptr);
+  for (int p = lane; p < geo.nsel_max; p += 64)
+    out[p] = selected_block(p, nb, ranked, geo.ns, geo.nr, geo.top_k, s_sel);
 }
 
 // ---------------------------------------------------------------------------
@@ -525,24 +415,34 @@ static void score_dispatch(const Geometry& g, dim3 grid, const SeqBatch& b, cons
   }
 }
 
-int select_chunks(const Geometry& g, int len) {
+int candidates(const Geometry& g, int len) {
   const int nb = len > 0 ? (len + g.tb - 1) / g.tb : 0;
-  const int nc = nb - g.nr - g.ns;
-  return ranked_select(g, nc) ? (nc + kSelChunk - 1) / kSelChunk : 0;
+  return nb - g.nr - g.ns;
+}
+
+static bool wave_selectable(const Geometry& g, int max_nc) {
+  return max_nc <= 64 * kSelKeysPerLane && g.top_k <= kSelMaxK;
+}
+
+// exact (canonical) scores of every ranked candidate
+static hipError_t score_exact(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                              int max_nc, hipStream_t s, Timing* prof) {
+  if (!ranked_select(g, max_nc)) return hipSuccess;
+  dim3 grid((max_nc + kSelChunk - 1) / kSelChunk, g.hkv, b.n);
+  if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s, prof);
+  else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s, prof);
+  return hipGetLastError();
 }
 
 hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                         int32_t* idx, int max_chunks, hipStream_t s, Timing* prof) {
-  if (max_chunks > 0) {
-    dim3 grid(max_chunks, g.hkv, b.n);
-    if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s, prof);
-    else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s, prof);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
-  const size_t lds = (size_t)g.mbps * 5;
-  launch(k_topk, dim3(g.hkv, b.n), dim3(256), lds, s, prof, kProfTopk, g, b, (const float*)scores,
-         idx);
+                         float* err, int32_t* idx, int max_nc, hipStream_t s, Timing* prof) {
+  const bool small = wave_selectable(g, max_nc);
+  if (!small && g.group >= 8)  // MFMA scores + exact rescoring of the band
+    return launch_select_large(g, b, q, scores, err, max_nc, idx, s, prof, false);
+  hipError_t e = score_exact(g, b, q, scores, max_nc, s, prof);
+  if (e != hipSuccess) return e;
+  if (!small) return launch_select_large(g, b, q, scores, err, max_nc, idx, s, prof, true);
+  launch(k_topk, dim3(g.hkv, b.n), dim3(64), 0, s, prof, kProfTopk, g, b, (const float*)scores, idx);
   return hipGetLastError();
 }
 
@@ -599,15 +499,10 @@ hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q, co
 int fused_select_limit(int top_k) { return top_k <= kSelMaxK ? 64 * kSelKeysPerLane : 0; }
 
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                         int32_t* idx_out, int max_chunks, float scale, void* out,
+                         int32_t* idx_out, int max_nc, float scale, void* out,
                          float* partials, hipStream_t s, Timing* prof) {
-  if (max_chunks > 0) {
-    dim3 grid(max_chunks, g.hkv, b.n);
-    if (g.dtype == 0) score_dispatch<0>(g, grid, b, (const uint16_t*)q, scores, s, prof);
-    else score_dispatch<1>(g, grid, b, (const uint16_t*)q, scores, s, prof);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
+  hipError_t e = score_exact(g, b, q, scores, max_nc, s, prof);
+  if (e != hipSuccess) return e;
   return attend_impl<true>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
 }
 

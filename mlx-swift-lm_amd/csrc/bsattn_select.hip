@@ -1,0 +1,467 @@
+// bsattn_select.hip -- block selection for large candidate sets (more than
+// one wave's worth of candidates) and wide GQA groups.
+//
+// k_select: one 1024-thread workgroup per (kv head, sequence).  Thread t owns
+// the contiguous candidates [t*per, t*per + per) (per <= 12) with their keys
+// in registers; the K-th largest key is found bit by bit from the top, each
+// step counting keys >= the candidate prefix with ballots and one workgroup
+// barrier (the counts of the 16 waves meet in double-buffered LDS slots), and
+// stops early once exactly K keys are >= the prefix.  Ties at the K-th key go
+// to the lowest indices (a workgroup scan over the owners' segments), and
+// the output is compacted in ascending block order.
+//
+// Wide groups (G >= 8): the block scores are first computed with MFMA
+// (k_score_mfma), which does not reproduce the canonical summation order.
+// Each approximate score s~ comes with a bound e >= |s~ - s| (s = canonical
+// score), so with s_K, s_K+1 the K-th and (K+1)-th largest approximate
+// scores, a block with s~ - e > s_K+1 + e is certainly selected, one with
+// s~ + e < s_K - e certainly is not, and only the blocks in between (the
+// band) are rescored in the canonical order; the remaining places go to the
+// best of the band by (exact score, index).  The selection is therefore the
+// canonical one, bit for bit.
+//
+// Bound: products of fp16 / bf16 pairs are exact or within one rounding in
+// fp32; the canonical order adds 11 roundings and any fp32 accumulation of
+// 128 products at most 128 more, so |s~ - s| <= 2^-14 * A with
+// A = max over the group of sum |q_d| |k_d| (computed by an MFMA on the
+// magnitudes).  Inputs below fp16's normal range that an MFMA might flush
+// change a dot by at most 2^-14 * (||q||_1 + ||k||_1), which is added.  The
+// bound used per (sequence, kv head) is the maximum over its blocks, widened
+// by 2^-8 of itself to cover the roundings of the comparisons.
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bsattn_device.h"
+
+namespace bsattn {
+
+constexpr int kMfmaChunk = 256;   // candidate blocks per MFMA-scoring workgroup
+constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kSelPer = 12;       // candidates per thread: mbps <= 12288
+
+// inverse of score_key; key 0 (NaN) -> -inf
+__device__ __forceinline__ float key_value(uint32_t key) {
+  if (key == 0u) return -INFINITY;
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
+__device__ __forceinline__ u32x4 abs16x8(u32x4 v) {
+  return u32x4{v[0] & 0x7FFF7FFFu, v[1] & 0x7FFF7FFFu, v[2] & 0x7FFF7FFFu, v[3] & 0x7FFF7FFFu};
+}
+
+__device__ __forceinline__ float max16(float x) {  // over the 16 lanes of a row
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA scoring (G >= 8): workgroup (chunk, kv head, sequence) handles
+// kMfmaChunk candidate blocks; each wave takes 16-block tiles:
+//   S^T[block][head] = Summ[block][:] . Q[head][:]   (A = summary rows, B = Q^T)
+// plus the same product on magnitudes and Summ . 1 on magnitudes for the
+// bound.  Writes the approximate score (max over the group) of every
+// candidate and the chunk's bound to err[seq row][chunk].
+// grid (chunks, Hkv, n)
+// ---------------------------------------------------------------------------
+template <int DT, int G>
+__global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
+                                                    const uint16_t* __restrict__ q,
+                                                    float* __restrict__ scores,
+                                                    float* __restrict__ err, int err_stride) {
+  __shared__ float s_e[4];
+  const int chunk = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int seq = sb.ids[bi];
+  const int len = geo.meta[seq];
+  const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
+  const int c0 = geo.ns, c1 = nb - geo.nr;
+  float* erow = err + ((size_t)bi * geo.hkv + h) * err_stride;
+  if (!ranked_select(geo, c1 - c0)) {
+    if (threadIdx.x == 0) erow[chunk] = 0.0f;
+    return;
+  }
+  u32x4 qf[4], qa[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) qf[s] = qa[s] = u32x4{0u, 0u, 0u, 0u};
+  if (n < G) {
+    const uint16_t* src = q + ((size_t)bi * geo.hq + h * G + n) * kHeadDim + 8 * g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      qf[s] = *(const u32x4*)(src + 32 * s);
+      qa[s] = abs16x8(qf[s]);
+    }
+  }
+  constexpr uint32_t one2 = DT == 0 ? 0x3C003C00u : 0x3F803F80u;
+  const u32x4 ones = u32x4{one2, one2, one2, one2};
+  // ||q_head||_1 (column n of ones . |Q|^T), max over the group
+  f32x4 q1 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) q1 = mfma16x16x32<DT>(ones, qa[s], q1);
+  const float q1max = max16(q1[0]);
+  float emax = 0.0f;
+  float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
+  const uint16_t* sbase = summary_row(geo, seq, h, 0) + 8 * g;
+  const int jbase = c0 + chunk * kMfmaChunk;
+#pragma unroll 1
+  for (int it = 0; it < kMfmaChunk / 64; ++it) {
+    const int j0 = jbase + (4 * it + wave) * 16;
+    if (j0 >= c1) break;
+    // rows past the candidates (still inside the table) are read, not used
+    const int jr = min(j0 + n, geo.mbps - 1);
+    const uint16_t* row = sbase + (size_t)jr * kHeadDim;
+    u32x4 af[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) af[s] = *(const u32x4*)(row + 32 * s);
+    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f}, a = d, k1 = d;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4 ab = abs16x8(af[s]);
+      d = mfma16x16x32<DT>(af[s], qf[s], d);
+      a = mfma16x16x32<DT>(ab, qa[s], a);
+      k1 = mfma16x16x32<DT>(ab, ones, k1);
+    }
+    // lane (head n, group g), entry i: block j0 + 4g + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = j0 + 4 * g + i;
+      float sc = n < G ? d[i] : -INFINITY;
+      const bool bad = n < G && (__builtin_isnan(sc) || __builtin_isinf(sc));
+      sc = max16(sc);
+      const float am = max16(a[i]);
+      // any non-finite head score makes the block's approximate score NaN
+      const bool any_bad = __ballot(bad) & (0xFFFFull << (16 * g));
+      if (j < c1) {
+        if (n == 0) srow[j] = any_bad ? __builtin_nanf("") : sc;
+        if (!any_bad) emax = fmaxf(emax, am + k1[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) emax = fmaxf(emax, __shfl_xor(emax, o, 64));
+  if (lane == 0) s_e[wave] = emax;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    erow[chunk] = 0x1p-14f * (fmaxf(fmaxf(s_e[0], s_e[1]), fmaxf(s_e[2], s_e[3])) + q1max);
+}
+
+// ---------------------------------------------------------------------------
+// workgroup primitives (1024 threads)
+// ---------------------------------------------------------------------------
+// keys >= cand over the workgroup; one barrier; s_cnt double-buffered by
+// the caller's parity (a slot is rewritten only after every wave has passed
+// the barrier that follows its last read)
+__device__ __forceinline__ int wg_count_ge(const uint32_t (&kr)[kSelPer], int per, uint32_t cand,
+                                           int (*s_cnt)[kSelWaves], int& parity) {
+  uint64_t m[kSelPer];
+#pragma unroll
+  for (int p = 0; p < kSelPer; ++p) m[p] = (p < per) ? __ballot(kr[p] >= cand) : 0ull;
+  __builtin_amdgcn_sched_barrier(0);
+  int c = 0;
+#pragma unroll
+  for (int p = 0; p < kSelPer; ++p) c += __popcll(m[p]);
+  if ((threadIdx.x & 63) == 0) s_cnt[parity][threadIdx.x >> 6] = c;
+  __syncthreads();
+  int tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) tot += s_cnt[parity][w];
+  parity ^= 1;
+  return tot;
+}
+
+// exclusive prefix sum of v over the workgroup in thread order; *total
+__device__ __forceinline__ int wg_scan_excl(int v, int* s_tmp, int* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  __syncthreads();  // s_tmp may still be read by an earlier call
+  if (lane == 63) s_tmp[w] = x;
+  __syncthreads();
+  int off = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kSelWaves; ++i) {
+    const int t = s_tmp[i];
+    off += (i < w) ? t : 0;
+    tot += t;
+  }
+  *total = tot;
+  return off + x - v;
+}
+
+__device__ __forceinline__ uint32_t wg_reduce_u32(uint32_t v, bool is_max, uint32_t* s_red) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_xor(v, o, 64);
+    v = is_max ? max(v, y) : min(v, y);
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t r = s_red[0];
+#pragma unroll
+  for (int i = 1; i < kSelWaves; ++i) r = is_max ? max(r, s_red[i]) : min(r, s_red[i]);
+  return r;
+}
+
+// K-th largest key over the workgroup's keys (kr[p], p < per; padding keys
+// are 0 and never counted, real keys may be 0).  Returns tau with
+// count(>= tau) >= K; *exact is set when exactly K keys are >= tau (then
+// those K keys are the selection, whatever tau is); otherwise tau is the
+// K-th largest key itself (0 when fewer than K keys are nonzero).
+__device__ __forceinline__ uint32_t wg_kth_key(const uint32_t (&kr)[kSelPer], int per, int K,
+                                               int (*s_cnt)[kSelWaves], int& parity,
+                                               bool* exact, int* cnt_at_tau) {
+  uint32_t tau = 0u;
+  int cnt = 0;
+  *exact = false;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    const int c = wg_count_ge(kr, per, cand, s_cnt, parity);
+    if (c >= K) {
+      tau = cand;
+      cnt = c;
+      if (c == K) {
+        *exact = true;
+        break;
+      }
+    }
+  }
+  *cnt_at_tau = cnt;
+  return tau;
+}
+
+// ---------------------------------------------------------------------------
+// block-wide selection; grid (Hkv, n), 1024 threads.
+// BAND: scores are the approximate MFMA scores with bounds in err (see the
+// top of this file); dynamic LDS then holds the band (u32 per candidate).
+// ---------------------------------------------------------------------------
+template <int DT, int G, bool BAND>
+__global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch sb,
+                                                        const uint16_t* __restrict__ q,
+                                                        const float* __restrict__ scores,
+                                                        const float* __restrict__ err,
+                                                        int err_stride, int err_count,
+                                                        int32_t* __restrict__ idx_out) {
+  extern __shared__ uint32_t s_band[];
+  __shared__ int s_cnt[2][kSelWaves];
+  __shared__ int s_tmp[kSelWaves];
+  __shared__ uint32_t s_red[kSelWaves];
+  __shared__ __align__(16) uint32_t s_q[BAND ? G * kHeadDim / 2 : 4];
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x, bi = blockIdx.y;
+  const int seq = sb.ids[bi];
+  const int len = geo.meta[seq];
+  const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
+  const int c0 = geo.ns, nc = nb - geo.nr - c0, K = geo.top_k;
+  int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
+  if (!ranked_select(geo, nc)) {  // every block is kept
+    for (int p = tid; p < geo.nsel_max; p += kSelThreads) out[p] = p < nb ? p : -1;
+    return;
+  }
+  const float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
+  const int per = (nc + kSelThreads - 1) / kSelThreads;
+  const int i0 = tid * per;  // this thread's candidates: c0 + i0 + p, p < per, i0 + p < nc
+  uint32_t kr[kSelPer];
+#pragma unroll
+  for (int p = 0; p < kSelPer; ++p) kr[p] = (p < per && i0 + p < nc) ? score_key(srow[c0 + i0 + p]) : 0u;
+  if constexpr (BAND) {
+    const uint32_t* qsrc = (const uint32_t*)(q + ((size_t)bi * geo.hq + h * G) * kHeadDim);
+    for (int e = tid; e < G * kHeadDim / 2; e += kSelThreads) s_q[e] = qsrc[e];
+  }
+  int parity = 0;
+  bool exact;
+  int cnt_tau;
+  const uint32_t tau = wg_kth_key(kr, per, K, s_cnt, parity, &exact, &cnt_tau);
+  uint32_t take = 0u;  // bit p: candidate i0 + p selected
+  if constexpr (!BAND) {
+    if (exact) {
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p)
+        if (p < per && i0 + p < nc && kr[p] >= tau) take |= 1u << p;
+    } else {
+      // keys > tau are taken; of the keys == tau, the lowest indices
+      int gt = 0, ties = 0;
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p)
+        if (p < per && i0 + p < nc) {
+          gt += kr[p] > tau;
+          ties += kr[p] == tau;
+        }
+      int gt_total, tie_total;
+      (void)wg_scan_excl(gt, s_tmp, &gt_total);
+      int rank = wg_scan_excl(ties, s_tmp, &tie_total);
+      const int krem = K - gt_total;
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p)
+        if (p < per && i0 + p < nc) {
+          if (kr[p] > tau) take |= 1u << p;
+          else if (kr[p] == tau) {
+            if (rank < krem) take |= 1u << p;
+            ++rank;
+          }
+        }
+    }
+  } else {
+    // K-th and (K+1)-th largest approximate keys
+    uint32_t t1 = tau, t2;
+    {
+      uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p)
+        if (p < per && i0 + p < nc) {
+          if (kr[p] >= tau) lo = min(lo, kr[p]);
+          else hi = max(hi, kr[p]);
+        }
+      const uint32_t below = wg_reduce_u32(hi, true, s_red);
+      if (exact) {
+        t1 = wg_reduce_u32(lo, false, s_red);
+        t2 = below;
+      } else {
+        t2 = cnt_tau > K ? tau : below;
+      }
+    }
+    float e = 0.0f;
+    const float* erow = err + ((size_t)bi * geo.hkv + h) * err_stride;
+    for (int c = 0; c < err_count; ++c) e = fmaxf(e, erow[c]);  // NaN bounds are skipped
+    e = e * (1.0f + 0x1p-8f) + 0x1p-120f;
+    const float lb = key_value(t1) - e, ub = key_value(t2) + e;
+    // with non-finite bounds nothing is certain: every candidate is rescored
+    const bool bounds_ok = __builtin_isfinite(lb) && __builtin_isfinite(ub);
+    // classify: certainly in (take), band (rescored), certainly out
+    uint32_t band = 0u;
+    int nin = 0, nband = 0;
+#pragma unroll
+    for (int p = 0; p < kSelPer; ++p)
+      if (p < per && i0 + p < nc) {
+        const float v = srow[c0 + i0 + p];
+        const bool sure = bounds_ok && __builtin_isfinite(v);
+        if (sure && v - e > ub) {
+          take |= 1u << p;
+          ++nin;
+        } else if (!(sure && v + e < lb)) {
+          band |= 1u << p;
+          ++nband;
+        }
+      }
+    int nin_total, nband_total;
+    (void)wg_scan_excl(nin, s_tmp, &nin_total);
+    const int bpos = wg_scan_excl(nband, s_tmp, &nband_total);
+    const int krem = K - nin_total;
+    if (nband_total <= krem) {
+      take |= band;
+    } else {
+      // band list, then the canonical score of every band block
+      int w = bpos;
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p)
+        if (band & (1u << p)) s_band[w++] = (uint32_t)(c0 + i0 + p);
+      __syncthreads();
+      const int c = tid & 15;
+      const uint16_t* qh = (const uint16_t*)s_q;
+      for (int bk = tid >> 4; bk < nband_total; bk += kSelThreads / 16) {
+        const int j = (int)s_band[bk];
+        float sv[8];
+        unpack8<DT>(*(const u32x4*)(summary_row(geo, seq, h, j) + 8 * c), sv);
+        float best = 0.0f;
+#pragma unroll 1
+        for (int gq = 0; gq < G; ++gq) {
+          float qv[8];
+          unpack8<DT>(*(const u32x4*)(qh + gq * kHeadDim + 8 * c), qv);
+          const float acc = canonical_dot16(qv, sv);
+          if (gq == 0 || acc > best) best = acc;
+        }
+        if (c == 0) s_band[bk] = score_key(best);  // the slot's index is no longer needed
+      }
+      __syncthreads();
+      // exact top-krem of the band: keys > tau2 and the lowest-index ties
+      uint32_t br[kSelPer];
+      w = bpos;
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p) br[p] = (band & (1u << p)) ? s_band[w++] : 0u;
+      bool ex2;
+      int cnt2;
+      const uint32_t tau2 = wg_kth_key(br, per, krem, s_cnt, parity, &ex2, &cnt2);
+      int gt = 0, ties = 0;
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p)
+        if (band & (1u << p)) {
+          gt += br[p] > tau2;
+          ties += br[p] == tau2;
+        }
+      int gt_total, tie_total;
+      (void)wg_scan_excl(gt, s_tmp, &gt_total);
+      int rank = wg_scan_excl(ties, s_tmp, &tie_total);
+      const int krem2 = krem - gt_total;
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p)
+        if (band & (1u << p)) {
+          if (br[p] > tau2) take |= 1u << p;
+          else if (br[p] == tau2) {
+            if (rank < krem2) take |= 1u << p;
+            ++rank;
+          }
+        }
+    }
+  }
+  // output: sinks, the chosen candidates in index order, recent blocks
+  int total;
+  const int pos = wg_scan_excl(__popc(take), s_tmp, &total);
+  int w = geo.ns + pos;
+#pragma unroll
+  for (int p = 0; p < kSelPer; ++p)
+    if (take & (1u << p)) out[w++] = c0 + i0 + p;
+  for (int p = tid; p < geo.ns; p += kSelThreads) out[p] = p;
+  for (int r = tid; r < geo.nr; r += kSelThreads) out[geo.ns + total + r] = nb - geo.nr + r;
+  for (int p = geo.ns + total + geo.nr + tid; p < geo.nsel_max; p += kSelThreads) out[p] = -1;
+}
+
+// ===========================================================================
+// launcher: scoring + block-wide selection for batches whose largest
+// candidate set exceeds one wave's selection (or whose top_k does)
+// ===========================================================================
+int mfma_err_stride(const Geometry& g) { return (g.mbps + kMfmaChunk - 1) / kMfmaChunk; }
+
+template <int DT, int G>
+static void select_wide(const Geometry& g, const SeqBatch& b, const uint16_t* q, float* scores,
+                        float* err, int max_nc, int32_t* idx, hipStream_t s, Timing* prof) {
+  const int chunks = (max_nc + kMfmaChunk - 1) / kMfmaChunk;
+  const int stride = mfma_err_stride(g);
+  launch(k_score_mfma<DT, G>, dim3(chunks, g.hkv, b.n), dim3(256), 0, s, prof, kProfScore, g, b, q,
+         scores, err, stride);
+  launch(k_select<DT, G, true>, dim3(g.hkv, b.n), dim3(kSelThreads), (size_t)g.mbps * 4, s, prof,
+         kProfTopk, g, b, q, (const float*)scores, (const float*)err, stride, chunks, idx);
+}
+
+hipError_t launch_select_large(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                               float* err, int max_nc, int32_t* idx, hipStream_t s, Timing* prof,
+                               bool scores_ready) {
+  const uint16_t* qq = (const uint16_t*)q;
+  if (!scores_ready && g.group >= 8) {
+    if (g.dtype == 0) {
+      if (g.group == 8) select_wide<0, 8>(g, b, qq, scores, err, max_nc, idx, s, prof);
+      else select_wide<0, 16>(g, b, qq, scores, err, max_nc, idx, s, prof);
+    } else {
+      if (g.group == 8) select_wide<1, 8>(g, b, qq, scores, err, max_nc, idx, s, prof);
+      else select_wide<1, 16>(g, b, qq, scores, err, max_nc, idx, s, prof);
+    }
+    return hipGetLastError();
+  }
+  // exact scores already in `scores`
+  if (g.dtype == 0)
+    launch(k_select<0, 1, false>, dim3(g.hkv, b.n), dim3(kSelThreads), 0, s, prof, kProfTopk, g, b,
+           qq, (const float*)scores, (const float*)nullptr, 0, 0, idx);
+  else
+    launch(k_select<1, 1, false>, dim3(g.hkv, b.n), dim3(kSelThreads), 0, s, prof, kProfTopk, g, b,
+           qq, (const float*)scores, (const float*)nullptr, 0, 0, idx);
+  return hipGetLastError();
+}
+
+}  // namespace bsattn

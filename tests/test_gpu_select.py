@@ -1,0 +1,95 @@
+"""Block-wide selection (candidate sets larger than one wave's selection, or
+top_k above it) and MFMA scoring for wide GQA groups with the exact
+rescoring band: selected indices bit-exact against the oracle, outputs within
+2e-3 (net of the output rounding)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from common import fill, from_dev, log, make_workload, new_cache, oracle_decode, output_error, to_dev
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def check(cache, w, gpu, decode=True):
+    import torch
+    q = to_dev(w.q[:, :, None, :], w.dtype, gpu)
+    idx_ref, out_ref = oracle_decode(w)
+    idx = cache.selectBlocks(q)
+    out = cache.attend(q, idx, w.scale)
+    torch.cuda.synchronize()
+    got = idx.cpu().numpy()
+    bad = np.argwhere(got != idx_ref)
+    assert bad.size == 0, f"selected blocks differ at {bad[:5]}: {got[tuple(bad[0][:2])][:12]} vs {idx_ref[tuple(bad[0][:2])][:12]}"
+    a = from_dev(out).reshape(w.B, w.Hq, w.D)
+    err = output_error(O.to_f32(a, w.dtype).astype(np.float64), out_ref, w.dtype)
+    assert err <= TOL, f"output error {err:.3g}"
+    if decode:
+        out2 = cache.decode(q, w.scale)
+        torch.cuda.synchronize()
+        assert np.array_equal(from_dev(out2).reshape(w.B, w.Hq, w.D), a), "decode != select + attend"
+    return err
+
+
+@pytest.mark.parametrize("dtype,Hq,Hkv,Tb,K", [
+    ("bf16", 16, 4, 64, 32), ("f16", 16, 4, 32, 5), ("bf16", 4, 4, 32, 300), ("f16", 4, 2, 64, 64),
+])
+def test_block_select_exact_scores(gpu, dtype, Hq, Hkv, Tb, K):
+    """G <= 4: canonical VALU scores, k_select over 1000 - 5000 candidates
+    (ragged, including sequences below and above one wave's limit)."""
+    lens = [Tb * 5000 - 7, Tb * 1100, Tb * 700 + 3, Tb * 30, Tb * 2500 + 1] if Tb == 32 else \
+        [Tb * 2600 - 7, Tb * 1100, Tb * 700 + 3, Tb * 30]
+    log(f"[select] {dtype} G={Hq // Hkv} Tb={Tb} K={K}")
+    w = make_workload(5000 + Hq + Tb + K, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype=dtype,
+                      top_k=K, ns=2, nr=3, lens=lens, salient_frac=0.01)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    err = check(cache, w, gpu)
+    log(f"[select] err={err:.3g}")
+
+
+@pytest.mark.parametrize("dtype,Hq,Hkv,Tb,K", [
+    ("bf16", 64, 4, 32, 128), ("f16", 64, 4, 32, 128), ("bf16", 32, 4, 64, 40), ("f16", 16, 2, 64, 7),
+])
+def test_wide_group_mfma_band(gpu, dtype, Hq, Hkv, Tb, K):
+    """G = 8 / 16 with more than one wave's candidates: MFMA scores, exact
+    rescoring of the band, bit-exact selection."""
+    lens = [Tb * 3000 + 5, Tb * 1030, Tb * 200, Tb * 4096] if Tb == 32 else \
+        [Tb * 2000 + 5, Tb * 1030, Tb * 200, Tb * 2500]
+    log(f"[band] {dtype} G={Hq // Hkv} Tb={Tb} K={K}")
+    w = make_workload(5100 + Hq + Tb + K, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype=dtype,
+                      top_k=K, ns=1, nr=4, lens=lens, salient_frac=0.01)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    err = check(cache, w, gpu)
+    log(f"[band] err={err:.3g}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_wide_group_ties_and_duplicates(gpu, dtype):
+    """Sequence 0: every block has the same keys (all scores tie: the band is
+    every candidate, lowest indices win).  Sequence 1: a few blocks copied
+    many times near the top (exact ties inside the band)."""
+    Tb = 32
+    lens = [Tb * 1500, Tb * 1600 + 11]
+    w = make_workload(5200, B=2, Hq=64, Hkv=4, T=max(lens), Tb=Tb, dtype=dtype, top_k=50, ns=1, nr=4,
+                      lens=lens, salient_frac=0.01)
+    for h in range(w.Hkv):
+        blk = w.keys[0][h][:Tb].copy()
+        for j in range(lens[0] // Tb):
+            w.keys[0][h][j * Tb:(j + 1) * Tb] = blk
+        rng = np.random.default_rng(h)
+        for src in rng.choice(lens[1] // Tb - 10, 5, replace=False) + 5:
+            for dst in rng.choice(lens[1] // Tb - 10, 20, replace=False) + 5:
+                w.keys[1][h][dst * Tb:(dst + 1) * Tb] = w.keys[1][h][src * Tb:(src + 1) * Tb]
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    check(cache, w, gpu)
+    q = to_dev(w.q[:, :, None, :], w.dtype, gpu)
+    idx = cache.selectBlocks(q).cpu().numpy()
+    nb = lens[0] // Tb
+    assert list(idx[0, 0][:52]) == list(range(51)) + [nb - 4]
