@@ -3,12 +3,12 @@
 //
 // k_select: one 1024-thread workgroup per (kv head, sequence).  Thread t owns
 // the contiguous candidates [t*per, t*per + per) (per <= 12) with their keys
-// in registers; the K-th largest key is found bit by bit from the top, each
-// step counting keys >= the candidate prefix with ballots and one workgroup
-// barrier (the counts of the 16 waves meet in double-buffered LDS slots), and
-// stops early once exactly K keys are >= the prefix.  Ties at the K-th key go
-// to the lowest indices (a workgroup scan over the owners' segments), and
-// the output is compacted in ascending block order.
+// in registers; the K-th largest key is found by a range-adaptive radix
+// select (a 2048-bin LDS histogram of the keys' range, refined inside the
+// bin that holds the K-th key, which one wave resolves once it holds at most
+// 64 keys).  Ties at the K-th key go to the lowest indices (a workgroup scan
+// over the owners' segments), and the output is compacted in ascending
+// block order.
 //
 // Wide groups (G >= 8): the block scores are first computed with MFMA
 // (k_score_mfma), which does not reproduce the canonical summation order.
@@ -151,27 +151,6 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
 // ---------------------------------------------------------------------------
 // workgroup primitives (1024 threads)
 // ---------------------------------------------------------------------------
-// keys >= cand over the workgroup; one barrier; s_cnt double-buffered by
-// the caller's parity (a slot is rewritten only after every wave has passed
-// the barrier that follows its last read)
-__device__ __forceinline__ int wg_count_ge(const uint32_t (&kr)[kSelPer], int per, uint32_t cand,
-                                           int (*s_cnt)[kSelWaves], int& parity) {
-  uint64_t m[kSelPer];
-#pragma unroll
-  for (int p = 0; p < kSelPer; ++p) m[p] = (p < per) ? __ballot(kr[p] >= cand) : 0ull;
-  __builtin_amdgcn_sched_barrier(0);
-  int c = 0;
-#pragma unroll
-  for (int p = 0; p < kSelPer; ++p) c += __popcll(m[p]);
-  if ((threadIdx.x & 63) == 0) s_cnt[parity][threadIdx.x >> 6] = c;
-  __syncthreads();
-  int tot = 0;
-#pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) tot += s_cnt[parity][w];
-  parity ^= 1;
-  return tot;
-}
-
 // exclusive prefix sum of v over the workgroup in thread order; *total
 __device__ __forceinline__ int wg_scan_excl(int v, int* s_tmp, int* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -195,47 +174,165 @@ __device__ __forceinline__ int wg_scan_excl(int v, int* s_tmp, int* total) {
   return off + x - v;
 }
 
-__device__ __forceinline__ uint32_t wg_reduce_u32(uint32_t v, bool is_max, uint32_t* s_red) {
+// workgroup minimum of a and maximum of b (one exchange)
+__device__ __forceinline__ void wg_minmax(uint32_t& a, uint32_t& b, uint32_t (*s_red)[kSelWaves]) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_xor(v, o, 64);
-    v = is_max ? max(v, y) : min(v, y);
+    a = min(a, (uint32_t)__shfl_xor(a, o, 64));
+    b = max(b, (uint32_t)__shfl_xor(b, o, 64));
   }
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  if ((threadIdx.x & 63) == 0) {
+    s_red[0][threadIdx.x >> 6] = a;
+    s_red[1][threadIdx.x >> 6] = b;
+  }
   __syncthreads();
-  uint32_t r = s_red[0];
+  a = s_red[0][0];
+  b = s_red[1][0];
 #pragma unroll
-  for (int i = 1; i < kSelWaves; ++i) r = is_max ? max(r, s_red[i]) : min(r, s_red[i]);
-  return r;
+  for (int i = 1; i < kSelWaves; ++i) {
+    a = min(a, s_red[0][i]);
+    b = max(b, s_red[1][i]);
+  }
 }
 
-// K-th largest key over the workgroup's keys (kr[p], p < per; padding keys
-// are 0 and never counted, real keys may be 0).  Returns tau with
-// count(>= tau) >= K; *exact is set when exactly K keys are >= tau (then
-// those K keys are the selection, whatever tau is); otherwise tau is the
-// K-th largest key itself (0 when fewer than K keys are nonzero).
-__device__ __forceinline__ uint32_t wg_kth_key(const uint32_t (&kr)[kSelPer], int per, int K,
-                                               int (*s_cnt)[kSelWaves], int& parity,
-                                               bool* exact, int* cnt_at_tau) {
-  uint32_t tau = 0u;
-  int cnt = 0;
-  *exact = false;
+constexpr int kHistBins = 2048;
+constexpr int kSmall = 64;  // keys resolved by one wave
+
+struct SelScratch {
+  uint32_t hist[kHistBins];
+  uint32_t small[kSmall];
+  int misc[8];
+  int s_tmp[kSelWaves];
+  uint32_t s_red[2][kSelWaves];
+};
+
+// The K-th largest of the workgroup's valid keys (bit p of vmask: kr[p]
+// valid), 1 <= K <= number of valid keys.  Range-adaptive radix select: the
+// keys in [lo, hi] are histogrammed into 2048 bins of width 2^s, the bin
+// holding the K-th largest becomes the new range, until the range is one
+// value or its bin holds at most 64 keys, which one wave then resolves by
+// a bitwise search of their offsets.  Each refinement divides the range by
+// 2048, so there are at most three.  *gt = valid keys > the result;
+// *eq = valid keys equal to it.
+__device__ uint32_t wg_kth(const uint32_t (&kr)[kSelPer], uint32_t vmask, int K, SelScratch& ss,
+                           int* gt, int* eq) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+#pragma unroll
+  for (int p = 0; p < kSelPer; ++p)
+    if ((vmask >> p) & 1u) {
+      lo = min(lo, kr[p]);
+      hi = max(hi, kr[p]);
+    }
+  wg_minmax(lo, hi, ss.s_red);
+  int need = K, above = 0;
+  uint32_t tau;
 #pragma unroll 1
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = tau | (1u << bit);
-    const int c = wg_count_ge(kr, per, cand, s_cnt, parity);
-    if (c >= K) {
-      tau = cand;
-      cnt = c;
-      if (c == K) {
-        *exact = true;
-        break;
+  while (true) {
+    if (lo == hi) {  // every remaining key has one value
+      tau = lo;
+      *gt = above;
+      *eq = -1;  // unknown here; computed below when asked for
+      break;
+    }
+    const int s = max(0, 32 - __clz(hi - lo) - 11);  // (hi - lo) >> s < 2048
+    for (int b = tid; b < kHistBins; b += kSelThreads) ss.hist[b] = 0u;
+    if (tid == 0) ss.misc[3] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < kSelPer; ++p)
+      if (((vmask >> p) & 1u) && kr[p] >= lo && kr[p] <= hi) atomicAdd(&ss.hist[(kr[p] - lo) >> s], 1u);
+    __syncthreads();
+    // thread t owns bins 2047 - 2t and 2046 - 2t, so a scan in thread order
+    // counts the keys in higher bins
+    const int b0 = kHistBins - 1 - 2 * tid, b1 = b0 - 1;
+    const int h0 = (int)ss.hist[b0], h1 = (int)ss.hist[b1];
+    int tot;
+    const int before = wg_scan_excl(h0 + h1, ss.s_tmp, &tot);
+    if (before < need && need <= before + h0) {
+      ss.misc[0] = b0;
+      ss.misc[1] = before;
+      ss.misc[2] = h0;
+    } else if (before + h0 < need && need <= before + h0 + h1) {
+      ss.misc[0] = b1;
+      ss.misc[1] = before + h0;
+      ss.misc[2] = h1;
+    }
+    __syncthreads();
+    const int bstar = ss.misc[0], abv = ss.misc[1], cnt = ss.misc[2];
+    above += abv;
+    need -= abv;
+    const uint32_t nlo = lo + ((uint32_t)bstar << s);
+    const uint32_t span = (1u << s) - 1u;
+    hi = (hi - nlo < span) ? hi : nlo + span;
+    lo = nlo;
+    if (s == 0) {  // one-value bin
+      tau = lo;
+      *gt = above;
+      *eq = cnt;
+      break;
+    }
+    if (cnt <= kSmall) {
+      // gather the bin's keys; one wave finds the need-th largest offset
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p)
+        if (((vmask >> p) & 1u) && kr[p] >= lo && kr[p] <= hi) ss.small[atomicAdd(&ss.misc[3], 1)] = kr[p];
+      __syncthreads();
+      if (tid < 64) {
+        const bool valid = lane < cnt;
+        const uint32_t x = valid ? ss.small[lane] - lo : 0u;
+        uint32_t t = 0u;
+        for (int bit = s - 1; bit >= 0; --bit) {
+          const uint32_t cand = t | (1u << bit);
+          if (__popcll(__ballot(valid && x >= cand)) >= need) t = cand;
+        }
+        const int g = __popcll(__ballot(valid && x > t));
+        const int e = __popcll(__ballot(valid && x == t));
+        if (lane == 0) {
+          ss.misc[4] = (int)(lo + t);
+          ss.misc[5] = g;
+          ss.misc[6] = e;
+        }
+      }
+      __syncthreads();
+      tau = (uint32_t)ss.misc[4];
+      *gt = above + ss.misc[5];
+      *eq = ss.misc[6];
+      break;
+    }
+    __syncthreads();  // misc / hist are rewritten by the next refinement
+  }
+  __syncthreads();  // ss is reused by the caller
+  return tau;
+}
+
+// Marks the K largest valid keys (ties at the K-th to the lowest index, i.e.
+// thread order then p) in the returned bitmask; all when fewer are valid.
+__device__ uint32_t wg_topk_mask(const uint32_t (&kr)[kSelPer], uint32_t vmask, int K, SelScratch& ss) {
+  if (K <= 0) return 0u;
+  int nvalid_total;
+  (void)wg_scan_excl(__popc(vmask), ss.s_tmp, &nvalid_total);
+  if (nvalid_total <= K) return vmask;
+  int gt, eq;
+  const uint32_t tau = wg_kth(kr, vmask, K, ss, &gt, &eq);
+  int ties = 0;
+#pragma unroll
+  for (int p = 0; p < kSelPer; ++p) ties += ((vmask >> p) & 1u) && kr[p] == tau;
+  int tie_total;
+  int rank = wg_scan_excl(ties, ss.s_tmp, &tie_total);
+  const int krem = K - gt;
+  uint32_t take = 0u;
+#pragma unroll
+  for (int p = 0; p < kSelPer; ++p)
+    if ((vmask >> p) & 1u) {
+      if (kr[p] > tau) take |= 1u << p;
+      else if (kr[p] == tau) {
+        if (rank < krem) take |= 1u << p;
+        ++rank;
       }
     }
-  }
-  *cnt_at_tau = cnt;
-  return tau;
+  return take;
 }
 
 // ---------------------------------------------------------------------------
@@ -251,9 +348,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
                                                         int err_stride, int err_count,
                                                         int32_t* __restrict__ idx_out) {
   extern __shared__ uint32_t s_band[];
-  __shared__ int s_cnt[2][kSelWaves];
-  __shared__ int s_tmp[kSelWaves];
-  __shared__ uint32_t s_red[kSelWaves];
+  __shared__ SelScratch ss;
   __shared__ __align__(16) uint32_t s_q[BAND ? G * kHeadDim / 2 : 4];
   const int tid = threadIdx.x;
   const int h = blockIdx.x, bi = blockIdx.y;
@@ -270,77 +365,57 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
   const int per = (nc + kSelThreads - 1) / kSelThreads;
   const int i0 = tid * per;  // this thread's candidates: c0 + i0 + p, p < per, i0 + p < nc
   uint32_t kr[kSelPer];
+  uint32_t vmask = 0u;
 #pragma unroll
-  for (int p = 0; p < kSelPer; ++p) kr[p] = (p < per && i0 + p < nc) ? score_key(srow[c0 + i0 + p]) : 0u;
-  if constexpr (BAND) {
+  for (int p = 0; p < kSelPer; ++p) {
+    const bool v = p < per && i0 + p < nc;
+    kr[p] = v ? score_key(srow[c0 + i0 + p]) : 0u;
+    vmask |= (uint32_t)v << p;
+  }
+  uint32_t take;
+  if constexpr (!BAND) {
+    take = wg_topk_mask(kr, vmask, K, ss);
+  } else {
     const uint32_t* qsrc = (const uint32_t*)(q + ((size_t)bi * geo.hq + h * G) * kHeadDim);
     for (int e = tid; e < G * kHeadDim / 2; e += kSelThreads) s_q[e] = qsrc[e];
-  }
-  int parity = 0;
-  bool exact;
-  int cnt_tau;
-  const uint32_t tau = wg_kth_key(kr, per, K, s_cnt, parity, &exact, &cnt_tau);
-  uint32_t take = 0u;  // bit p: candidate i0 + p selected
-  if constexpr (!BAND) {
-    if (exact) {
-#pragma unroll
-      for (int p = 0; p < kSelPer; ++p)
-        if (p < per && i0 + p < nc && kr[p] >= tau) take |= 1u << p;
-    } else {
-      // keys > tau are taken; of the keys == tau, the lowest indices
-      int gt = 0, ties = 0;
-#pragma unroll
-      for (int p = 0; p < kSelPer; ++p)
-        if (p < per && i0 + p < nc) {
-          gt += kr[p] > tau;
-          ties += kr[p] == tau;
-        }
-      int gt_total, tie_total;
-      (void)wg_scan_excl(gt, s_tmp, &gt_total);
-      int rank = wg_scan_excl(ties, s_tmp, &tie_total);
-      const int krem = K - gt_total;
-#pragma unroll
-      for (int p = 0; p < kSelPer; ++p)
-        if (p < per && i0 + p < nc) {
-          if (kr[p] > tau) take |= 1u << p;
-          else if (kr[p] == tau) {
-            if (rank < krem) take |= 1u << p;
-            ++rank;
-          }
-        }
-    }
-  } else {
-    // K-th and (K+1)-th largest approximate keys
-    uint32_t t1 = tau, t2;
-    {
-      uint32_t lo = 0xFFFFFFFFu, hi = 0u;
-#pragma unroll
-      for (int p = 0; p < kSelPer; ++p)
-        if (p < per && i0 + p < nc) {
-          if (kr[p] >= tau) lo = min(lo, kr[p]);
-          else hi = max(hi, kr[p]);
-        }
-      const uint32_t below = wg_reduce_u32(hi, true, s_red);
-      if (exact) {
-        t1 = wg_reduce_u32(lo, false, s_red);
-        t2 = below;
-      } else {
-        t2 = cnt_tau > K ? tau : below;
-      }
-    }
+    // the bound: maximum over the chunks' bounds (NaN bounds are skipped)
     float e = 0.0f;
-    const float* erow = err + ((size_t)bi * geo.hkv + h) * err_stride;
-    for (int c = 0; c < err_count; ++c) e = fmaxf(e, erow[c]);  // NaN bounds are skipped
-    e = e * (1.0f + 0x1p-8f) + 0x1p-120f;
+    if (tid < 64) {
+      const float* erow = err + ((size_t)bi * geo.hkv + h) * err_stride;
+      for (int c = tid; c < err_count; c += 64) e = fmaxf(e, erow[c]);
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) e = fmaxf(e, __shfl_xor(e, o, 64));
+      if (tid == 0) ss.misc[7] = __float_as_int(e);
+    }
+    // K-th and (K+1)-th largest approximate keys
+    int gt, eq;
+    const uint32_t t1 = wg_kth(kr, vmask, K, ss, &gt, &eq);
+    e = __int_as_float(ss.misc[7]) * (1.0f + 0x1p-8f) + 0x1p-120f;
+    uint32_t t2;
+    {
+      int cnt_ge = 0;
+      uint32_t below = 0u, unused = 0xFFFFFFFFu;
+#pragma unroll
+      for (int p = 0; p < kSelPer; ++p)
+        if ((vmask >> p) & 1u) {
+          cnt_ge += kr[p] >= t1;
+          if (kr[p] < t1) below = max(below, kr[p]);
+        }
+      int ge_total;
+      (void)wg_scan_excl(cnt_ge, ss.s_tmp, &ge_total);
+      wg_minmax(unused, below, ss.s_red);
+      t2 = ge_total > K ? t1 : below;
+    }
     const float lb = key_value(t1) - e, ub = key_value(t2) + e;
     // with non-finite bounds nothing is certain: every candidate is rescored
     const bool bounds_ok = __builtin_isfinite(lb) && __builtin_isfinite(ub);
     // classify: certainly in (take), band (rescored), certainly out
     uint32_t band = 0u;
+    take = 0u;
     int nin = 0, nband = 0;
 #pragma unroll
     for (int p = 0; p < kSelPer; ++p)
-      if (p < per && i0 + p < nc) {
+      if ((vmask >> p) & 1u) {
         const float v = srow[c0 + i0 + p];
         const bool sure = bounds_ok && __builtin_isfinite(v);
         if (sure && v - e > ub) {
@@ -352,8 +427,8 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
         }
       }
     int nin_total, nband_total;
-    (void)wg_scan_excl(nin, s_tmp, &nin_total);
-    const int bpos = wg_scan_excl(nband, s_tmp, &nband_total);
+    (void)wg_scan_excl(nin, ss.s_tmp, &nin_total);
+    const int bpos = wg_scan_excl(nband, ss.s_tmp, &nband_total);
     const int krem = K - nin_total;
     if (nband_total <= krem) {
       take |= band;
@@ -381,39 +456,16 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
         if (c == 0) s_band[bk] = score_key(best);  // the slot's index is no longer needed
       }
       __syncthreads();
-      // exact top-krem of the band: keys > tau2 and the lowest-index ties
       uint32_t br[kSelPer];
       w = bpos;
 #pragma unroll
       for (int p = 0; p < kSelPer; ++p) br[p] = (band & (1u << p)) ? s_band[w++] : 0u;
-      bool ex2;
-      int cnt2;
-      const uint32_t tau2 = wg_kth_key(br, per, krem, s_cnt, parity, &ex2, &cnt2);
-      int gt = 0, ties = 0;
-#pragma unroll
-      for (int p = 0; p < kSelPer; ++p)
-        if (band & (1u << p)) {
-          gt += br[p] > tau2;
-          ties += br[p] == tau2;
-        }
-      int gt_total, tie_total;
-      (void)wg_scan_excl(gt, s_tmp, &gt_total);
-      int rank = wg_scan_excl(ties, s_tmp, &tie_total);
-      const int krem2 = krem - gt_total;
-#pragma unroll
-      for (int p = 0; p < kSelPer; ++p)
-        if (band & (1u << p)) {
-          if (br[p] > tau2) take |= 1u << p;
-          else if (br[p] == tau2) {
-            if (rank < krem2) take |= 1u << p;
-            ++rank;
-          }
-        }
+      take |= wg_topk_mask(br, band, krem, ss);
     }
   }
   // output: sinks, the chosen candidates in index order, recent blocks
   int total;
-  const int pos = wg_scan_excl(__popc(take), s_tmp, &total);
+  const int pos = wg_scan_excl(__popc(take), ss.s_tmp, &total);
   int w = geo.ns + pos;
 #pragma unroll
   for (int p = 0; p < kSelPer; ++p)
