@@ -110,71 +110,249 @@ __host__ __device__ inline bool ranked_select(const Geometry& g, int nc) {
   return nc > g.top_k && g.top_k > 0;
 }
 
-// Canonical dot product of one 128-dim pair held by 16 consecutive lanes
-// (lane c = chunk c: dims 8c .. 8c+7): left fold of the chunk's 8 products,
-// then the pairwise tree over chunks as an xor butterfly 1, 2, 4, 8.  Every
-// one of the 16 lanes returns the same bits.
+// x of the lane K places up in the same 16-lane DPP row (row_shl:K); lanes
+// whose source falls outside the row get 0
+template <int K>
+__device__ __forceinline__ float row_shl(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + K, 0xF, 0xF, true));
+}
+
+// Canonical dot product of one 128-dim pair held by the 16 lanes of a DPP
+// row (lane c = chunk c: dims 8c .. 8c+7): left fold of the chunk's 8
+// products, then the pairwise tree over chunks, (c, c+1), then (c, c+2),
+// (c, c+4), (c, c+8), which lane 0 of the row accumulates through row
+// shifts (fp32 addition is commutative, so the order of each pair does not
+// matter).  Only lane 0 of the row (c == 0) holds the result.
 __device__ __forceinline__ float canonical_dot16(const float* a, const float* b) {
   float acc = __fmul_rn(a[0], b[0]);
 #pragma unroll
   for (int e = 1; e < 8; ++e) acc = __fadd_rn(acc, __fmul_rn(a[e], b[e]));
-  acc = __fadd_rn(acc, __shfl_xor(acc, 1, 64));
-  acc = __fadd_rn(acc, __shfl_xor(acc, 2, 64));
-  acc = __fadd_rn(acc, __shfl_xor(acc, 4, 64));
-  acc = __fadd_rn(acc, __shfl_xor(acc, 8, 64));
+  acc = __fadd_rn(acc, row_shl<1>(acc));
+  acc = __fadd_rn(acc, row_shl<2>(acc));
+  acc = __fadd_rn(acc, row_shl<4>(acc));
+  acc = __fadd_rn(acc, row_shl<8>(acc));
   return acc;
 }
 
 // ---------------------------------------------------------------------------
 // wave-level top-K of one (sequence, kv head): the same selection as the
 // oracle (K largest keys, ties to the lower index), computed by one wave with
-// no LDS atomics and no workgroup barriers.  Lane l holds candidates
-// c0 + l + 64*k, k < S (S a power of two; padded keys are 0).  tau = the
-// K-th largest key is found bit by bit from the top: a candidate prefix
-// (always >= 1, so padded keys never count) stays if at least K keys are
-// >= it, counted with ballots.  Candidates c0 .. c0+nc-1, nc <= 64 * S,
-// nc > K > 0.  Writes the K chosen block indices, ascending, to sel_blk and
-// their pages (from bt) to sel_page when sel_page is not null.
+// no workgroup barriers.  Lane l holds candidates c0 + l + 64*k, k < S (S a
+// power of two; padded keys are 0 and never counted).  The K-th largest key
+// tau is found by a range-adaptive histogram select in LDS (kWaveBins bins
+// over the score range, refined inside the bin that holds the K-th key until
+// it holds at most 64 keys, which a bitwise search of their offsets
+// resolves); keys > tau are taken, and of the keys == tau the lowest indices.
+// Candidates c0 .. c0+nc-1, nc <= 64 * S, nc > K > 0.  Writes the K chosen
+// block indices, ascending, to sel_blk and their pages (from bt) to sel_page
+// when sel_page is not null.  ws: kWaveScratch words of LDS, 16-B aligned.
 // ---------------------------------------------------------------------------
 constexpr int kSelKeysPerLane = 16;
 constexpr int kSelMaxK = 256;  // top_k limit of the in-kernel selection
+constexpr int kWaveBins = 1024;
+constexpr int kWaveScratch = kWaveBins + 64;
+
+// inverse of score_key; key 0 (NaN) -> -inf
+__device__ __forceinline__ float key_value(uint32_t key) {
+  if (key == 0u) return -INFINITY;
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
+// cross-lane moves on the VALU: DPP within 16-lane rows, permlane swaps
+// across rows (no LDS round trips)
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, true);
+}
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowRor4 = 0x124, kDppRowRor8 = 0x128;
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_allreduce_u32(uint32_t x, Op op) {
+  x = op(x, dpp_u32<kDppQuadXor1>(x));
+  x = op(x, dpp_u32<kDppQuadXor2>(x));
+  x = op(x, dpp_u32<kDppRowRor4>(x));
+  x = op(x, dpp_u32<kDppRowRor8>(x));
+  const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = op((uint32_t)a[0], (uint32_t)a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return op((uint32_t)b[0], (uint32_t)b[1]);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  return wave_allreduce_u32(x, [](uint32_t a, uint32_t b) { return min(a, b); });
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  return wave_allreduce_u32(x, [](uint32_t a, uint32_t b) { return max(a, b); });
+}
+// inclusive prefix sum over the wave's lanes
+__device__ __forceinline__ int wave_scan_incl(int v) {
+  uint32_t x = (uint32_t)v;
+  x += dpp_u32<kDppRowShr1>(x);
+  x += dpp_u32<kDppRowShr2>(x);
+  x += dpp_u32<kDppRowShr4>(x);
+  x += dpp_u32<kDppRowShr8>(x);
+  x += dpp_u32<kDppRowBcast15, 0xA>(x);
+  x += dpp_u32<kDppRowBcast31, 0xC>(x);
+  return (int)x;
+}
+// orders this wave's LDS accesses (a wave's LDS instructions complete in
+// issue order; this keeps the compiler from moving them across)
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
 
 template <int S>
-__device__ __forceinline__ void wave_topk_s(const float* __restrict__ srow,
-                                            const int32_t* __restrict__ bt, int c0, int nc,
-                                            int K, int* sel_blk, int* sel_page) {
+__device__ __forceinline__ uint32_t wave_kth_key(const uint32_t (&key)[S], int nc, int K, uint32_t* ws) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+#pragma unroll
+  for (int k = 0; k < S; ++k)
+    if (lane + 64 * k < nc) {
+      lo = min(lo, key[k]);
+      hi = max(hi, key[k]);
+    }
+  lo = wave_min_u32(lo);
+  hi = wave_max_u32(hi);
+  int need = K;
+  bool by_value = true;
+  uint32_t* hist = ws;
+  uint32_t* small = ws + kWaveBins;
+#pragma unroll 1
+  while (true) {
+    if (lo == hi) return lo;
+    // the first pass bins by score value (keys crowd in a few binary
+    // exponents), later passes by key bits
+    const float vlo = key_value(lo), span = key_value(hi) - vlo;
+    const bool use_v = by_value && __builtin_isfinite(vlo) && __builtin_isfinite(span) && span > 0.0f;
+    const float scale = use_v ? (float)(kWaveBins - 1) / span : 0.0f;
+    const int sh = use_v ? 0 : max(0, 32 - __clz(hi - lo) - 10);  // (hi - lo) >> sh < 1024
+    auto bin = [&](uint32_t k) -> int {
+      return use_v ? min(kWaveBins - 1, (int)((key_value(k) - vlo) * scale)) : (int)((k - lo) >> sh);
+    };
+    u32x4* h4 = (u32x4*)hist + lane * (kWaveBins / 256);
+#pragma unroll
+    for (int i = 0; i < kWaveBins / 256; ++i) h4[i] = u32x4{0u, 0u, 0u, 0u};
+    wave_lds_order();
+#pragma unroll
+    for (int k = 0; k < S; ++k)
+      if (lane + 64 * k < nc && key[k] >= lo && key[k] <= hi) atomicAdd(&hist[bin(key[k])], 1u);
+    wave_lds_order();
+    // lane l owns bins 1023 - 16l - j, j < 16 (descending), so a scan over
+    // lanes counts the keys in higher bins
+    constexpr int BPL = kWaveBins / 64;
+    const u32x4* r4 = (const u32x4*)(hist + kWaveBins - BPL * (lane + 1));
+    uint32_t c[BPL];  // c[j] = bin 1023 - 16 * lane - j
+#pragma unroll
+    for (int i = 0; i < BPL / 4; ++i) {
+      const u32x4 v = r4[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c[BPL - 1 - (4 * i + e)] = v[e];
+    }
+    int lsum = 0;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) lsum += (int)c[j];
+    const int incl = wave_scan_incl(lsum);
+    const int excl = incl - lsum;
+    const bool mine = excl < need && need <= incl;
+    int b_star = 0, abv = 0, cnt = 0;
+    if (mine) {
+      int cum = excl;
+#pragma unroll
+      for (int j = 0; j < BPL; ++j) {
+        if (cum < need && need <= cum + (int)c[j]) {
+          b_star = kWaveBins - 1 - BPL * lane - j;
+          abv = cum;
+          cnt = (int)c[j];
+        }
+        cum += (int)c[j];
+      }
+    }
+    const int src = __ffsll((unsigned long long)__ballot(mine)) - 1;
+    b_star = __builtin_amdgcn_readlane(b_star, src);
+    abv = __builtin_amdgcn_readlane(abv, src);
+    cnt = __builtin_amdgcn_readlane(cnt, src);
+    need -= abv;
+    if (!use_v && sh == 0) return lo + (uint32_t)b_star;  // one-value bin
+    if (cnt <= 64) {
+      // the bin's keys, in any order; a bitwise search of their offsets
+      int base = 0;
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        const bool in = lane + 64 * k < nc && key[k] >= lo && key[k] <= hi && bin(key[k]) == b_star;
+        const uint64_t m = __ballot(in);
+        if (in) small[base + __popcll(m & below)] = key[k];
+        base += __popcll(m);
+      }
+      wave_lds_order();
+      const bool valid = lane < cnt;
+      const uint32_t x = valid ? small[lane] : 0u;
+      const uint32_t mn = wave_min_u32(valid ? x : 0xFFFFFFFFu), mx = wave_max_u32(x);
+      const uint32_t off = x - mn;
+      uint32_t t = 0u;
+      for (int bit = mx == mn ? -1 : 31 - __clz(mx - mn); bit >= 0; --bit) {
+        const uint32_t cand = t | (1u << bit);
+        if (__popcll(__ballot(valid && off >= cand)) >= need) t = cand;
+      }
+      wave_lds_order();  // the scratch may be reused right after
+      return mn + t;
+    }
+    if (use_v) {
+      uint32_t nlo = 0xFFFFFFFFu, nhi = 0u;
+#pragma unroll
+      for (int k = 0; k < S; ++k)
+        if (lane + 64 * k < nc && key[k] >= lo && key[k] <= hi && bin(key[k]) == b_star) {
+          nlo = min(nlo, key[k]);
+          nhi = max(nhi, key[k]);
+        }
+      lo = wave_min_u32(nlo);
+      hi = wave_max_u32(nhi);
+    } else {
+      const uint32_t nlo = lo + ((uint32_t)b_star << sh);
+      const uint32_t span_k = (1u << sh) - 1u;
+      hi = (hi - nlo < span_k) ? hi : nlo + span_k;
+      lo = nlo;
+    }
+    by_value = false;
+    wave_lds_order();
+  }
+}
+
+// Raw scores and block-table entries of the candidates c0 + lane + 64*k,
+// k < kSelKeysPerLane, loaded before the sequence length is known (the
+// score and block-table rows are mbps wide; the remaining slots read 0).
+struct WaveCand {
+  float score[kSelKeysPerLane];
+  int page[kSelKeysPerLane];
+};
+__device__ __forceinline__ void wave_cand_load(const float* __restrict__ srow,
+                                               const int32_t* __restrict__ bt, int c0, int mbps,
+                                               WaveCand& wc) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < kSelKeysPerLane; ++k) {
+    const int j = c0 + lane + 64 * k;
+    wc.score[k] = j < mbps ? srow[j] : 0.0f;
+    wc.page[k] = (bt != nullptr && j < mbps) ? bt[j] : 0;
+  }
+}
+
+template <int S>
+__device__ __forceinline__ void wave_topk_s(const WaveCand& wc, int c0, int nc, int K, int* sel_blk,
+                                            int* sel_page, uint32_t* ws) {
   const int lane = threadIdx.x & 63;
   uint32_t key[S];
-  int page[S];
 #pragma unroll
-  for (int k = 0; k < S; ++k) {
-    const int i = lane + 64 * k;
-    const bool real = i < nc;
-    key[k] = real ? score_key(srow[c0 + i]) : 0u;
-    page[k] = (real && sel_page) ? bt[c0 + i] : 0;
-  }
-  // all compares of a step are issued before the first popcount: each
-  // scalar read of a VALU-written mask waits for the VALU pipeline, and
-  // grouping them pays that wait once per step instead of once per slot
-  uint32_t tau = 0u;
-#pragma unroll 1
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = tau | (1u << bit);
-    uint64_t m[S];
-#pragma unroll
-    for (int k = 0; k < S; ++k) m[k] = __ballot(key[k] >= cand);
-    __builtin_amdgcn_sched_barrier(0);
-    int cnt = 0;
-#pragma unroll
-    for (int k = 0; k < S; ++k) cnt += __popcll(m[k]);
-    if (cnt >= K) tau = cand;
-  }
+  for (int k = 0; k < S; ++k) key[k] = lane + 64 * k < nc ? score_key(wc.score[k]) : 0u;
+  const uint32_t tau = wave_kth_key<S>(key, nc, K, ws);
   // keys > tau are taken; of the keys == tau, the krem lowest indices
   int gt_total = 0;
   {
     uint64_t m[S];
 #pragma unroll
-    for (int k = 0; k < S; ++k) m[k] = __ballot(key[k] > tau);
+    for (int k = 0; k < S; ++k) m[k] = __ballot(lane + 64 * k < nc && key[k] > tau);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < S; ++k) gt_total += __popcll(m[k]);
@@ -185,14 +363,15 @@ __device__ __forceinline__ void wave_topk_s(const float* __restrict__ srow,
 #pragma unroll
   for (int k = 0; k < S; ++k) {
     const int i = lane + 64 * k;
-    const bool eq = i < nc && key[k] == tau;
+    const bool real = i < nc;
+    const bool eq = real && key[k] == tau;
     const uint64_t eqm = __ballot(eq);
-    const bool take = key[k] > tau || (eq && ties_before + __popcll(eqm & below) < krem);
+    const bool take = (real && key[k] > tau) || (eq && ties_before + __popcll(eqm & below) < krem);
     const uint64_t tm = __ballot(take);
     if (take) {
       const int pos = sel_before + __popcll(tm & below);
       sel_blk[pos] = c0 + i;
-      if (sel_page) sel_page[pos] = page[k];
+      if (sel_page) sel_page[pos] = wc.page[k];
     }
     sel_before += __popcll(tm);
     ties_before += __popcll(eqm);
@@ -200,14 +379,13 @@ __device__ __forceinline__ void wave_topk_s(const float* __restrict__ srow,
 }
 
 // S = smallest power of two with 64 * S >= nc (nc <= 64 * kSelKeysPerLane)
-__device__ __forceinline__ void wave_topk(const float* __restrict__ srow,
-                                          const int32_t* __restrict__ bt, int c0, int nc, int K,
-                                          int* sel_blk, int* sel_page) {
-  if (nc <= 64) wave_topk_s<1>(srow, bt, c0, nc, K, sel_blk, sel_page);
-  else if (nc <= 128) wave_topk_s<2>(srow, bt, c0, nc, K, sel_blk, sel_page);
-  else if (nc <= 256) wave_topk_s<4>(srow, bt, c0, nc, K, sel_blk, sel_page);
-  else if (nc <= 512) wave_topk_s<8>(srow, bt, c0, nc, K, sel_blk, sel_page);
-  else wave_topk_s<16>(srow, bt, c0, nc, K, sel_blk, sel_page);
+__device__ __forceinline__ void wave_topk(const WaveCand& wc, int c0, int nc, int K, int* sel_blk,
+                                          int* sel_page, uint32_t* ws) {
+  if (nc <= 64) wave_topk_s<1>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else if (nc <= 128) wave_topk_s<2>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else if (nc <= 256) wave_topk_s<4>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else if (nc <= 512) wave_topk_s<8>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else wave_topk_s<16>(wc, c0, nc, K, sel_blk, sel_page, ws);
 }
 
 // Block in output slot p of the selection for nb blocks: sinks [0, ns),
@@ -319,8 +497,8 @@ template <int TB, int W, bool SEL>
 __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, int seq, int len,
                                             int split, int wave, int lane,
                                             int32_t* __restrict__ idx,
-                                            const float* __restrict__ scores, int* s_sel,
-                                            int* s_selp, int& j_out, int& page_out) {
+                                            const WaveCand* wc, int* s_sel, int* s_selp,
+                                            uint32_t* s_ws, int& j_out, int& page_out) {
   const int slot = split * W + wave;
   int j = -1, page = -1;
   if constexpr (SEL) {
@@ -335,7 +513,7 @@ __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, 
       if (j >= 0) page = uniform(bt[j]);
     }
     if (ranked && K > 0) {  // one wave selects, the workgroup shares the result
-      if (wave == 0) wave_topk(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, bt, c0, nc, K, s_sel, s_selp);
+      if (wave == 0) wave_topk(*wc, c0, nc, K, s_sel, s_selp, s_ws);
       __syncthreads();
       if (picked) {
         j = s_sel[slot - geo.ns];

@@ -12,8 +12,8 @@
 //
 // Bit-exact parts (summary, score, selection) use __fadd_rn / __fmul_rn so
 // the compiler cannot contract or reorder them; the order is the one the
-// oracle states (sequential token fold; 16 chunks of 8 dims, then an xor
-// butterfly 1, 2, 4, 8; max over the GQA group scanning upward).
+// oracle states (sequential token fold; 16 chunks of 8 dims, then the
+// pairwise tree over chunks; max over the GQA group scanning upward).
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -141,15 +141,19 @@ __global__ __launch_bounds__(64) void k_topk(Geometry geo, SeqBatch sb,
                                              const float* __restrict__ scores,
                                              int32_t* __restrict__ idx_out) {
   __shared__ int s_sel[kSelMaxK];
+  __shared__ __align__(16) uint32_t s_ws[kWaveScratch];
   const int lane = threadIdx.x;
   const int h = blockIdx.x, bi = blockIdx.y;
   const int seq = sb.ids[bi];
+  const int c0 = geo.ns;
+  WaveCand wc;
+  wave_cand_load(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, nullptr, c0, geo.mbps, wc);
   const int len = geo.meta[seq];
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
-  const int c0 = geo.ns, nc = nb - geo.nr - c0;
+  const int nc = nb - geo.nr - c0;
   const bool ranked = ranked_select(geo, nc);
   int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
-  if (ranked) wave_topk(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, nullptr, c0, nc, geo.top_k, s_sel, nullptr);
+  if (ranked) wave_topk(wc, c0, nc, geo.top_k, s_sel, nullptr, s_ws);
   for (int p = lane; p < geo.nsel_max; p += 64)
     out[p] = selected_block(p, nb, ranked, geo.ns, geo.nr, geo.top_k, s_sel);
 }
@@ -190,6 +194,7 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   __shared__ float s_o[W][G][kHeadDim];
   __shared__ int s_sel[SEL ? kSelMaxK : 1];
   __shared__ int s_selp[SEL ? kSelMaxK : 1];
+  __shared__ __align__(16) uint32_t s_ws[SEL ? kWaveScratch : 4];
   const int split = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
@@ -202,9 +207,17 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = *(const u32x4*)(src + 32 * s);
   }
+  // the selecting wave loads every candidate's score and page before the
+  // sequence length is known
+  WaveCand wc;
+  if constexpr (SEL) {
+    if (wave == 0)
+      wave_cand_load(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, block_table(geo, seq), geo.ns,
+                     geo.mbps, wc);
+  }
   const int len = uniform(geo.meta[seq]);
   int j, page;
-  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, scores, s_sel, s_selp, j, page);
+  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, &wc, s_sel, s_selp, s_ws, j, page);
   if (j >= 0) {
     const int valid = min(TB, len - j * TB);
     const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;

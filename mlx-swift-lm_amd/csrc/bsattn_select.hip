@@ -2,11 +2,12 @@
 // one wave's worth of candidates) and wide GQA groups.
 //
 // k_select: one 1024-thread workgroup per (kv head, sequence).  Thread t owns
-// the contiguous candidates [t*per, t*per + per) (per <= 12) with their keys
-// in registers; the K-th largest key is found by a range-adaptive radix
-// select (a 2048-bin LDS histogram of the keys' range, refined inside the
-// bin that holds the K-th key, which one wave resolves once it holds at most
-// 64 keys).  Ties at the K-th key go to the lowest indices (a workgroup scan
+// the contiguous candidates [t*PER, t*PER + PER) with their keys in
+// registers (PER = 1, 2, 4, 8 or 12, the smallest that covers the batch:
+// every pass over the keys costs in proportion to PER); the K-th largest
+// key is found by a range-adaptive radix select (a 2048-bin LDS histogram
+// of the keys' range, refined inside the bin that holds the K-th key, which
+// one wave resolves once it holds at most 64 keys).  Ties at the K-th key go to the lowest indices (a workgroup scan
 // over the owners' segments), and the output is compacted in ascending
 // block order.
 //
@@ -18,7 +19,8 @@
 // s~ + e < s_K - e certainly is not, and only the blocks in between (the
 // band) are rescored in the canonical order; the remaining places go to the
 // best of the band by (exact score, index).  The selection is therefore the
-// canonical one, bit for bit.
+// canonical one, bit for bit.  (A block whose approximate score is not
+// finite has no bound; if there is one, every candidate is rescored.)
 //
 // Bound: products of fp16 / bf16 pairs are exact or within one rounding in
 // fp32; the canonical order adds 11 roundings and any fp32 accumulation of
@@ -36,16 +38,11 @@
 
 namespace bsattn {
 
-constexpr int kMfmaChunk = 256;   // candidate blocks per MFMA-scoring workgroup
+constexpr int kMfmaTiles = 4;     // 16-block tiles per MFMA-scoring wave
+constexpr int kMfmaChunk = 4 * 16 * kMfmaTiles;  // candidate blocks per MFMA-scoring workgroup
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
-constexpr int kSelPer = 12;       // candidates per thread: mbps <= 12288
-
-// inverse of score_key; key 0 (NaN) -> -inf
-__device__ __forceinline__ float key_value(uint32_t key) {
-  if (key == 0u) return -INFINITY;
-  return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
-}
+constexpr int kSelPerMax = 12;    // candidates per thread: mbps <= 12288
 
 __device__ __forceinline__ u32x4 abs16x8(u32x4 v) {
   return u32x4{v[0] & 0x7FFF7FFFu, v[1] & 0x7FFF7FFFu, v[2] & 0x7FFF7FFFu, v[3] & 0x7FFF7FFFu};
@@ -59,7 +56,8 @@ __device__ __forceinline__ float max16(float x) {  // over the 16 lanes of a row
 
 // ---------------------------------------------------------------------------
 // MFMA scoring (G >= 8): workgroup (chunk, kv head, sequence) handles
-// kMfmaChunk candidate blocks; each wave takes 16-block tiles:
+// kMfmaChunk candidate blocks; each wave takes kMfmaTiles 16-block tiles
+// (the query operand is loaded once per wave):
 //   S^T[block][head] = Summ[block][:] . Q[head][:]   (A = summary rows, B = Q^T)
 // plus the same product on magnitudes and Summ . 1 on magnitudes for the
 // bound.  Writes the approximate score (max over the group) of every
@@ -104,23 +102,27 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
   const float q1max = max16(q1[0]);
   float emax = 0.0f;
   float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
-  const uint16_t* sbase = summary_row(geo, seq, h, 0) + 8 * g;
-  const int jbase = c0 + chunk * kMfmaChunk;
-#pragma unroll 1
-  for (int it = 0; it < kMfmaChunk / 64; ++it) {
-    const int j0 = jbase + (4 * it + wave) * 16;
-    if (j0 >= c1) break;
-    // rows past the candidates (still inside the table) are read, not used
-    const int jr = min(j0 + n, geo.mbps - 1);
-    const uint16_t* row = sbase + (size_t)jr * kHeadDim;
-    u32x4 af[4];
+  // this wave's kMfmaTiles consecutive 16-block tiles; every load is issued
+  // first (rows past the candidates, still inside the table, are read and
+  // not used)
+  const int jw = c0 + chunk * kMfmaChunk + wave * 16 * kMfmaTiles;
+  u32x4 af[kMfmaTiles][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) af[s] = *(const u32x4*)(row + 32 * s);
+  for (int t = 0; t < kMfmaTiles; ++t) {
+    const int jr = min(jw + 16 * t + n, geo.mbps - 1);
+    const uint16_t* row = summary_row(geo, seq, h, jr) + 8 * g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) af[t][s] = *(const u32x4*)(row + 32 * s);
+  }
+#pragma unroll
+  for (int t = 0; t < kMfmaTiles; ++t) {
+    const int j0 = jw + 16 * t;
+    if (j0 >= c1) break;
     f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f}, a = d, k1 = d;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4 ab = abs16x8(af[s]);
-      d = mfma16x16x32<DT>(af[s], qf[s], d);
+      const u32x4 ab = abs16x8(af[t][s]);
+      d = mfma16x16x32<DT>(af[t][s], qf[s], d);
       a = mfma16x16x32<DT>(ab, qa[s], a);
       k1 = mfma16x16x32<DT>(ab, ones, k1);
     }
@@ -207,42 +209,50 @@ struct SelScratch {
   uint32_t s_red[2][kSelWaves];
 };
 
-// The K-th largest of the workgroup's valid keys (bit p of vmask: kr[p]
-// valid), 1 <= K <= number of valid keys.  Range-adaptive radix select: the
-// keys in [lo, hi] are histogrammed into 2048 bins of width 2^s, the bin
-// holding the K-th largest becomes the new range, until the range is one
-// value or its bin holds at most 64 keys, which one wave then resolves by
-// a bitwise search of their offsets.  Each refinement divides the range by
-// 2048, so there are at most three.  *gt = valid keys > the result;
-// *eq = valid keys equal to it.
-__device__ uint32_t wg_kth(const uint32_t (&kr)[kSelPer], uint32_t vmask, int K, SelScratch& ss,
-                           int* gt, int* eq) {
+// The K-th largest of the workgroup's nvalid valid keys (bit p of vmask:
+// kr[p] valid), 1 <= K <= nvalid.  Range-adaptive radix select: the keys in
+// [lo, hi] are histogrammed into 2048 LDS bins, the bin holding the K-th
+// largest becomes the new range, until the range is one value or its bin
+// holds at most 64 keys, which one wave then resolves by a bitwise search of
+// their offsets.  The first pass bins by score value (scores cluster in a
+// few binary exponents, so key bits would crowd them into a few bins); later
+// passes bin by key bits, dividing the range by 2048 each time.
+// *gt = valid keys > the result, *eq = valid keys equal to it.
+template <int PER>
+__device__ uint32_t wg_kth(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid, int K,
+                           SelScratch& ss, int* gt, int* eq) {
   const int tid = threadIdx.x, lane = tid & 63;
+  for (int b = tid; b < kHistBins; b += kSelThreads) ss.hist[b] = 0u;
+  if (tid == 0) ss.misc[3] = 0;
   uint32_t lo = 0xFFFFFFFFu, hi = 0u;
 #pragma unroll
-  for (int p = 0; p < kSelPer; ++p)
+  for (int p = 0; p < PER; ++p)
     if ((vmask >> p) & 1u) {
       lo = min(lo, kr[p]);
       hi = max(hi, kr[p]);
     }
-  wg_minmax(lo, hi, ss.s_red);
-  int need = K, above = 0;
+  wg_minmax(lo, hi, ss.s_red);  // its barriers also order the zeroing above
+  int need = K, above = 0, rcnt = nvalid;
+  bool by_value = true;
   uint32_t tau;
 #pragma unroll 1
   while (true) {
     if (lo == hi) {  // every remaining key has one value
       tau = lo;
       *gt = above;
-      *eq = -1;  // unknown here; computed below when asked for
+      *eq = rcnt;
       break;
     }
-    const int s = max(0, 32 - __clz(hi - lo) - 11);  // (hi - lo) >> s < 2048
-    for (int b = tid; b < kHistBins; b += kSelThreads) ss.hist[b] = 0u;
-    if (tid == 0) ss.misc[3] = 0;
-    __syncthreads();
+    const float vlo = key_value(lo), span = key_value(hi) - vlo;
+    const bool use_v = by_value && __builtin_isfinite(vlo) && __builtin_isfinite(span) && span > 0.0f;
+    const float scale = use_v ? (float)(kHistBins - 1) / span : 0.0f;
+    const int sh = use_v ? 0 : max(0, 32 - __clz(hi - lo) - 11);  // (hi - lo) >> sh < 2048
+    auto bin = [&](uint32_t key) -> int {
+      return use_v ? min(kHistBins - 1, (int)((key_value(key) - vlo) * scale)) : (int)((key - lo) >> sh);
+    };
 #pragma unroll
-    for (int p = 0; p < kSelPer; ++p)
-      if (((vmask >> p) & 1u) && kr[p] >= lo && kr[p] <= hi) atomicAdd(&ss.hist[(kr[p] - lo) >> s], 1u);
+    for (int p = 0; p < PER; ++p)
+      if (((vmask >> p) & 1u) && kr[p] >= lo && kr[p] <= hi) atomicAdd(&ss.hist[bin(kr[p])], 1u);
     __syncthreads();
     // thread t owns bins 2047 - 2t and 2046 - 2t, so a scan in thread order
     // counts the keys in higher bins
@@ -263,36 +273,41 @@ __device__ uint32_t wg_kth(const uint32_t (&kr)[kSelPer], uint32_t vmask, int K,
     const int bstar = ss.misc[0], abv = ss.misc[1], cnt = ss.misc[2];
     above += abv;
     need -= abv;
-    const uint32_t nlo = lo + ((uint32_t)bstar << s);
-    const uint32_t span = (1u << s) - 1u;
-    hi = (hi - nlo < span) ? hi : nlo + span;
-    lo = nlo;
-    if (s == 0) {  // one-value bin
-      tau = lo;
+    rcnt = cnt;
+    if (!use_v && sh == 0) {  // one-value bin
+      tau = lo + (uint32_t)bstar;
       *gt = above;
       *eq = cnt;
       break;
     }
     if (cnt <= kSmall) {
-      // gather the bin's keys; one wave finds the need-th largest offset
+      // gather the bin's keys; one wave finds the need-th largest
 #pragma unroll
-      for (int p = 0; p < kSelPer; ++p)
-        if (((vmask >> p) & 1u) && kr[p] >= lo && kr[p] <= hi) ss.small[atomicAdd(&ss.misc[3], 1)] = kr[p];
+      for (int p = 0; p < PER; ++p)
+        if (((vmask >> p) & 1u) && kr[p] >= lo && kr[p] <= hi && bin(kr[p]) == bstar)
+          ss.small[atomicAdd(&ss.misc[3], 1)] = kr[p];
       __syncthreads();
       if (tid < 64) {
         const bool valid = lane < cnt;
-        const uint32_t x = valid ? ss.small[lane] - lo : 0u;
-        uint32_t t = 0u;
-        for (int bit = s - 1; bit >= 0; --bit) {
-          const uint32_t cand = t | (1u << bit);
-          if (__popcll(__ballot(valid && x >= cand)) >= need) t = cand;
+        const uint32_t x = valid ? ss.small[lane] : 0u;
+        uint32_t mn = valid ? x : 0xFFFFFFFFu, mx = x;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          mn = min(mn, (uint32_t)__shfl_xor(mn, o, 64));
+          mx = max(mx, (uint32_t)__shfl_xor(mx, o, 64));
         }
-        const int g = __popcll(__ballot(valid && x > t));
-        const int e = __popcll(__ballot(valid && x == t));
+        const uint32_t off = x - mn;
+        uint32_t t = 0u;
+        for (int bit = mx == mn ? -1 : 31 - __clz(mx - mn); bit >= 0; --bit) {
+          const uint32_t cand = t | (1u << bit);
+          if (__popcll(__ballot(valid && off >= cand)) >= need) t = cand;
+        }
+        const int gcount = __popcll(__ballot(valid && off > t));
+        const int ecount = __popcll(__ballot(valid && off == t));
         if (lane == 0) {
-          ss.misc[4] = (int)(lo + t);
-          ss.misc[5] = g;
-          ss.misc[6] = e;
+          ss.misc[4] = (int)(mn + t);
+          ss.misc[5] = gcount;
+          ss.misc[6] = ecount;
         }
       }
       __syncthreads();
@@ -301,30 +316,58 @@ __device__ uint32_t wg_kth(const uint32_t (&kr)[kSelPer], uint32_t vmask, int K,
       *eq = ss.misc[6];
       break;
     }
-    __syncthreads();  // misc / hist are rewritten by the next refinement
+    // refine to the bin's keys; the histogram is cleared for the next pass
+    // (every read of it is behind the barrier above)
+    for (int b = tid; b < kHistBins; b += kSelThreads) ss.hist[b] = 0u;
+    if (tid == 0) ss.misc[3] = 0;
+    if (use_v) {
+      uint32_t nlo = 0xFFFFFFFFu, nhi = 0u;
+#pragma unroll
+      for (int p = 0; p < PER; ++p)
+        if (((vmask >> p) & 1u) && kr[p] >= lo && kr[p] <= hi && bin(kr[p]) == bstar) {
+          nlo = min(nlo, kr[p]);
+          nhi = max(nhi, kr[p]);
+        }
+      wg_minmax(nlo, nhi, ss.s_red);
+      lo = nlo;
+      hi = nhi;
+    } else {
+      const uint32_t nlo = lo + ((uint32_t)bstar << sh);
+      const uint32_t span_k = (1u << sh) - 1u;
+      hi = (hi - nlo < span_k) ? hi : nlo + span_k;
+      lo = nlo;
+      __syncthreads();
+    }
+    by_value = false;
   }
   __syncthreads();  // ss is reused by the caller
   return tau;
 }
 
-// Marks the K largest valid keys (ties at the K-th to the lowest index, i.e.
-// thread order then p) in the returned bitmask; all when fewer are valid.
-__device__ uint32_t wg_topk_mask(const uint32_t (&kr)[kSelPer], uint32_t vmask, int K, SelScratch& ss) {
+// Marks the K largest of the nvalid valid keys (ties at the K-th to the
+// lowest index, i.e. thread order then p); all of them when K >= nvalid.
+template <int PER>
+__device__ uint32_t wg_topk_mask(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid, int K,
+                                 SelScratch& ss) {
   if (K <= 0) return 0u;
-  int nvalid_total;
-  (void)wg_scan_excl(__popc(vmask), ss.s_tmp, &nvalid_total);
-  if (nvalid_total <= K) return vmask;
+  if (nvalid <= K) return vmask;
   int gt, eq;
-  const uint32_t tau = wg_kth(kr, vmask, K, ss, &gt, &eq);
-  int ties = 0;
-#pragma unroll
-  for (int p = 0; p < kSelPer; ++p) ties += ((vmask >> p) & 1u) && kr[p] == tau;
-  int tie_total;
-  int rank = wg_scan_excl(ties, ss.s_tmp, &tie_total);
+  const uint32_t tau = wg_kth(kr, vmask, nvalid, K, ss, &gt, &eq);
   const int krem = K - gt;
   uint32_t take = 0u;
+  if (eq == krem) {  // every key equal to the K-th is taken
 #pragma unroll
-  for (int p = 0; p < kSelPer; ++p)
+    for (int p = 0; p < PER; ++p)
+      if (((vmask >> p) & 1u) && kr[p] >= tau) take |= 1u << p;
+    return take;
+  }
+  int ties = 0;
+#pragma unroll
+  for (int p = 0; p < PER; ++p) ties += ((vmask >> p) & 1u) && kr[p] == tau;
+  int tie_total;
+  int rank = wg_scan_excl(ties, ss.s_tmp, &tie_total);
+#pragma unroll
+  for (int p = 0; p < PER; ++p)
     if ((vmask >> p) & 1u) {
       if (kr[p] > tau) take |= 1u << p;
       else if (kr[p] == tau) {
@@ -340,7 +383,7 @@ __device__ uint32_t wg_topk_mask(const uint32_t (&kr)[kSelPer], uint32_t vmask, 
 // BAND: scores are the approximate MFMA scores with bounds in err (see the
 // top of this file); dynamic LDS then holds the band (u32 per candidate).
 // ---------------------------------------------------------------------------
-template <int DT, int G, bool BAND>
+template <int DT, int G, bool BAND, int PER>
 __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch sb,
                                                         const uint16_t* __restrict__ q,
                                                         const float* __restrict__ scores,
@@ -353,28 +396,33 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
   const int tid = threadIdx.x;
   const int h = blockIdx.x, bi = blockIdx.y;
   const int seq = sb.ids[bi];
+  const int c0 = geo.ns, K = geo.top_k;
+  // this thread's candidates: c0 + i0 + p, p < PER; their scores are loaded
+  // before the sequence length is known (rows are mbps wide)
+  const float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
+  const int i0 = tid * PER;
+  float sc[PER];
+#pragma unroll
+  for (int p = 0; p < PER; ++p) sc[p] = c0 + i0 + p < geo.mbps ? srow[c0 + i0 + p] : 0.0f;
   const int len = geo.meta[seq];
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
-  const int c0 = geo.ns, nc = nb - geo.nr - c0, K = geo.top_k;
+  const int nc = nb - geo.nr - c0;
   int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
   if (!ranked_select(geo, nc)) {  // every block is kept
     for (int p = tid; p < geo.nsel_max; p += kSelThreads) out[p] = p < nb ? p : -1;
     return;
   }
-  const float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
-  const int per = (nc + kSelThreads - 1) / kSelThreads;
-  const int i0 = tid * per;  // this thread's candidates: c0 + i0 + p, p < per, i0 + p < nc
-  uint32_t kr[kSelPer];
+  uint32_t kr[PER];
   uint32_t vmask = 0u;
 #pragma unroll
-  for (int p = 0; p < kSelPer; ++p) {
-    const bool v = p < per && i0 + p < nc;
-    kr[p] = v ? score_key(srow[c0 + i0 + p]) : 0u;
+  for (int p = 0; p < PER; ++p) {
+    const bool v = i0 + p < nc;
+    kr[p] = v ? score_key(sc[p]) : 0u;
     vmask |= (uint32_t)v << p;
   }
   uint32_t take;
   if constexpr (!BAND) {
-    take = wg_topk_mask(kr, vmask, K, ss);
+    take = wg_topk_mask(kr, vmask, nc, K, ss);
   } else {
     const uint32_t* qsrc = (const uint32_t*)(q + ((size_t)bi * geo.hq + h * G) * kHeadDim);
     for (int e = tid; e < G * kHeadDim / 2; e += kSelThreads) s_q[e] = qsrc[e];
@@ -389,34 +437,35 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
     }
     // K-th and (K+1)-th largest approximate keys
     int gt, eq;
-    const uint32_t t1 = wg_kth(kr, vmask, K, ss, &gt, &eq);
+    const uint32_t t1 = wg_kth(kr, vmask, nc, K, ss, &gt, &eq);
     e = __int_as_float(ss.misc[7]) * (1.0f + 0x1p-8f) + 0x1p-120f;
-    uint32_t t2;
-    {
-      int cnt_ge = 0;
+    uint32_t t2 = t1;
+    if (gt + eq <= K) {  // the (K+1)-th is below t1
       uint32_t below = 0u, unused = 0xFFFFFFFFu;
 #pragma unroll
-      for (int p = 0; p < kSelPer; ++p)
-        if ((vmask >> p) & 1u) {
-          cnt_ge += kr[p] >= t1;
-          if (kr[p] < t1) below = max(below, kr[p]);
-        }
-      int ge_total;
-      (void)wg_scan_excl(cnt_ge, ss.s_tmp, &ge_total);
+      for (int p = 0; p < PER; ++p)
+        if (((vmask >> p) & 1u) && kr[p] < t1) below = max(below, kr[p]);
       wg_minmax(unused, below, ss.s_red);
-      t2 = ge_total > K ? t1 : below;
+      t2 = below;
     }
     const float lb = key_value(t1) - e, ub = key_value(t2) + e;
-    // with non-finite bounds nothing is certain: every candidate is rescored
-    const bool bounds_ok = __builtin_isfinite(lb) && __builtin_isfinite(ub);
+    // a candidate whose approximate score is not finite has no bound (its
+    // exact score may exceed any other), and non-finite limits certify
+    // nothing: then every candidate is rescored
+    int nbad = 0;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) nbad += ((vmask >> p) & 1u) && !__builtin_isfinite(key_value(kr[p]));
+    int nbad_total;
+    (void)wg_scan_excl(nbad, ss.s_tmp, &nbad_total);
+    const bool bounds_ok = nbad_total == 0 && __builtin_isfinite(lb) && __builtin_isfinite(ub);
     // classify: certainly in (take), band (rescored), certainly out
     uint32_t band = 0u;
     take = 0u;
     int nin = 0, nband = 0;
 #pragma unroll
-    for (int p = 0; p < kSelPer; ++p)
+    for (int p = 0; p < PER; ++p)
       if ((vmask >> p) & 1u) {
-        const float v = srow[c0 + i0 + p];
+        const float v = key_value(kr[p]);  // the approximate score (NaN -> -inf)
         const bool sure = bounds_ok && __builtin_isfinite(v);
         if (sure && v - e > ub) {
           take |= 1u << p;
@@ -436,7 +485,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
       // band list, then the canonical score of every band block
       int w = bpos;
 #pragma unroll
-      for (int p = 0; p < kSelPer; ++p)
+      for (int p = 0; p < PER; ++p)
         if (band & (1u << p)) s_band[w++] = (uint32_t)(c0 + i0 + p);
       __syncthreads();
       const int c = tid & 15;
@@ -456,11 +505,11 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
         if (c == 0) s_band[bk] = score_key(best);  // the slot's index is no longer needed
       }
       __syncthreads();
-      uint32_t br[kSelPer];
+      uint32_t br[PER];
       w = bpos;
 #pragma unroll
-      for (int p = 0; p < kSelPer; ++p) br[p] = (band & (1u << p)) ? s_band[w++] : 0u;
-      take |= wg_topk_mask(br, band, krem, ss);
+      for (int p = 0; p < PER; ++p) br[p] = (band & (1u << p)) ? s_band[w++] : 0u;
+      take |= wg_topk_mask(br, band, nband_total, krem, ss);
     }
   }
   // output: sinks, the chosen candidates in index order, recent blocks
@@ -468,7 +517,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
   const int pos = wg_scan_excl(__popc(take), ss.s_tmp, &total);
   int w = geo.ns + pos;
 #pragma unroll
-  for (int p = 0; p < kSelPer; ++p)
+  for (int p = 0; p < PER; ++p)
     if (take & (1u << p)) out[w++] = c0 + i0 + p;
   for (int p = tid; p < geo.ns; p += kSelThreads) out[p] = p;
   for (int r = tid; r < geo.nr; r += kSelThreads) out[geo.ns + total + r] = nb - geo.nr + r;
@@ -481,6 +530,26 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
 // ===========================================================================
 int mfma_err_stride(const Geometry& g) { return (g.mbps + kMfmaChunk - 1) / kMfmaChunk; }
 
+template <int DT, int G, bool BAND>
+static void select_per(const Geometry& g, const SeqBatch& b, const uint16_t* q, const float* scores,
+                       const float* err, int stride, int chunks, int max_nc, int32_t* idx,
+                       hipStream_t s, Timing* prof) {
+  const int per = (max_nc + kSelThreads - 1) / kSelThreads;
+  const dim3 grid(g.hkv, b.n), blk(kSelThreads);
+  const size_t lds = BAND ? (size_t)g.mbps * 4 : 0;
+  if (per <= 1)
+    launch(k_select<DT, G, BAND, 1>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, idx);
+  else if (per <= 2)
+    launch(k_select<DT, G, BAND, 2>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, idx);
+  else if (per <= 4)
+    launch(k_select<DT, G, BAND, 4>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, idx);
+  else if (per <= 8)
+    launch(k_select<DT, G, BAND, 8>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, idx);
+  else
+    launch(k_select<DT, G, BAND, kSelPerMax>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride,
+           chunks, idx);
+}
+
 template <int DT, int G>
 static void select_wide(const Geometry& g, const SeqBatch& b, const uint16_t* q, float* scores,
                         float* err, int max_nc, int32_t* idx, hipStream_t s, Timing* prof) {
@@ -488,8 +557,7 @@ static void select_wide(const Geometry& g, const SeqBatch& b, const uint16_t* q,
   const int stride = mfma_err_stride(g);
   launch(k_score_mfma<DT, G>, dim3(chunks, g.hkv, b.n), dim3(256), 0, s, prof, kProfScore, g, b, q,
          scores, err, stride);
-  launch(k_select<DT, G, true>, dim3(g.hkv, b.n), dim3(kSelThreads), (size_t)g.mbps * 4, s, prof,
-         kProfTopk, g, b, q, (const float*)scores, (const float*)err, stride, chunks, idx);
+  select_per<DT, G, true>(g, b, q, scores, err, stride, chunks, max_nc, idx, s, prof);
 }
 
 hipError_t launch_select_large(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
@@ -507,12 +575,8 @@ hipError_t launch_select_large(const Geometry& g, const SeqBatch& b, const void*
     return hipGetLastError();
   }
   // exact scores already in `scores`
-  if (g.dtype == 0)
-    launch(k_select<0, 1, false>, dim3(g.hkv, b.n), dim3(kSelThreads), 0, s, prof, kProfTopk, g, b,
-           qq, (const float*)scores, (const float*)nullptr, 0, 0, idx);
-  else
-    launch(k_select<1, 1, false>, dim3(g.hkv, b.n), dim3(kSelThreads), 0, s, prof, kProfTopk, g, b,
-           qq, (const float*)scores, (const float*)nullptr, 0, 0, idx);
+  if (g.dtype == 0) select_per<0, 1, false>(g, b, qq, scores, nullptr, 0, 0, max_nc, idx, s, prof);
+  else select_per<1, 1, false>(g, b, qq, scores, nullptr, 0, 0, max_nc, idx, s, prof);
   return hipGetLastError();
 }
 

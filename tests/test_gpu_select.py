@@ -93,3 +93,35 @@ def test_wide_group_ties_and_duplicates(gpu, dtype):
     idx = cache.selectBlocks(q).cpu().numpy()
     nb = lens[0] // Tb
     assert list(idx[0, 0][:52]) == list(range(51)) + [nb - 4]
+
+
+@pytest.mark.parametrize("T_blocks,Hq,Hkv,K", [(300, 32, 8, 20), (2500, 32, 8, 40), (1500, 64, 4, 30)])
+def test_nonfinite_scores_select_like_oracle(gpu, T_blocks, Hq, Hkv, K):
+    """Keys holding +-inf give infinite or NaN block scores (NaN sorts lowest,
+    -0 == +0); selection stays bit-exact on the one-wave, workgroup and
+    MFMA-band paths.  Indices only: the attention of such keys is NaN."""
+    import torch
+    Tb = 64
+    w = make_workload(5300 + T_blocks + Hq, B=2, Hq=Hq, Hkv=Hkv, T=T_blocks * Tb, Tb=Tb, dtype="f16",
+                      top_k=K, ns=1, nr=2)
+    rng = np.random.default_rng(T_blocks)
+    for b in range(w.B):
+        for h in range(w.Hkv):
+            for j in rng.choice(T_blocks - 4, 6, replace=False) + 1:
+                w.keys[b][h][j * Tb + 3, rng.integers(0, 128)] = 0x7C00        # +inf
+            for j in rng.choice(T_blocks - 4, 4, replace=False) + 1:
+                w.keys[b][h][j * Tb + 5, rng.integers(0, 128)] = 0xFC00        # -inf
+            j = int(rng.integers(1, T_blocks - 4))
+            w.keys[b][h][j * Tb + 1, 7] = 0x7C00                                # +inf and -inf: NaN
+            w.keys[b][h][j * Tb + 2, 7] = 0xFC00
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    q = to_dev(w.q[:, :, None, :], w.dtype, gpu)
+    idx_ref, _ = oracle_decode(w)
+    idx = cache.selectBlocks(q)
+    idx2 = torch.empty_like(idx)
+    cache.decode(q, w.scale, idx_out=idx2)
+    torch.cuda.synchronize()
+    got = idx.cpu().numpy()
+    assert np.array_equal(got, idx_ref), f"differ at {np.argwhere(got != idx_ref)[:5]}"
+    assert np.array_equal(idx2.cpu().numpy(), idx_ref)
