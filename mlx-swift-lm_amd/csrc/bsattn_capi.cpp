@@ -399,8 +399,10 @@ int append_impl(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t
     sb.n = ab.n;
     Timing tm[kProfKinds];
     Timing* prof = prof_slots(c, s, tm);
-    hipError_t e = kernels(ab, (size_t)i0, prof);
-    if (e == hipSuccess && max_count > 0) e = launch_summary(c->geo, sb, max_count, s, prof);
+    // one token into a 16-bit cache: the append kernel writes the summaries
+    const bool fused = n_tokens == 1 && c->d.kv_bits == 0;
+    hipError_t e = kernels(ab, (size_t)i0, fused, prof);
+    if (e == hipSuccess && max_count > 0 && !fused) e = launch_summary(c->geo, sb, max_count, s, prof);
     prof_collect(c, prof);
     if (e != hipSuccess) return hip_fail(e, "append launch");
   }
@@ -414,11 +416,12 @@ int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* 
   hipStream_t s = (hipStream_t)stream;
   const size_t row = (size_t)c->geo.hkv * n_tokens * kHeadDim;  // elements per sequence
   const bool quant = c->d.kv_bits != 0;
-  return append_impl(c, seq_ids, n_seqs, n_tokens, s, [&](const AppendBatch& ab, size_t i0, Timing* prof) {
+  return append_impl(c, seq_ids, n_seqs, n_tokens, s, [&](const AppendBatch& ab, size_t i0, bool fused,
+                                                           Timing* prof) {
     const uint16_t* kk = (const uint16_t*)k + i0 * row;
     const uint16_t* vv = (const uint16_t*)v + i0 * row;
     return quant ? launch_append_q16(c->geo, ab, kk, vv, s, prof)
-                 : launch_append(c->geo, ab, kk, vv, s, prof);
+                 : launch_append(c->geo, ab, kk, vv, fused, s, prof);
   });
 }
 
@@ -431,7 +434,8 @@ int bsattn_append_quantized(bsattn_cache* c, const uint32_t* k_w, const void* k_
   hipStream_t s = (hipStream_t)stream;
   const size_t rows = (size_t)c->geo.hkv * n_tokens;  // token rows per sequence
   const size_t words = kHeadDim * c->d.kv_bits / 32, groups = kHeadDim / c->d.group_size;
-  return append_impl(c, seq_ids, n_seqs, n_tokens, s, [&](const AppendBatch& ab, size_t i0, Timing* prof) {
+  return append_impl(c, seq_ids, n_seqs, n_tokens, s, [&](const AppendBatch& ab, size_t i0, bool,
+                                                           Timing* prof) {
     const size_t wo = i0 * rows * words, go = i0 * rows * groups;
     return launch_append_quantized(c->geo, ab, k_w + wo, (const uint16_t*)k_s + go,
                                    (const uint16_t*)k_b + go, v_w + wo, (const uint16_t*)v_s + go,

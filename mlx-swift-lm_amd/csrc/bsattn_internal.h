@@ -15,7 +15,7 @@ constexpr int kMaxPatch = 240;  // metadata words patched per launch
 #define BSATTN_WAVES 4
 #endif
 constexpr int kWaves = BSATTN_WAVES;  // waves per attention workgroup (one block each)
-constexpr int kMaxSplits = 256;       // attention splits per (sequence, kv head)
+constexpr int kMaxSplits = 512;       // attention splits per (sequence, kv head)
 
 // Static geometry of one cache, copied into every launch.
 struct Geometry {
@@ -74,8 +74,10 @@ struct Timing {
 
 // launchers (bsattn_kernels.hip); return hipError_t of the launch
 hipError_t launch_patch(const Geometry& g, const PatchBatch& pb, hipStream_t s);
+// fuse_summary (one token per sequence): blocks completed by the append get
+// their summary from the append kernel itself (no launch_summary needed)
 hipError_t launch_append(const Geometry& g, const AppendBatch& ab, const void* k,
-                         const void* v, hipStream_t s, Timing* prof);
+                         const void* v, bool fuse_summary, hipStream_t s, Timing* prof);
 // quantized caches (bsattn_quant.hip): append from fp16 (quantize on append)
 // or from the MLX layout; block summaries of dequantized keys; attention
 hipError_t launch_append_q16(const Geometry& g, const AppendBatch& ab, const void* k,

@@ -29,12 +29,42 @@ __global__ __launch_bounds__(256) void k_patch(int32_t* meta, PatchBatch pb) {
 }
 
 // ---------------------------------------------------------------------------
-// append: 16 tokens x 16 lanes (8 dims each) per workgroup
+// block summary of one (block, kv head) by the 16 lanes that own its dims
+// 8c .. 8c+7: sequential fp32 fold over the block's tokens from token 0,
+// times 1/Tb, rounded to the cache dtype.  Each lane reads 16 contiguous
+// bytes per token (its chunk of the fragment-major K tile).
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ void summary16(const Geometry& geo, const uint16_t* __restrict__ Kt, int c,
+                                          uint16_t* __restrict__ dst) {
+  float acc[8];
+  unpack8<DT>(*(const u32x4*)(Kt + k_elem(0, 8 * c)), acc);
+#pragma unroll 8
+  for (int t = 1; t < geo.tb; ++t) {
+    float x[8];
+    unpack8<DT>(*(const u32x4*)(Kt + k_elem(t, 8 * c)), x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = __fadd_rn(acc[e], x[e]);
+  }
+  const float inv = 1.0f / (float)geo.tb;
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack2<DT>(__fmul_rn(acc[2 * e], inv), __fmul_rn(acc[2 * e + 1], inv));
+  *(u32x4*)(dst + 8 * c) = o;
+}
+
+// ---------------------------------------------------------------------------
+// append: 16 tokens x 16 lanes (8 dims each) per workgroup.  With
+// fuse_summary (one token per sequence), the 16 lanes of a token that fills
+// its block also write the block's summary: every K chunk a lane folds was
+// written by that lane itself or by an earlier launch.
 // grid (ceil(L/16), Hkv, n)
 // ---------------------------------------------------------------------------
+template <int DT>
 __global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
                                                 const uint16_t* __restrict__ k,
-                                                const uint16_t* __restrict__ v) {
+                                                const uint16_t* __restrict__ v, bool fuse_summary) {
   const int bi = blockIdx.z, h = blockIdx.y;
   const int tok = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int c = threadIdx.x & 15;
@@ -48,34 +78,33 @@ __global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
   const u32x4 vr = *(const u32x4*)(v + src);
   uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
   // dims 8c .. 8c+7 of a key are 16 contiguous bytes of the K tile
-  *(u32x4*)((uint16_t*)(slab + geo.k_off) + k_elem(slot, 8 * c)) = kr;
+  uint16_t* Kt = (uint16_t*)(slab + geo.k_off);
+  *(u32x4*)(Kt + k_elem(slot, 8 * c)) = kr;
   uint16_t* Vt = (uint16_t*)(slab + geo.v_off);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const uint32_t w = vr[e >> 1];
     Vt[v_elem(geo.tb, slot, 8 * c + e)] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xFFFFu));
   }
+  if (fuse_summary && slot == geo.tb - 1) summary16<DT>(geo, Kt, c, summary_row(geo, seq, h, blk));
 }
 
 // ---------------------------------------------------------------------------
-// block summary: one workgroup per (block, kv head, sequence), one thread
-// per dim; sequential fp32 fold over the block's tokens, times 1/Tb.
-// Summaries are stored by logical block: summ[seq][kv head][block][D].
-// grid (max_count, Hkv, n)
+// block summaries of the blocks completed by an append: 4 (block, kv head)
+// pairs per 64-thread workgroup, 16 lanes each.  Summaries are stored by
+// logical block: summ[seq][kv head][block][D].
+// grid (max_count, ceil(Hkv / 4), n)
 // ---------------------------------------------------------------------------
 template <int DT>
-__global__ __launch_bounds__(128) void k_summary(Geometry geo, SummaryBatch sb) {
-  const int bi = blockIdx.z, h = blockIdx.y;
-  if ((int)blockIdx.x >= sb.count[bi]) return;
+__global__ __launch_bounds__(64) void k_summary(Geometry geo, SummaryBatch sb) {
+  const int bi = blockIdx.z;
+  const int h = blockIdx.y * 4 + (threadIdx.x >> 4), c = threadIdx.x & 15;
+  if ((int)blockIdx.x >= sb.count[bi] || h >= geo.hkv) return;
   const int seq = sb.seq[bi];
   const int j = sb.first[bi] + blockIdx.x;
   const int page = block_table(geo, seq)[j];
-  const int d = threadIdx.x;
   const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
-  const uint16_t* Kt = (const uint16_t*)(slab + geo.k_off);
-  float acc = to_f32<DT>(Kt[k_elem(0, d)]);
-  for (int t = 1; t < geo.tb; ++t) acc = __fadd_rn(acc, to_f32<DT>(Kt[k_elem(t, d)]));
-  summary_row(geo, seq, h, j)[d] = from_f32<DT>(__fmul_rn(acc, 1.0f / (float)geo.tb));
+  summary16<DT>(geo, (const uint16_t*)(slab + geo.k_off), c, summary_row(geo, seq, h, j));
 }
 
 // ---------------------------------------------------------------------------
@@ -397,21 +426,22 @@ hipError_t launch_patch(const Geometry& g, const PatchBatch& pb, hipStream_t s) 
 }
 
 hipError_t launch_append(const Geometry& g, const AppendBatch& ab, const void* k, const void* v,
-                         hipStream_t s, Timing* prof) {
+                         bool fuse_summary, hipStream_t s, Timing* prof) {
   dim3 grid((ab.L + 15) / 16, g.hkv, ab.n);
-  launch(k_append, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, (const uint16_t*)k,
-         (const uint16_t*)v);
+  const uint16_t *kk = (const uint16_t*)k, *vv = (const uint16_t*)v;
+  if (g.dtype == 0) launch(k_append<0>, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, kk, vv, fuse_summary);
+  else launch(k_append<1>, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, kk, vv, fuse_summary);
   return hipGetLastError();
 }
 
 hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
                           hipStream_t s, Timing* prof) {
   if (g.kv_bits != 0) return launch_summary_q(g, sb, max_count, s, prof);
-  dim3 grid(max_count, g.hkv, sb.n);
+  dim3 grid(max_count, (g.hkv + 3) / 4, sb.n);
   if (g.dtype == 0)
-    launch(k_summary<0>, grid, dim3(128), 0, s, prof, kProfSummary, g, sb);
+    launch(k_summary<0>, grid, dim3(64), 0, s, prof, kProfSummary, g, sb);
   else
-    launch(k_summary<1>, grid, dim3(128), 0, s, prof, kProfSummary, g, sb);
+    launch(k_summary<1>, grid, dim3(64), 0, s, prof, kProfSummary, g, sb);
   return hipGetLastError();
 }
 
