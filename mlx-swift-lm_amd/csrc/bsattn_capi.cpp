@@ -51,7 +51,7 @@ struct bsattn_cache {
   Geometry geo{};
   int64_t num_pages = 0;
   size_t pool_bytes = 0, summ_bytes = 0, meta_words = 0;
-  float* scores = nullptr;    // [max_seqs][hkv][mbps]
+  float* scores = nullptr;    // [max_seqs][hkv][sstride] + kScoreSlack
   int32_t* idx_ws = nullptr;  // [max_seqs][hkv][nsel_max]
   float* partials = nullptr;  // [max_seqs][hq][nsplit][D + 2]
   float* err_ws = nullptr;    // [max_seqs][hkv][mfma_err_stride]: MFMA score bounds
@@ -282,6 +282,7 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   g.nsel_max = d.top_k + d.sink_blocks + d.recent_blocks;
   g.nsplit = (g.nsel_max + kWaves - 1) / kWaves;
   g.mbps = d.max_blocks_per_seq;
+  g.sstride = (g.mbps + 63) & ~63;
   g.bt_off = d.max_seqs;
   // slab: K tile then V tile (16-bit elements, or b-bit codes), then for
   // quantized caches 16 B of scales / biases per token
@@ -307,7 +308,7 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   if ((e = hipMalloc((void**)&g.pool, c->pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(pool)"));
   if ((e = hipMalloc((void**)&g.summ, c->summ_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(summaries)"));
   if ((e = hipMalloc((void**)&g.meta, c->meta_words * 4)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(meta)"));
-  if ((e = hipMalloc((void**)&c->scores, (size_t)d.max_seqs * g.hkv * g.mbps * 4)) != hipSuccess)
+  if ((e = hipMalloc((void**)&c->scores, ((size_t)d.max_seqs * g.hkv * g.sstride + kScoreSlack) * 4)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMalloc(scores)"));
   if ((e = hipMalloc((void**)&c->idx_ws, (size_t)d.max_seqs * g.hkv * g.nsel_max * 4)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMalloc(indices)"));
@@ -455,7 +456,7 @@ static int do_select(bsattn_cache* c, const void* q, const std::vector<int32_t>&
       max_nc = std::max(max_nc, candidates(c->geo, c->len[b.ids[i]]));
     }
     const uint16_t* qq = (const uint16_t*)q + (size_t)i0 * c->geo.hq * kHeadDim;
-    float* sc = c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps;
+    float* sc = c->scores + (size_t)i0 * c->geo.hkv * c->geo.sstride;
     int32_t* io = idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max;
     Timing tm[kProfKinds];
     Timing* prof = prof_slots(c, s, tm);
@@ -541,7 +542,7 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
     Timing tm[kProfKinds];
     Timing* prof = prof_slots(c, s, tm);
     hipError_t e = launch_decode(c->geo, b, (const char*)q + qoff,
-                                 c->scores + (size_t)i0 * c->geo.hkv * c->geo.mbps,
+                                 c->scores + (size_t)i0 * c->geo.hkv * c->geo.sstride,
                                  idx_out ? idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max : nullptr,
                                  max_nc, scale, (char*)out + qoff,
                                  c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2),

@@ -55,6 +55,9 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
 }
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+// An empty use of a uniform value at this point: its load is issued here
+// rather than sunk into a later branch behind other waits.
+__device__ __forceinline__ void issue_here(int x) { asm volatile("" ::"s"(x)); }
 
 __device__ __forceinline__ const int32_t* block_table(const Geometry& g, int seq) {
   return g.meta + g.bt_off + (size_t)seq * g.mbps;
@@ -87,6 +90,16 @@ __host__ __device__ inline int v_elem(int tb, int tok, int d) {
 
 // ---------------------------------------------------------------------------
 // metadata patch: meta[idx[i]] = val[i]
+// Block-score row of (batch entry bi, kv head h): sstride floats, entry j =
+// block j (only candidate blocks are written).
+__device__ __forceinline__ float* score_row(const Geometry& g, float* scores, int bi, int h) {
+  return scores + ((size_t)bi * g.hkv + h) * g.sstride;
+}
+__device__ __forceinline__ const float* score_row(const Geometry& g, const float* scores, int bi,
+                                                  int h) {
+  return scores + ((size_t)bi * g.hkv + h) * g.sstride;
+}
+
 __device__ __forceinline__ uint16_t* summary_row(const Geometry& g, int seq, int h, int j) {
   return g.summ + (((size_t)seq * g.hkv + h) * g.mbps + j) * kHeadDim;
 }
@@ -491,12 +504,19 @@ __host__ __device__ inline int sb_entry(int tb, int tok) {
 // entries alongside their scores, and shares blocks and pages through
 // s_sel / s_selp); forced slots load their page before the selection is
 // known.  Split 0 then writes the selected indices to idx (if not null).
-// Otherwise the block comes from idx; -1 and indices past the sequence's
-// last block contribute nothing.  Contains a workgroup barrier when SEL.
+// Otherwise the block is jg (given_index); -1 and indices past the
+// sequence's last block contribute nothing.  Contains a workgroup barrier
+// when SEL.
+// Block index of a slot in the given-index table (-1 past the table).
+__device__ __forceinline__ int given_index(const Geometry& geo, const int32_t* __restrict__ idx,
+                                           int bi, int h, int slot) {
+  return slot < geo.nsel_max ? idx[((size_t)bi * geo.hkv + h) * geo.nsel_max + slot] : -1;
+}
+
 template <int TB, int W, bool SEL>
 __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, int seq, int len,
                                             int split, int wave, int lane,
-                                            int32_t* __restrict__ idx,
+                                            int32_t* __restrict__ idx, int jg,
                                             const WaveCand* wc, int* s_sel, int* s_selp,
                                             uint32_t* s_ws, int& j_out, int& page_out) {
   const int slot = split * W + wave;
@@ -526,10 +546,14 @@ __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, 
         row[p] = selected_block(p, nb, ranked, geo.ns, geo.nr, K, s_sel);
     }
   } else {
-    if (slot < geo.nsel_max) j = idx[((size_t)bi * geo.hkv + h) * geo.nsel_max + slot];
-    j = uniform(j);
-    if (j >= geo.mbps || (int64_t)j * TB >= len) j = -1;
-    if (j >= 0) page = uniform(block_table(geo, seq)[j]);
+    // the page is requested before the length check: every j in [0, mbps)
+    // has an in-bounds table entry; other j read entry 0 and are dropped
+    j = uniform(jg);
+    const bool in_table = j >= 0 && j < geo.mbps;
+    const int pg = uniform(block_table(geo, seq)[in_table ? j : 0]);
+    issue_here(pg);
+    if (!in_table || (int64_t)j * TB >= len) j = -1;
+    if (j >= 0) page = uniform(pg);
   }
   j_out = uniform(j);
   page_out = uniform(page);

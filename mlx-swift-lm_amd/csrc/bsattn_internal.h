@@ -16,6 +16,10 @@ constexpr int kMaxPatch = 240;  // metadata words patched per launch
 #endif
 constexpr int kWaves = BSATTN_WAVES;  // waves per attention workgroup (one block each)
 constexpr int kMaxSplits = 512;       // attention splits per (sequence, kv head)
+// floats after the last block-score row: the workgroup selection reads a
+// thread's candidates as whole vectors, up to 12 x 1024 entries from a row
+// start, and the entries past the row are never candidates
+constexpr int kScoreSlack = 12 * 1024;
 
 // Static geometry of one cache, copied into every launch.
 struct Geometry {
@@ -26,6 +30,7 @@ struct Geometry {
   int32_t gsize;              // affine group size
   int32_t top_k, ns, nr, nsel_max, nsplit;
   int32_t mbps;               // block-table width
+  int32_t sstride;            // block-score row stride (mbps rounded up to 64)
   int32_t bt_off;             // offset of the block table inside meta
   int64_t slab_bytes;         // bytes of one (page, kv head) slab
   // byte offsets inside a slab: K tile (or K codes), V tile (or V codes),

@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int c1 = nb - geo.nr;
   if (!ranked_select(geo, c1 - geo.ns)) return;
-  float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
+  float* srow = score_row(geo, scores, bi, h);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int j = j0 + 16 * p;
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(64) void k_topk(Geometry geo, SeqBatch sb,
   const int seq = sb.ids[bi];
   const int c0 = geo.ns;
   WaveCand wc;
-  wave_cand_load(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, nullptr, c0, geo.mbps, wc);
+  wave_cand_load(score_row(geo, scores, bi, h), nullptr, c0, geo.mbps, wc);
   const int len = geo.meta[seq];
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int nc = nb - geo.nr - c0;
@@ -225,9 +225,12 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   __shared__ int s_selp[SEL ? kSelMaxK : 1];
   __shared__ __align__(16) uint32_t s_ws[SEL ? kWaveScratch : 4];
   const int split = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int seq = sb.ids[bi];
+  // given indices: the slot's block index heads the longest dependent chain
+  // (index -> page -> K/V), so it is requested before the length and Q
+  const int jg = SEL ? -1 : given_index(geo, idx, bi, h, split * W + wave);
   u32x4 qf[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
@@ -241,12 +244,13 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   WaveCand wc;
   if constexpr (SEL) {
     if (wave == 0)
-      wave_cand_load(scores + ((size_t)bi * geo.hkv + h) * geo.mbps, block_table(geo, seq), geo.ns,
+      wave_cand_load(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns,
                      geo.mbps, wc);
   }
   const int len = uniform(geo.meta[seq]);
   int j, page;
-  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, &wc, s_sel, s_selp, s_ws, j, page);
+  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, jg, &wc, s_sel, s_selp, s_ws, j,
+                          page);
   if (j >= 0) {
     const int valid = min(TB, len - j * TB);
     const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;

@@ -2,14 +2,14 @@
 // one wave's worth of candidates) and wide GQA groups.
 //
 // k_select: one 1024-thread workgroup per (kv head, sequence).  Thread t owns
-// the contiguous candidates [t*PER, t*PER + PER) with their keys in
-// registers (PER = 1, 2, 4, 8 or 12, the smallest that covers the batch:
-// every pass over the keys costs in proportion to PER); the K-th largest
-// key is found by a range-adaptive radix select (a 2048-bin LDS histogram
-// of the keys' range, refined inside the bin that holds the K-th key, which
-// one wave resolves once it holds at most 64 keys).  Ties at the K-th key go to the lowest indices (a workgroup scan
-// over the owners' segments), and the output is compacted in ascending
-// block order.
+// blocks [t*PER, t*PER + PER) of the score row (read as whole vectors), with
+// their keys in registers (PER = 1, 2, 4, 8 or 12, the smallest that covers
+// the batch: every pass over the keys costs in proportion to PER); the K-th
+// largest key is found by a range-adaptive radix select (a 2048-bin LDS
+// histogram of the keys' range, refined inside the bin that holds the K-th
+// key, which one wave resolves once it holds at most 64 keys).  Ties at the
+// K-th key go to the lowest indices (a workgroup scan over the owners'
+// segments), and the output is compacted in ascending block order.
 //
 // Wide groups (G >= 8): the block scores are first computed with MFMA
 // (k_score_mfma), which does not reproduce the canonical summation order.
@@ -18,7 +18,8 @@
 // scores, a block with s~ - e > s_K+1 + e is certainly selected, one with
 // s~ + e < s_K - e certainly is not, and only the blocks in between (the
 // band) are rescored in the canonical order; the remaining places go to the
-// best of the band by (exact score, index).  The selection is therefore the
+// best of the band by (exact score, index) (one wave decides a band of at
+// most 64 blocks).  The selection is therefore the
 // canonical one, bit for bit.  (A block whose approximate score is not
 // finite has no bound; if there is one, every candidate is rescored.)
 //
@@ -42,27 +43,41 @@ constexpr int kMfmaTiles = 4;     // 16-block tiles per MFMA-scoring wave
 constexpr int kMfmaChunk = 4 * 16 * kMfmaTiles;  // candidate blocks per MFMA-scoring workgroup
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
-constexpr int kSelPerMax = 12;    // candidates per thread: mbps <= 12288
+constexpr int kSelPerMax = 12;    // blocks per thread: mbps <= 12288
+static_assert(kSelPerMax * kSelThreads / kMfmaChunk <= 64, "one wave reads every chunk bound");
 
 __device__ __forceinline__ u32x4 abs16x8(u32x4 v) {
   return u32x4{v[0] & 0x7FFF7FFFu, v[1] & 0x7FFF7FFFu, v[2] & 0x7FFF7FFFu, v[3] & 0x7FFF7FFFu};
 }
 
-__device__ __forceinline__ float max16(float x) {  // over the 16 lanes of a row
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-  return x;
+// fmaxf over the wave's four 16-lane rows (lane l gets the maximum over
+// lanes l mod 16 + 16 r)
+__device__ __forceinline__ float max_rows(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = fmaxf(__uint_as_float((uint32_t)a[0]), __uint_as_float((uint32_t)a[1]));
+  const uint32_t v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float((uint32_t)b[0]), __uint_as_float((uint32_t)b[1]));
+}
+
+// fmaxf over the whole wave
+__device__ __forceinline__ float wave_max_f32(float x) {
+  return __uint_as_float(wave_allreduce_u32(__float_as_uint(x), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
 }
 
 // ---------------------------------------------------------------------------
 // MFMA scoring (G >= 8): workgroup (chunk, kv head, sequence) handles
 // kMfmaChunk candidate blocks; each wave takes kMfmaTiles 16-block tiles
 // (the query operand is loaded once per wave):
-//   S^T[block][head] = Summ[block][:] . Q[head][:]   (A = summary rows, B = Q^T)
-// plus the same product on magnitudes and Summ . 1 on magnitudes for the
-// bound.  Writes the approximate score (max over the group) of every
-// candidate and the chunk's bound to err[seq row][chunk].
-// grid (chunks, Hkv, n)
+//   S[head][block] = Q[head][:] . Summ[block][:]   (A = Q, B = summary rows^T)
+// so that lane (block n, group g) holds heads 4g .. 4g+3 of block n and the
+// maximum over the group is taken in-lane and across the four lane groups;
+// plus the same product on magnitudes and 1 . |Summ| for the bound.  Writes
+// the approximate score (max over the group) of every candidate and the
+// chunk's bound to err[seq row][chunk].  grid (chunks, Hkv, n)
 // ---------------------------------------------------------------------------
 template <int DT, int G>
 __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
@@ -71,16 +86,21 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
                                                     float* __restrict__ err, int err_stride) {
   __shared__ float s_e[4];
   const int chunk = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int seq = sb.ids[bi];
-  const int len = geo.meta[seq];
-  const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
-  const int c0 = geo.ns, c1 = nb - geo.nr;
-  float* erow = err + ((size_t)bi * geo.hkv + h) * err_stride;
-  if (!ranked_select(geo, c1 - c0)) {
-    if (threadIdx.x == 0) erow[chunk] = 0.0f;
-    return;
+  const int c0 = geo.ns;
+  // this wave's kMfmaTiles consecutive 16-block tiles; every summary load is
+  // issued before the sequence length is known (rows are clamped into the
+  // table; rows past the candidates are read and not used)
+  const int jw = c0 + chunk * kMfmaChunk + wave * 16 * kMfmaTiles;
+  u32x4 af[kMfmaTiles][4];
+#pragma unroll
+  for (int t = 0; t < kMfmaTiles; ++t) {
+    const int jr = min(jw + 16 * t + n, geo.mbps - 1);
+    const uint16_t* row = summary_row(geo, seq, h, jr) + 8 * g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) af[t][s] = *(const u32x4*)(row + 32 * s);
   }
   u32x4 qf[4], qa[4];
 #pragma unroll
@@ -93,27 +113,27 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
       qa[s] = abs16x8(qf[s]);
     }
   }
+  const int len = geo.meta[seq];
+  const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
+  const int c1 = nb - geo.nr;
+  float* erow = err + ((size_t)bi * geo.hkv + h) * err_stride;
+  if (!ranked_select(geo, c1 - c0)) {
+    if (threadIdx.x == 0) erow[chunk] = 0.0f;
+    return;
+  }
   constexpr uint32_t one2 = DT == 0 ? 0x3C003C00u : 0x3F803F80u;
   const u32x4 ones = u32x4{one2, one2, one2, one2};
-  // ||q_head||_1 (column n of ones . |Q|^T), max over the group
+  // ||q_head||_1 (|Q| . 1), maximum over the group
   f32x4 q1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) q1 = mfma16x16x32<DT>(ones, qa[s], q1);
-  const float q1max = max16(q1[0]);
+  for (int s = 0; s < 4; ++s) q1 = mfma16x16x32<DT>(qa[s], ones, q1);
+  float q1h = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (4 * g + i < G) q1h = fmaxf(q1h, q1[i]);
+  const float q1max = max_rows(q1h);
   float emax = 0.0f;
-  float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
-  // this wave's kMfmaTiles consecutive 16-block tiles; every load is issued
-  // first (rows past the candidates, still inside the table, are read and
-  // not used)
-  const int jw = c0 + chunk * kMfmaChunk + wave * 16 * kMfmaTiles;
-  u32x4 af[kMfmaTiles][4];
-#pragma unroll
-  for (int t = 0; t < kMfmaTiles; ++t) {
-    const int jr = min(jw + 16 * t + n, geo.mbps - 1);
-    const uint16_t* row = summary_row(geo, seq, h, jr) + 8 * g;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) af[t][s] = *(const u32x4*)(row + 32 * s);
-  }
+  float* srow = score_row(geo, scores, bi, h);
 #pragma unroll
   for (int t = 0; t < kMfmaTiles; ++t) {
     const int j0 = jw + 16 * t;
@@ -122,28 +142,32 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const u32x4 ab = abs16x8(af[t][s]);
-      d = mfma16x16x32<DT>(af[t][s], qf[s], d);
-      a = mfma16x16x32<DT>(ab, qa[s], a);
-      k1 = mfma16x16x32<DT>(ab, ones, k1);
+      d = mfma16x16x32<DT>(qf[s], af[t][s], d);
+      a = mfma16x16x32<DT>(qa[s], ab, a);
+      k1 = mfma16x16x32<DT>(ones, ab, k1);
     }
-    // lane (head n, group g), entry i: block j0 + 4g + i
+    // lane (block j0 + n, group g), entry i: head 4g + i
+    float sc = -INFINITY, am = 0.0f;
+    bool bad = false;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = j0 + 4 * g + i;
-      float sc = n < G ? d[i] : -INFINITY;
-      const bool bad = n < G && (__builtin_isnan(sc) || __builtin_isinf(sc));
-      sc = max16(sc);
-      const float am = max16(a[i]);
-      // any non-finite head score makes the block's approximate score NaN
-      const bool any_bad = __ballot(bad) & (0xFFFFull << (16 * g));
-      if (j < c1) {
-        if (n == 0) srow[j] = any_bad ? __builtin_nanf("") : sc;
-        if (!any_bad) emax = fmaxf(emax, am + k1[i]);
+    for (int i = 0; i < 4; ++i)
+      if (4 * g + i < G) {
+        sc = fmaxf(sc, d[i]);
+        am = fmaxf(am, a[i]);
+        bad = bad || __builtin_isnan(d[i]) || __builtin_isinf(d[i]);
       }
+    sc = max_rows(sc);
+    am = max_rows(am);
+    // any non-finite head score makes the block's approximate score NaN
+    const uint64_t bm = __ballot(bad);
+    const bool any_bad = (((bm | (bm >> 16) | (bm >> 32) | (bm >> 48)) >> n) & 1ull) != 0ull;
+    const int j = j0 + n;
+    if (j < c1) {
+      if (g == 0) srow[j] = any_bad ? __builtin_nanf("") : sc;
+      if (!any_bad) emax = fmaxf(emax, am + k1[0]);  // k1[i] = ||summary row||_1 for every i
     }
   }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) emax = fmaxf(emax, __shfl_xor(emax, o, 64));
+  emax = wave_max_f32(emax);
   if (lane == 0) s_e[wave] = emax;
   __syncthreads();
   if (threadIdx.x == 0)
@@ -151,24 +175,34 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
 }
 
 // ---------------------------------------------------------------------------
-// workgroup primitives (1024 threads)
+// workgroup primitives (1024 threads).  The cross-wave exchanges are
+// double-buffered: call n uses buffer n & 1 (ph counts the calls, uniformly
+// over the workgroup), so a call's writes never meet the previous call's
+// reads, and the barrier of call n + 1 orders call n's reads before call
+// n + 2's writes.  One barrier per call.
 // ---------------------------------------------------------------------------
+constexpr int kHistBins = 2048;
+constexpr int kSmall = 64;  // keys resolved by one wave
+
+struct SelScratch {
+  uint32_t hist[kHistBins];
+  uint32_t small[kSmall];
+  int misc[8];
+  __align__(16) uint32_t xch[2][2][kSelWaves];
+};
+
 // exclusive prefix sum of v over the workgroup in thread order; *total
-__device__ __forceinline__ int wg_scan_excl(int v, int* s_tmp, int* total) {
+__device__ __forceinline__ int wg_scan_excl(int v, SelScratch& ss, int& ph, int* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  __syncthreads();  // s_tmp may still be read by an earlier call
-  if (lane == 63) s_tmp[w] = x;
+  const int x = wave_scan_incl(v);
+  uint32_t* buf = ss.xch[ph & 1][0];
+  ++ph;
+  if (lane == 63) buf[w] = (uint32_t)x;
   __syncthreads();
   int off = 0, tot = 0;
 #pragma unroll
   for (int i = 0; i < kSelWaves; ++i) {
-    const int t = s_tmp[i];
+    const int t = (int)buf[i];
     off += (i < w) ? t : 0;
     tot += t;
   }
@@ -177,37 +211,24 @@ __device__ __forceinline__ int wg_scan_excl(int v, int* s_tmp, int* total) {
 }
 
 // workgroup minimum of a and maximum of b (one exchange)
-__device__ __forceinline__ void wg_minmax(uint32_t& a, uint32_t& b, uint32_t (*s_red)[kSelWaves]) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    a = min(a, (uint32_t)__shfl_xor(a, o, 64));
-    b = max(b, (uint32_t)__shfl_xor(b, o, 64));
-  }
-  __syncthreads();
+__device__ __forceinline__ void wg_minmax(uint32_t& a, uint32_t& b, SelScratch& ss, int& ph) {
+  a = wave_min_u32(a);
+  b = wave_max_u32(b);
+  uint32_t(*buf)[kSelWaves] = ss.xch[ph & 1];
+  ++ph;
   if ((threadIdx.x & 63) == 0) {
-    s_red[0][threadIdx.x >> 6] = a;
-    s_red[1][threadIdx.x >> 6] = b;
+    buf[0][threadIdx.x >> 6] = a;
+    buf[1][threadIdx.x >> 6] = b;
   }
   __syncthreads();
-  a = s_red[0][0];
-  b = s_red[1][0];
+  a = buf[0][0];
+  b = buf[1][0];
 #pragma unroll
   for (int i = 1; i < kSelWaves; ++i) {
-    a = min(a, s_red[0][i]);
-    b = max(b, s_red[1][i]);
+    a = min(a, buf[0][i]);
+    b = max(b, buf[1][i]);
   }
 }
-
-constexpr int kHistBins = 2048;
-constexpr int kSmall = 64;  // keys resolved by one wave
-
-struct SelScratch {
-  uint32_t hist[kHistBins];
-  uint32_t small[kSmall];
-  int misc[8];
-  int s_tmp[kSelWaves];
-  uint32_t s_red[2][kSelWaves];
-};
 
 // The K-th largest of the workgroup's nvalid valid keys (bit p of vmask:
 // kr[p] valid), 1 <= K <= nvalid.  Range-adaptive radix select: the keys in
@@ -220,7 +241,7 @@ struct SelScratch {
 // *gt = valid keys > the result, *eq = valid keys equal to it.
 template <int PER>
 __device__ uint32_t wg_kth(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid, int K,
-                           SelScratch& ss, int* gt, int* eq) {
+                           SelScratch& ss, int& ph, int* gt, int* eq) {
   const int tid = threadIdx.x, lane = tid & 63;
   for (int b = tid; b < kHistBins; b += kSelThreads) ss.hist[b] = 0u;
   if (tid == 0) ss.misc[3] = 0;
@@ -231,7 +252,7 @@ __device__ uint32_t wg_kth(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid
       lo = min(lo, kr[p]);
       hi = max(hi, kr[p]);
     }
-  wg_minmax(lo, hi, ss.s_red);  // its barriers also order the zeroing above
+  wg_minmax(lo, hi, ss, ph);  // its barrier also orders the zeroing above
   int need = K, above = 0, rcnt = nvalid;
   bool by_value = true;
   uint32_t tau;
@@ -259,7 +280,7 @@ __device__ uint32_t wg_kth(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid
     const int b0 = kHistBins - 1 - 2 * tid, b1 = b0 - 1;
     const int h0 = (int)ss.hist[b0], h1 = (int)ss.hist[b1];
     int tot;
-    const int before = wg_scan_excl(h0 + h1, ss.s_tmp, &tot);
+    const int before = wg_scan_excl(h0 + h1, ss, ph, &tot);
     if (before < need && need <= before + h0) {
       ss.misc[0] = b0;
       ss.misc[1] = before;
@@ -290,12 +311,7 @@ __device__ uint32_t wg_kth(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid
       if (tid < 64) {
         const bool valid = lane < cnt;
         const uint32_t x = valid ? ss.small[lane] : 0u;
-        uint32_t mn = valid ? x : 0xFFFFFFFFu, mx = x;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          mn = min(mn, (uint32_t)__shfl_xor(mn, o, 64));
-          mx = max(mx, (uint32_t)__shfl_xor(mx, o, 64));
-        }
+        const uint32_t mn = wave_min_u32(valid ? x : 0xFFFFFFFFu), mx = wave_max_u32(x);
         const uint32_t off = x - mn;
         uint32_t t = 0u;
         for (int bit = mx == mn ? -1 : 31 - __clz(mx - mn); bit >= 0; --bit) {
@@ -317,7 +333,7 @@ __device__ uint32_t wg_kth(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid
       break;
     }
     // refine to the bin's keys; the histogram is cleared for the next pass
-    // (every read of it is behind the barrier above)
+    // (every read of it is behind the barriers above)
     for (int b = tid; b < kHistBins; b += kSelThreads) ss.hist[b] = 0u;
     if (tid == 0) ss.misc[3] = 0;
     if (use_v) {
@@ -328,7 +344,7 @@ __device__ uint32_t wg_kth(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid
           nlo = min(nlo, kr[p]);
           nhi = max(nhi, kr[p]);
         }
-      wg_minmax(nlo, nhi, ss.s_red);
+      wg_minmax(nlo, nhi, ss, ph);
       lo = nlo;
       hi = nhi;
     } else {
@@ -348,11 +364,11 @@ __device__ uint32_t wg_kth(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid
 // lowest index, i.e. thread order then p); all of them when K >= nvalid.
 template <int PER>
 __device__ uint32_t wg_topk_mask(const uint32_t (&kr)[PER], uint32_t vmask, int nvalid, int K,
-                                 SelScratch& ss) {
+                                 SelScratch& ss, int& ph) {
   if (K <= 0) return 0u;
   if (nvalid <= K) return vmask;
   int gt, eq;
-  const uint32_t tau = wg_kth(kr, vmask, nvalid, K, ss, &gt, &eq);
+  const uint32_t tau = wg_kth(kr, vmask, nvalid, K, ss, ph, &gt, &eq);
   const int krem = K - gt;
   uint32_t take = 0u;
   if (eq == krem) {  // every key equal to the K-th is taken
@@ -365,7 +381,7 @@ __device__ uint32_t wg_topk_mask(const uint32_t (&kr)[PER], uint32_t vmask, int 
 #pragma unroll
   for (int p = 0; p < PER; ++p) ties += ((vmask >> p) & 1u) && kr[p] == tau;
   int tie_total;
-  int rank = wg_scan_excl(ties, ss.s_tmp, &tie_total);
+  int rank = wg_scan_excl(ties, ss, ph, &tie_total);
 #pragma unroll
   for (int p = 0; p < PER; ++p)
     if ((vmask >> p) & 1u) {
@@ -378,8 +394,48 @@ __device__ uint32_t wg_topk_mask(const uint32_t (&kr)[PER], uint32_t vmask, int 
   return take;
 }
 
+// The krem best of one wave's keys x (lanes with valid set; lane order is
+// index order) by (key desc, lane asc), 1 <= krem < number of valid lanes.
+__device__ __forceinline__ bool wave_take_best(uint32_t x, bool valid, int krem) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const uint32_t mn = wave_min_u32(valid ? x : 0xFFFFFFFFu), mx = wave_max_u32(valid ? x : 0u);
+  const uint32_t off = x - mn;
+  uint32_t t = 0u;  // the krem-th largest offset
+  for (int bit = mx == mn ? -1 : 31 - __clz(mx - mn); bit >= 0; --bit) {
+    const uint32_t cand = t | (1u << bit);
+    if (__popcll(__ballot(valid && off >= cand)) >= krem) t = cand;
+  }
+  const int gcount = __popcll(__ballot(valid && off > t));
+  const uint64_t eqm = __ballot(valid && off == t);
+  return valid && (off > t || (off == t && gcount + __popcll(eqm & below) < krem));
+}
+
+// thread's PER consecutive score-row entries as whole vectors
+template <int PER>
+__device__ __forceinline__ void load_scores(const float* __restrict__ src, float (&v)[PER]) {
+  if constexpr (PER % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < PER / 4; ++i) {
+      const float4 x = ((const float4*)src)[i];
+      v[4 * i] = x.x;
+      v[4 * i + 1] = x.y;
+      v[4 * i + 2] = x.z;
+      v[4 * i + 3] = x.w;
+    }
+  } else if constexpr (PER == 2) {
+    const float2 x = *(const float2*)src;
+    v[0] = x.x;
+    v[1] = x.y;
+  } else {
+    v[0] = src[0];
+  }
+}
+
 // ---------------------------------------------------------------------------
-// block-wide selection; grid (Hkv, n), 1024 threads.
+// block-wide selection; grid (Hkv, n), 1024 threads.  Thread t owns blocks
+// j = t*PER + p, p < PER, of its score row (the candidates are ns <= j <
+// ns + nc), so thread order then p is block order.
 // BAND: scores are the approximate MFMA scores with bounds in err (see the
 // top of this file); dynamic LDS then holds the band (u32 per candidate).
 // ---------------------------------------------------------------------------
@@ -393,17 +449,18 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
   extern __shared__ uint32_t s_band[];
   __shared__ SelScratch ss;
   __shared__ __align__(16) uint32_t s_q[BAND ? G * kHeadDim / 2 : 4];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int h = blockIdx.x, bi = blockIdx.y;
   const int seq = sb.ids[bi];
   const int c0 = geo.ns, K = geo.top_k;
-  // this thread's candidates: c0 + i0 + p, p < PER; their scores are loaded
-  // before the sequence length is known (rows are mbps wide)
-  const float* srow = scores + ((size_t)bi * geo.hkv + h) * geo.mbps;
+  // scores (and the chunk bounds) are loaded before the sequence length is
+  // known: the row reads stay inside the score buffer (its slack covers
+  // the last row), and entries that are not candidates are never used
   const int i0 = tid * PER;
   float sc[PER];
-#pragma unroll
-  for (int p = 0; p < PER; ++p) sc[p] = c0 + i0 + p < geo.mbps ? srow[c0 + i0 + p] : 0.0f;
+  load_scores<PER>(score_row(geo, scores, bi, h) + i0, sc);
+  float ev = 0.0f;
+  if (BAND && tid < 64 && lane < err_count) ev = err[((size_t)bi * geo.hkv + h) * err_stride + lane];
   const int len = geo.meta[seq];
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int nc = nb - geo.nr - c0;
@@ -416,48 +473,42 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
   uint32_t vmask = 0u;
 #pragma unroll
   for (int p = 0; p < PER; ++p) {
-    const bool v = i0 + p < nc;
+    const bool v = i0 + p >= c0 && i0 + p < c0 + nc;
     kr[p] = v ? score_key(sc[p]) : 0u;
     vmask |= (uint32_t)v << p;
   }
+  int ph = 0;
   uint32_t take;
   if constexpr (!BAND) {
-    take = wg_topk_mask(kr, vmask, nc, K, ss);
+    take = wg_topk_mask(kr, vmask, nc, K, ss, ph);
   } else {
     const uint32_t* qsrc = (const uint32_t*)(q + ((size_t)bi * geo.hq + h * G) * kHeadDim);
     for (int e = tid; e < G * kHeadDim / 2; e += kSelThreads) s_q[e] = qsrc[e];
     // the bound: maximum over the chunks' bounds (NaN bounds are skipped)
-    float e = 0.0f;
     if (tid < 64) {
-      const float* erow = err + ((size_t)bi * geo.hkv + h) * err_stride;
-      for (int c = tid; c < err_count; c += 64) e = fmaxf(e, erow[c]);
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) e = fmaxf(e, __shfl_xor(e, o, 64));
-      if (tid == 0) ss.misc[7] = __float_as_int(e);
+      ev = wave_max_f32(ev);
+      if (tid == 0) ss.misc[7] = __float_as_int(ev);
     }
-    // K-th and (K+1)-th largest approximate keys
+    // K-th largest approximate key (wg_kth's barriers publish misc[7] and s_q)
     int gt, eq;
-    const uint32_t t1 = wg_kth(kr, vmask, nc, K, ss, &gt, &eq);
-    e = __int_as_float(ss.misc[7]) * (1.0f + 0x1p-8f) + 0x1p-120f;
-    uint32_t t2 = t1;
-    if (gt + eq <= K) {  // the (K+1)-th is below t1
-      uint32_t below = 0u, unused = 0xFFFFFFFFu;
+    const uint32_t t1 = wg_kth(kr, vmask, nc, K, ss, ph, &gt, &eq);
+    const float e = __int_as_float(ss.misc[7]) * (1.0f + 0x1p-8f) + 0x1p-120f;
+    // one exchange: the largest key below t1 and whether every approximate
+    // score is finite
+    uint32_t fin = 1u, below = 0u;
 #pragma unroll
-      for (int p = 0; p < PER; ++p)
-        if (((vmask >> p) & 1u) && kr[p] < t1) below = max(below, kr[p]);
-      wg_minmax(unused, below, ss.s_red);
-      t2 = below;
-    }
+    for (int p = 0; p < PER; ++p)
+      if ((vmask >> p) & 1u) {
+        if (kr[p] < t1) below = max(below, kr[p]);
+        if (!__builtin_isfinite(key_value(kr[p]))) fin = 0u;
+      }
+    wg_minmax(fin, below, ss, ph);
+    const uint32_t t2 = gt + eq <= K ? below : t1;  // the (K+1)-th largest
     const float lb = key_value(t1) - e, ub = key_value(t2) + e;
     // a candidate whose approximate score is not finite has no bound (its
     // exact score may exceed any other), and non-finite limits certify
     // nothing: then every candidate is rescored
-    int nbad = 0;
-#pragma unroll
-    for (int p = 0; p < PER; ++p) nbad += ((vmask >> p) & 1u) && !__builtin_isfinite(key_value(kr[p]));
-    int nbad_total;
-    (void)wg_scan_excl(nbad, ss.s_tmp, &nbad_total);
-    const bool bounds_ok = nbad_total == 0 && __builtin_isfinite(lb) && __builtin_isfinite(ub);
+    const bool bounds_ok = fin != 0u && __builtin_isfinite(lb) && __builtin_isfinite(ub);
     // classify: certainly in (take), band (rescored), certainly out
     uint32_t band = 0u;
     take = 0u;
@@ -475,9 +526,11 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
           ++nband;
         }
       }
-    int nin_total, nband_total;
-    (void)wg_scan_excl(nin, ss.s_tmp, &nin_total);
-    const int bpos = wg_scan_excl(nband, ss.s_tmp, &nband_total);
+    // both counts in one scan (each total <= 12288 fits 16 bits)
+    int packed_total;
+    const int packed_pos = wg_scan_excl((nin << 16) | nband, ss, ph, &packed_total);
+    const int nin_total = packed_total >> 16, nband_total = packed_total & 0xFFFF;
+    const int bpos = packed_pos & 0xFFFF;
     const int krem = K - nin_total;
     if (nband_total <= krem) {
       take |= band;
@@ -486,7 +539,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
       int w = bpos;
 #pragma unroll
       for (int p = 0; p < PER; ++p)
-        if (band & (1u << p)) s_band[w++] = (uint32_t)(c0 + i0 + p);
+        if (band & (1u << p)) s_band[w++] = (uint32_t)(i0 + p);
       __syncthreads();
       const int c = tid & 15;
       const uint16_t* qh = (const uint16_t*)s_q;
@@ -505,20 +558,36 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
         if (c == 0) s_band[bk] = score_key(best);  // the slot's index is no longer needed
       }
       __syncthreads();
-      uint32_t br[PER];
-      w = bpos;
+      if (nband_total <= 64) {
+        // one wave picks the krem best of the band (band slots are in block
+        // order) and leaves a 0/1 flag in each slot
+        if (tid < 64) {
+          const bool valid = lane < nband_total;
+          const uint32_t x = valid ? s_band[lane] : 0u;
+          const bool t = wave_take_best(x, valid, krem);
+          if (valid) s_band[lane] = t ? 1u : 0u;
+        }
+        __syncthreads();
+        w = bpos;
 #pragma unroll
-      for (int p = 0; p < PER; ++p) br[p] = (band & (1u << p)) ? s_band[w++] : 0u;
-      take |= wg_topk_mask(br, band, nband_total, krem, ss);
+        for (int p = 0; p < PER; ++p)
+          if (band & (1u << p)) take |= (s_band[w++] != 0u ? 1u : 0u) << p;
+      } else {
+        uint32_t br[PER];
+        w = bpos;
+#pragma unroll
+        for (int p = 0; p < PER; ++p) br[p] = (band & (1u << p)) ? s_band[w++] : 0u;
+        take |= wg_topk_mask(br, band, nband_total, krem, ss, ph);
+      }
     }
   }
-  // output: sinks, the chosen candidates in index order, recent blocks
+  // output: sinks, the chosen candidates in block order, recent blocks
   int total;
-  const int pos = wg_scan_excl(__popc(take), ss.s_tmp, &total);
+  const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
   int w = geo.ns + pos;
 #pragma unroll
   for (int p = 0; p < PER; ++p)
-    if (take & (1u << p)) out[w++] = c0 + i0 + p;
+    if (take & (1u << p)) out[w++] = i0 + p;
   for (int p = tid; p < geo.ns; p += kSelThreads) out[p] = p;
   for (int r = tid; r < geo.nr; r += kSelThreads) out[geo.ns + total + r] = nb - geo.nr + r;
   for (int p = geo.ns + total + geo.nr + tid; p < geo.nsel_max; p += kSelThreads) out[p] = -1;
@@ -534,7 +603,7 @@ template <int DT, int G, bool BAND>
 static void select_per(const Geometry& g, const SeqBatch& b, const uint16_t* q, const float* scores,
                        const float* err, int stride, int chunks, int max_nc, int32_t* idx,
                        hipStream_t s, Timing* prof) {
-  const int per = (max_nc + kSelThreads - 1) / kSelThreads;
+  const int per = (g.ns + max_nc + kSelThreads - 1) / kSelThreads;  // blocks 0 .. ns + max_nc - 1
   const dim3 grid(g.hkv, b.n), blk(kSelThreads);
   const size_t lds = BAND ? (size_t)g.mbps * 4 : 0;
   if (per <= 1)
