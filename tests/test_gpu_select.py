@@ -125,3 +125,25 @@ def test_nonfinite_scores_select_like_oracle(gpu, T_blocks, Hq, Hkv, K):
     got = idx.cpu().numpy()
     assert np.array_equal(got, idx_ref), f"differ at {np.argwhere(got != idx_ref)[:5]}"
     assert np.array_equal(idx2.cpu().numpy(), idx_ref)
+
+
+@pytest.mark.parametrize("dtype,Hq,Hkv,Tb,K,scale", [
+    ("f16", 64, 4, 32, 128, 1e-3), ("bf16", 32, 4, 64, 40, 1e-2), ("f16", 16, 4, 64, 32, 1e-3),
+])
+def test_near_equal_scores(gpu, dtype, Hq, Hkv, Tb, K, scale):
+    """Every block's keys are one shared row plus small noise, so the scores
+    crowd within a few bound widths: the compacted-list selection must fall
+    back to the full workgroup path (wide groups) or stay exact (G = 4)."""
+    lens = [Tb * 3000 + 9, Tb * 1500]
+    w = make_workload(5400 + Hq + K, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype=dtype,
+                      top_k=K, ns=1, nr=2, lens=lens)
+    rng = np.random.default_rng(K)
+    for b in range(w.B):
+        for h in range(w.Hkv):
+            base = rng.standard_normal(128)
+            noise = rng.standard_normal((w.keys[b][h].shape[0], 128)) * scale
+            w.keys[b][h][:] = O.from_f32((base[None, :] + noise).astype(np.float32), w.dtype)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    err = check(cache, w, gpu)
+    log(f"[near-equal] {dtype} G={Hq // Hkv} err={err:.3g}")
