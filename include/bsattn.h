@@ -135,6 +135,19 @@ int bsattn_decode(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
                   int32_t n_seqs, float scale, void* out, int32_t* idx_out,
                   void* stream);
 
+/* Decode of n_query (1..16) query tokens per sequence whose n_query keys /
+ * values were appended last: the speculative-verify pass of
+ * Evaluate.swift:862-870 (L = numDraft + 1 under a causal mask).  q / out
+ * are [n_seqs, Hq, n_query, D]; query i of a sequence holding T tokens
+ * attends to its first T - n_query + 1 + i tokens, selecting its own blocks
+ * there, i.e. exactly what n_query single-token decodes would compute one
+ * after another.  idx_out (may be NULL) is [n_seqs, n_query, Hkv,
+ * nsel_max]. */
+int bsattn_decode_multi(bsattn_cache* cache, const void* q,
+                        const int32_t* seq_ids, int32_t n_seqs,
+                        int32_t n_query, float scale, void* out,
+                        int32_t* idx_out, void* stream);
+
 /* Drops the last n_tokens of each listed sequence (clamped to its length);
  * writes the number trimmed per sequence to trimmed (host, may be NULL).
  * KVCacheSimple.trim (KVCache.swift:396-402). */

@@ -3,6 +3,7 @@ reference's KVCache / attentionWithCacheUpdate API over libbsattn.so."""
 from ._lib import BsattnError, EXPORTS, LIB_PATH, lib
 from .attention import attentionWithCacheUpdate
 from .cache import BlockSparseKVCache
+from .prompt_cache import loadPromptCache, savePromptCache
 
 __all__ = ["BlockSparseKVCache", "BsattnError", "attentionWithCacheUpdate", "lib", "LIB_PATH",
-           "EXPORTS"]
+           "EXPORTS", "savePromptCache", "loadPromptCache"]

@@ -34,6 +34,7 @@ EXPORTS = (
     "bsattn_select",
     "bsattn_attend",
     "bsattn_decode",
+    "bsattn_decode_multi",
     "bsattn_trim",
     "bsattn_reset",
     "bsattn_copy",
@@ -111,6 +112,7 @@ def lib() -> ctypes.CDLL:
         "bsattn_select": (ctypes.c_int, [P, P, PI32, i32, P, P]),
         "bsattn_attend": (ctypes.c_int, [P, P, PI32, i32, P, ctypes.c_float, P, P]),
         "bsattn_decode": (ctypes.c_int, [P, P, PI32, i32, ctypes.c_float, P, P, P]),
+        "bsattn_decode_multi": (ctypes.c_int, [P, P, PI32, i32, i32, ctypes.c_float, P, P, P]),
         "bsattn_trim": (ctypes.c_int, [P, PI32, i32, i32, PI32, P]),
         "bsattn_reset": (ctypes.c_int, [P, PI32, i32, P]),
         "bsattn_copy": (ctypes.c_int, [P, PP, P]),

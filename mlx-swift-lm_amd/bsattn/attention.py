@@ -14,6 +14,9 @@ import torch
 from .cache import BlockSparseKVCache
 
 
+MAX_QUERIES = 16  # query tokens per sequence of one multi-token pass
+
+
 def attentionWithCacheUpdate(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                              cache, scale: float, mask="none") -> torch.Tensor:
     """queries [B, Hq, L, D], keys / values [B, Hkv, L, D] -> [B, Hq, L, D]."""
@@ -21,13 +24,18 @@ def attentionWithCacheUpdate(queries: torch.Tensor, keys: torch.Tensor, values: 
         raise TypeError("attentionWithCacheUpdate here handles BlockSparseKVCache only; "
                         "other caches use the reference's dense path")
     L = queries.shape[2]
-    if L != 1:
-        raise NotImplementedError("block-sparse attention is a decode path (L == 1); "
-                                  "multi-token prefill attention is not provided")
-    if mask not in ("none", None):
-        raise ValueError("decode (L == 1) takes no mask (BaseKVCache.makeMask returns .none)")
+    if L == 1:
+        if mask not in ("none", None):
+            raise ValueError("decode (L == 1) takes no mask (BaseKVCache.makeMask returns .none)")
+        cache.append(keys, values)
+        return cache.decode(queries, scale)
+    if L > MAX_QUERIES:
+        raise NotImplementedError(f"block-sparse attention serves decode and verify passes of up to "
+                                  f"{MAX_QUERIES} tokens; a {L}-token prefill is not provided")
+    if mask != "causal":
+        raise ValueError("a multi-token pass takes the causal mask (BaseKVCache.makeMask(n > 1))")
     cache.append(keys, values)
-    return cache.decode(queries, scale)
+    return cache.decodeMulti(queries, scale)
 
 
 __all__ = ["attentionWithCacheUpdate"]

@@ -229,12 +229,13 @@ class BlockSparseKVCache:
         return out
 
     # -- selector-index API and attention -----------------------------------
-    def _check_q(self, q: torch.Tensor) -> int:
+    def _check_q(self, q: torch.Tensor, multi: bool = False) -> int:
         if q.device != self.device or q.dtype != self.dtype or not q.is_contiguous():
             raise ValueError(f"queries must be a contiguous {self.dtype} tensor on {self.device}")
-        if q.dim() != 4 or q.shape[1] != self.desc.num_q_heads or q.shape[2] != 1 \
+        L = "L" if multi else 1
+        if q.dim() != 4 or q.shape[1] != self.desc.num_q_heads or (not multi and q.shape[2] != 1) \
                 or q.shape[3] != self.desc.head_dim:
-            raise ValueError(f"queries must be [B, {self.desc.num_q_heads}, 1, {self.desc.head_dim}], "
+            raise ValueError(f"queries must be [B, {self.desc.num_q_heads}, {L}, {self.desc.head_dim}], "
                              f"got {tuple(q.shape)}")
         return q.shape[0]
 
@@ -271,6 +272,28 @@ class BlockSparseKVCache:
             idx_p = _ptr(idx_out)
         check(lib().bsattn_decode(self._h, _ptr(queries), i32_array(seq_ids), B,
                                   ctypes.c_float(scale), _ptr(out), idx_p, _stream(self.device)))
+        return out
+
+    def decodeMulti(self, queries: torch.Tensor, scale: float,
+                    seq_ids: Optional[Sequence[int]] = None,
+                    idx_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Decode of L = queries.shape[2] (1..16) query tokens per sequence
+        whose keys / values were appended last (speculative verify,
+        Evaluate.swift:862-870): query i of a sequence holding T tokens sees
+        its first T - L + 1 + i tokens and selects its own blocks there, as L
+        single-token decodes would.  queries / result [B, Hq, L, D];
+        idx_out [B, L, Hkv, nselMax] int32."""
+        B = self._check_q(queries, multi=True)
+        L = queries.shape[2]
+        out = torch.empty_like(queries)
+        idx_p = None
+        if idx_out is not None:
+            if idx_out.dtype != torch.int32 or not idx_out.is_contiguous() \
+                    or tuple(idx_out.shape) != (B, L, self.desc.num_kv_heads, self.nselMax):
+                raise ValueError("idx_out must be a contiguous int32 [B, L, Hkv, nselMax] tensor")
+            idx_p = _ptr(idx_out)
+        check(lib().bsattn_decode_multi(self._h, _ptr(queries), i32_array(seq_ids), B, L,
+                                        ctypes.c_float(scale), _ptr(out), idx_p, _stream(self.device)))
         return out
 
     # -- kernel timing -------------------------------------------------------

@@ -51,10 +51,11 @@ struct bsattn_cache {
   Geometry geo{};
   int64_t num_pages = 0;
   size_t pool_bytes = 0, summ_bytes = 0, meta_words = 0;
-  float* scores = nullptr;    // [max_seqs][hkv][sstride] + kScoreSlack
-  int32_t* idx_ws = nullptr;  // [max_seqs][hkv][nsel_max]
-  float* partials = nullptr;  // [max_seqs][hq][nsplit][D + 2]
-  float* err_ws = nullptr;    // [max_seqs][hkv][mfma_err_stride]: MFMA score bounds
+  // per-launch workspaces, rows = batch entries of one launch
+  float* scores = nullptr;    // [rows][hkv][sstride] + kScoreSlack
+  int32_t* idx_ws = nullptr;  // [rows][hkv][nsel_max]
+  float* partials = nullptr;  // [rows][hq][nsplit][D + 2]
+  float* err_ws = nullptr;    // [rows][hkv][mfma_err_stride]: MFMA score bounds
   std::vector<int32_t> len;
   std::vector<std::vector<int32_t>> pages;
   std::vector<int32_t> free_pages;  // stack; back() is handed out next
@@ -308,13 +309,15 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   if ((e = hipMalloc((void**)&g.pool, c->pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(pool)"));
   if ((e = hipMalloc((void**)&g.summ, c->summ_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(summaries)"));
   if ((e = hipMalloc((void**)&g.meta, c->meta_words * 4)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(meta)"));
-  if ((e = hipMalloc((void**)&c->scores, ((size_t)d.max_seqs * g.hkv * g.sstride + kScoreSlack) * 4)) != hipSuccess)
+  // per-launch workspaces: one row per batch entry of a launch
+  const size_t rows = (size_t)std::min(kMaxBatch, d.max_seqs * kMaxQueries);
+  if ((e = hipMalloc((void**)&c->scores, (rows * g.hkv * g.sstride + kScoreSlack) * 4)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMalloc(scores)"));
-  if ((e = hipMalloc((void**)&c->idx_ws, (size_t)d.max_seqs * g.hkv * g.nsel_max * 4)) != hipSuccess)
+  if ((e = hipMalloc((void**)&c->idx_ws, rows * g.hkv * g.nsel_max * 4)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMalloc(indices)"));
-  if ((e = hipMalloc((void**)&c->partials, (size_t)d.max_seqs * g.hq * g.nsplit * (kHeadDim + 2) * 4)) != hipSuccess)
+  if ((e = hipMalloc((void**)&c->partials, rows * g.hq * g.nsplit * (kHeadDim + 2) * 4)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMalloc(partials)"));
-  if ((e = hipMalloc((void**)&c->err_ws, (size_t)d.max_seqs * g.hkv * mfma_err_stride(g) * 4)) != hipSuccess)
+  if ((e = hipMalloc((void**)&c->err_ws, rows * g.hkv * mfma_err_stride(g) * 4)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMalloc(bounds)"));
   // zeroed pages: never-written token slots hold finite values
   if ((e = hipMemset(g.pool, 0, c->pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(pool)"));
@@ -444,48 +447,75 @@ int bsattn_append_quantized(bsattn_cache* c, const uint32_t* k_w, const void* k_
   });
 }
 
-static int do_select(bsattn_cache* c, const void* q, const std::vector<int32_t>& seqs,
-                     int32_t* idx_out, hipStream_t s) {
-  const int n = (int)seqs.size();
-  for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
-    SeqBatch b{};
-    b.n = std::min(kMaxBatch, n - i0);
-    int max_nc = 0;
-    for (int i = 0; i < b.n; ++i) {
-      b.ids[i] = seqs[i0 + i];
-      max_nc = std::max(max_nc, candidates(c->geo, c->len[b.ids[i]]));
-    }
-    const uint16_t* qq = (const uint16_t*)q + (size_t)i0 * c->geo.hq * kHeadDim;
-    float* sc = c->scores + (size_t)i0 * c->geo.hkv * c->geo.sstride;
-    int32_t* io = idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max;
-    Timing tm[kProfKinds];
-    Timing* prof = prof_slots(c, s, tm);
-    float* err = c->err_ws + (size_t)i0 * c->geo.hkv * mfma_err_stride(c->geo);
-    hipError_t e = launch_select(c->geo, b, qq, sc, err, io, max_nc, s, prof);
-    prof_collect(c, prof);
-    if (e != hipSuccess) return hip_fail(e, "select launch");
-  }
-  return BSATTN_OK;
+// One query of a launch: the sequence, the tokens it sees (-1: all), the
+// element offset of its q / out rows.
+struct Entry {
+  int32_t seq, len;
+  int64_t qoff;
+};
+
+// Entries of n_query query tokens per listed sequence, q / out laid out
+// [n, Hq, n_query, D]: query i of a sequence holding T tokens (the n_query
+// new ones included) sees its first T - n_query + 1 + i tokens.
+static std::vector<Entry> entries(const bsattn_cache* c, const std::vector<int32_t>& seqs, int n_query) {
+  std::vector<Entry> es;
+  es.reserve(seqs.size() * n_query);
+  const int64_t hq = c->geo.hq;
+  for (size_t b = 0; b < seqs.size(); ++b)
+    for (int i = 0; i < n_query; ++i)
+      es.push_back({seqs[b], n_query == 1 ? -1 : c->len[seqs[b]] - n_query + 1 + i,
+                    ((int64_t)b * hq * n_query + i) * kHeadDim});
+  return es;
 }
 
-static int do_attend(bsattn_cache* c, const void* q, const std::vector<int32_t>& seqs,
-                     const int32_t* idx, float scale, void* out, hipStream_t s) {
-  const int n = (int)seqs.size();
-  const size_t elem = 2;
-  for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
-    SeqBatch b{};
-    b.n = std::min(kMaxBatch, n - i0);
-    for (int i = 0; i < b.n; ++i) b.ids[i] = seqs[i0 + i];
-    const size_t qoff = (size_t)i0 * c->geo.hq * kHeadDim * elem;
+static int visible(const bsattn_cache* c, const Entry& e) { return e.len >= 0 ? e.len : c->len[e.seq]; }
+
+// the launch batch for entries [e0, e0 + n); q / out offsets relative to entry e0
+static SeqBatch make_batch(const std::vector<Entry>& es, int e0, int n, int qhs) {
+  SeqBatch b{};
+  b.n = n;
+  b.qhs = qhs;
+  for (int i = 0; i < n; ++i) {
+    b.ids[i] = es[e0 + i].seq;
+    b.len[i] = es[e0 + i].len;
+    b.qoff[i] = (int32_t)(es[e0 + i].qoff - es[e0].qoff);
+  }
+  return b;
+}
+
+// Selection, attention or both (the selection inside the attention kernel
+// when every entry's candidates fit one wave) for the entries, in launches
+// of at most kMaxBatch entries.  The score, bound, index and partial
+// workspaces are per launch (launches on one stream run in order).
+enum class Op { Select, Attend, Decode };
+static int run_entries(bsattn_cache* c, Op op, const void* q, const std::vector<Entry>& es, int qhs,
+                       const int32_t* idx_in, int32_t* idx_out, float scale, void* out, hipStream_t s) {
+  const int n = (int)es.size();
+  const Geometry& g = c->geo;
+  const size_t idx_row = (size_t)g.hkv * g.nsel_max;
+  for (int e0 = 0; e0 < n; e0 += kMaxBatch) {
+    const SeqBatch b = make_batch(es, e0, std::min(kMaxBatch, n - e0), qhs);
+    int max_nc = 0;
+    for (int i = 0; i < b.n; ++i) max_nc = std::max(max_nc, candidates(g, visible(c, es[e0 + i])));
+    const uint16_t* qq = (const uint16_t*)q + es[e0].qoff;
+    uint16_t* oo = out ? (uint16_t*)out + es[e0].qoff : nullptr;
+    int32_t* io = idx_out ? idx_out + e0 * idx_row : nullptr;
     Timing tm[kProfKinds];
     Timing* prof = prof_slots(c, s, tm);
-    hipError_t e = launch_attend(c->geo, b, (const char*)q + qoff,
-                                 idx + (size_t)i0 * c->geo.hkv * c->geo.nsel_max, scale,
-                                 (char*)out + qoff,
-                                 c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2),
-                                 s, prof);
+    hipError_t e = hipSuccess;
+    if (op == Op::Select) {
+      e = launch_select(g, b, qq, c->scores, c->err_ws, io, max_nc, s, prof);
+    } else if (op == Op::Attend) {
+      e = launch_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, c->partials, s, prof);
+    } else if (max_nc > fused_select_limit(g.top_k)) {
+      int32_t* sel = io ? io : c->idx_ws;
+      e = launch_select(g, b, qq, c->scores, c->err_ws, sel, max_nc, s, prof);
+      if (e == hipSuccess) e = launch_attend(g, b, qq, sel, scale, oo, c->partials, s, prof);
+    } else {
+      e = launch_decode(g, b, qq, c->scores, io, max_nc, scale, oo, c->partials, s, prof);
+    }
     prof_collect(c, prof);
-    if (e != hipSuccess) return hip_fail(e, "attend launch");
+    if (e != hipSuccess) return hip_fail(e, op == Op::Select ? "select launch" : op == Op::Attend ? "attend launch" : "decode launch");
   }
   return BSATTN_OK;
 }
@@ -497,7 +527,8 @@ int bsattn_select(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
-  return do_select(c, q, seqs, idx_out, (hipStream_t)stream);
+  return run_entries(c, Op::Select, q, entries(c, seqs, 1), kHeadDim, nullptr, idx_out, 0.0f, nullptr,
+                     (hipStream_t)stream);
 }
 
 int bsattn_attend(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
@@ -507,7 +538,8 @@ int bsattn_attend(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
-  return do_attend(c, q, seqs, idx, scale, out, (hipStream_t)stream);
+  return run_entries(c, Op::Attend, q, entries(c, seqs, 1), kHeadDim, idx, nullptr, scale, out,
+                     (hipStream_t)stream);
 }
 
 int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
@@ -517,40 +549,25 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
-  hipStream_t s = (hipStream_t)stream;
-  // the selection runs inside the attention kernel when every sequence has
-  // few enough candidate blocks; otherwise select, then attend
-  const int tb = c->d.block_size;
-  int max_nc = 0;
-  for (int sq : seqs) max_nc = std::max(max_nc, (c->len[sq] + tb - 1) / tb - c->geo.ns - c->geo.nr);
-  if (max_nc > fused_select_limit(c->geo.top_k)) {
-    int32_t* idx = idx_out ? idx_out : c->idx_ws;
-    rc = do_select(c, q, seqs, idx, s);
-    if (rc) return rc;
-    return do_attend(c, q, seqs, idx, scale, out, s);
-  }
-  const int n = (int)seqs.size();
-  for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
-    SeqBatch b{};
-    b.n = std::min(kMaxBatch, n - i0);
-    int max_nc = 0;
-    for (int i = 0; i < b.n; ++i) {
-      b.ids[i] = seqs[i0 + i];
-      max_nc = std::max(max_nc, candidates(c->geo, c->len[b.ids[i]]));
-    }
-    const size_t qoff = (size_t)i0 * c->geo.hq * kHeadDim * 2;
-    Timing tm[kProfKinds];
-    Timing* prof = prof_slots(c, s, tm);
-    hipError_t e = launch_decode(c->geo, b, (const char*)q + qoff,
-                                 c->scores + (size_t)i0 * c->geo.hkv * c->geo.sstride,
-                                 idx_out ? idx_out + (size_t)i0 * c->geo.hkv * c->geo.nsel_max : nullptr,
-                                 max_nc, scale, (char*)out + qoff,
-                                 c->partials + (size_t)i0 * c->geo.hq * c->geo.nsplit * (kHeadDim + 2),
-                                 s, prof);
-    prof_collect(c, prof);
-    if (e != hipSuccess) return hip_fail(e, "decode launch");
-  }
-  return BSATTN_OK;
+  return run_entries(c, Op::Decode, q, entries(c, seqs, 1), kHeadDim, nullptr, idx_out, scale, out,
+                     (hipStream_t)stream);
+}
+
+int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
+                        int32_t n_query, float scale, void* out, int32_t* idx_out, void* stream) {
+  if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (n_query < 1 || n_query > kMaxQueries)
+    return fail(BSATTN_ERR_INVALID, "n_query %d out of range [1, %d]", n_query, kMaxQueries);
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  for (int sq : seqs)
+    if (c->len[sq] < n_query)
+      return fail(BSATTN_ERR_INVALID, "sequence %d holds %d tokens, fewer than its %d queries", sq, c->len[sq],
+                  n_query);
+  DeviceGuard dg(c->d.device);
+  return run_entries(c, Op::Decode, q, entries(c, seqs, n_query), n_query * kHeadDim, nullptr, idx_out,
+                     scale, out, (hipStream_t)stream);
 }
 
 int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
@@ -625,7 +642,10 @@ int bsattn_export(const bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs,
   for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
     SeqBatch b{};
     b.n = std::min(kMaxBatch, n_seqs - i0);
-    for (int i = 0; i < b.n; ++i) b.ids[i] = seqs[i0 + i];
+    for (int i = 0; i < b.n; ++i) {
+      b.ids[i] = seqs[i0 + i];
+      b.len[i] = -1;
+    }
     HIP_TRY(launch_export(c->geo, b, T, (char*)k_out + i0 * row, (char*)v_out + i0 * row,
                           (hipStream_t)stream),
             "export launch");
@@ -651,7 +671,10 @@ int bsattn_export_quantized(const bsattn_cache* c, const int32_t* seq_ids, int32
   for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
     SeqBatch b{};
     b.n = std::min(kMaxBatch, n_seqs - i0);
-    for (int i = 0; i < b.n; ++i) b.ids[i] = seqs[i0 + i];
+    for (int i = 0; i < b.n; ++i) {
+      b.ids[i] = seqs[i0 + i];
+      b.len[i] = -1;
+    }
     const size_t wo = (size_t)i0 * rows * words, go = (size_t)i0 * rows * groups;
     HIP_TRY(launch_export_quantized(c->geo, b, T, k_w + wo, (uint16_t*)k_s + go, (uint16_t*)k_b + go,
                                     v_w + wo, (uint16_t*)v_s + go, (uint16_t*)v_b + go,

@@ -59,6 +59,16 @@ __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirs
 // rather than sunk into a later branch behind other waits.
 __device__ __forceinline__ void issue_here(int x) { asm volatile("" ::"s"(x)); }
 
+// tokens batch entry bi attends to, and the element offset of its q / out
+// row for query head `head`
+__device__ __forceinline__ int entry_len(const Geometry& g, const SeqBatch& sb, int bi, int seq) {
+  const int l = sb.len[bi];
+  return l >= 0 ? l : g.meta[seq];
+}
+__device__ __forceinline__ size_t q_row(const SeqBatch& sb, int bi, int head) {
+  return (size_t)sb.qoff[bi] + (size_t)head * sb.qhs;
+}
+
 __device__ __forceinline__ const int32_t* block_table(const Geometry& g, int seq) {
   return g.meta + g.bt_off + (size_t)seq * g.mbps;
 }
@@ -592,7 +602,8 @@ __device__ __forceinline__ void store_empty(float* s_m, float* s_l, float (*s_o)
 // normalised output (one split) or the unnormalised partial (o, m, l) for
 // k_combine.
 template <int DT, int G, int W>
-__device__ __forceinline__ void attend_merge(const Geometry& geo, int bi, int h, int split,
+__device__ __forceinline__ void attend_merge(const Geometry& geo, const SeqBatch& sb, int bi, int h,
+                                             int split,
                                              const float (*s_m)[16], const float (*s_l)[16],
                                              const float (*s_o)[G][kHeadDim],
                                              uint16_t* __restrict__ out,
@@ -615,7 +626,7 @@ __device__ __forceinline__ void attend_merge(const Geometry& geo, int bi, int h,
     }
     const size_t row = (size_t)bi * geo.hq + h * G + head;
     if (nsplit == 1) {
-      out[row * kHeadDim + d] = from_f32<DT>(L > 0.f ? a / L : 0.f);
+      out[q_row(sb, bi, h * G + head) + d] = from_f32<DT>(L > 0.f ? a / L : 0.f);
     } else {
       float* pp = partials + (row * nsplit + split) * (kHeadDim + 2);
       pp[d] = a;

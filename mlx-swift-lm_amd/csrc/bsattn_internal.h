@@ -10,6 +10,7 @@ namespace bsattn {
 
 constexpr int kHeadDim = 128;
 constexpr int kMaxBatch = 64;   // sequences per launch (host splits larger calls)
+constexpr int kMaxQueries = 16; // query tokens per sequence in one multi-token decode
 constexpr int kMaxPatch = 240;  // metadata words patched per launch
 #ifndef BSATTN_WAVES
 #define BSATTN_WAVES 4
@@ -41,9 +42,17 @@ struct Geometry {
   int32_t* meta;              // [max_seqs] lengths, then [max_seqs][mbps] pages
 };
 
+// A launch's batch entries: entry i is a query of sequence ids[i] that sees
+// its first len[i] tokens (-1: all of them; a multi-token decode has one
+// entry per query token, each seeing the tokens up to its own position);
+// its q and output rows start at element qoff[i] (from the launch's q / out
+// pointers), heads qhs elements apart.
 struct SeqBatch {
   int32_t n;
+  int32_t qhs;
   int32_t ids[kMaxBatch];
+  int32_t len[kMaxBatch];
+  int32_t qoff[kMaxBatch];
 };
 
 struct AppendBatch {

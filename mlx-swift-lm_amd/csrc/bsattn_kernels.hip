@@ -135,10 +135,9 @@ __global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
     raw[p] = (j < geo.mbps) ? *(const u32x4*)(sbase + (size_t)j * kHeadDim) : u32x4{0u, 0u, 0u, 0u};
   }
   float qv[G][8];
-  const uint16_t* qrow = q + ((size_t)bi * geo.hq + h * G) * kHeadDim + 8 * c;
 #pragma unroll
-  for (int g = 0; g < G; ++g) unpack8<DT>(*(const u32x4*)(qrow + (size_t)g * kHeadDim), qv[g]);
-  const int len = geo.meta[seq];
+  for (int g = 0; g < G; ++g) unpack8<DT>(*(const u32x4*)(q + q_row(sb, bi, h * G + g) + 8 * c), qv[g]);
+  const int len = entry_len(geo, sb, bi, seq);
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int c1 = nb - geo.nr;
   if (!ranked_select(geo, c1 - geo.ns)) return;
@@ -177,7 +176,7 @@ __global__ __launch_bounds__(64) void k_topk(Geometry geo, SeqBatch sb,
   const int c0 = geo.ns;
   WaveCand wc;
   wave_cand_load(score_row(geo, scores, bi, h), nullptr, c0, geo.mbps, wc);
-  const int len = geo.meta[seq];
+  const int len = entry_len(geo, sb, bi, seq);
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int nc = nb - geo.nr - c0;
   const bool ranked = ranked_select(geo, nc);
@@ -235,7 +234,7 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
 #pragma unroll
   for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
   if (n < G) {
-    const uint16_t* src = q + ((size_t)bi * geo.hq + h * G + n) * kHeadDim + 8 * g;
+    const uint16_t* src = q + q_row(sb, bi, h * G + n) + 8 * g;
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = *(const u32x4*)(src + 32 * s);
   }
@@ -247,7 +246,7 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
       wave_cand_load(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns,
                      geo.mbps, wc);
   }
-  const int len = uniform(geo.meta[seq]);
+  const int len = uniform(entry_len(geo, sb, bi, seq));
   int j, page;
   attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, jg, &wc, s_sel, s_selp, s_ws, j,
                           page);
@@ -344,7 +343,7 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
     store_empty<G>(s_m[wave], s_l[wave], s_o[wave], lane);
   }
   __syncthreads();
-  attend_merge<DT, G, W>(geo, bi, h, split, s_m, s_l, s_o, out, partials);
+  attend_merge<DT, G, W>(geo, sb, bi, h, split, s_m, s_l, s_o, out, partials);
 }
 
 // ---------------------------------------------------------------------------
@@ -364,7 +363,8 @@ __device__ __forceinline__ float block_reduce_128(float v, bool is_max, float* s
 }
 
 template <int DT>
-__global__ __launch_bounds__(128) void k_combine(Geometry geo, const float* __restrict__ partials,
+__global__ __launch_bounds__(128) void k_combine(Geometry geo, SeqBatch sb,
+                                                 const float* __restrict__ partials,
                                                  uint16_t* __restrict__ out) {
   __shared__ float s_w[kMaxSplits];
   __shared__ float s_red[2];
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(128) void k_combine(Geometry geo, const float* __re
   const float inv = wl > 0.f ? 1.f / wl : 0.f;
   float a = 0.f;
   for (int sp = 0; sp < ns; ++sp) a += s_w[sp] * pp[sp * (kHeadDim + 2) + d];
-  out[row * kHeadDim + d] = from_f32<DT>(a * inv);
+  out[q_row(sb, bi, hq) + d] = from_f32<DT>(a * inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -531,9 +531,9 @@ static hipError_t attend_impl(const Geometry& g, const SeqBatch& b, const void* 
   if (e != hipSuccess || g.nsplit == 1) return e;
   const float* pc = partials;
   if (g.dtype == 0)
-    launch(k_combine<0>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, pc, oo);
+    launch(k_combine<0>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, b, pc, oo);
   else
-    launch(k_combine<1>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, pc, oo);
+    launch(k_combine<1>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, b, pc, oo);
   return hipGetLastError();
 }
 

@@ -322,7 +322,7 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
 #pragma unroll
   for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
   if (n < G) {
-    const uint16_t* src = q + ((size_t)bi * geo.hq + h * G + n) * kHeadDim + 8 * g;
+    const uint16_t* src = q + q_row(sb, bi, h * G + n) + 8 * g;
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = *(const u32x4*)(src + 32 * s);
   }
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
       wave_cand_load(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns,
                      geo.mbps, wc);
   }
-  const int len = uniform(geo.meta[seq]);
+  const int len = uniform(entry_len(geo, sb, bi, seq));
   int j, page;
   attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, jg, &wc, s_sel, s_selp, s_ws, j,
                           page);
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
     store_empty<G>(s_m[wave], s_l[wave], s_o[wave], lane);
   }
   __syncthreads();
-  attend_merge<0, G, W>(geo, bi, h, split, s_m, s_l, s_o, out, partials);
+  attend_merge<0, G, W>(geo, sb, bi, h, split, s_m, s_l, s_o, out, partials);
 }
 
 // ---------------------------------------------------------------------------

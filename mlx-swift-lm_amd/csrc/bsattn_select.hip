@@ -106,14 +106,14 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
 #pragma unroll
   for (int s = 0; s < 4; ++s) qf[s] = qa[s] = u32x4{0u, 0u, 0u, 0u};
   if (n < G) {
-    const uint16_t* src = q + ((size_t)bi * geo.hq + h * G + n) * kHeadDim + 8 * g;
+    const uint16_t* src = q + q_row(sb, bi, h * G + n) + 8 * g;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       qf[s] = *(const u32x4*)(src + 32 * s);
       qa[s] = abs16x8(qf[s]);
     }
   }
-  const int len = geo.meta[seq];
+  const int len = entry_len(geo, sb, bi, seq);
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int c1 = nb - geo.nr;
   float* erow = err + ((size_t)bi * geo.hkv + h) * err_stride;
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
   load_scores<PER>(score_row(geo, scores, bi, h) + i0, sc);
   float ev = 0.0f;
   if (BAND && tid < 64 && lane < err_count) ev = err[((size_t)bi * geo.hkv + h) * err_stride + lane];
-  const int len = geo.meta[seq];
+  const int len = entry_len(geo, sb, bi, seq);
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int nc = nb - geo.nr - c0;
   int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
@@ -482,8 +482,8 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
   if constexpr (!BAND) {
     take = wg_topk_mask(kr, vmask, nc, K, ss, ph);
   } else {
-    const uint32_t* qsrc = (const uint32_t*)(q + ((size_t)bi * geo.hq + h * G) * kHeadDim);
-    for (int e = tid; e < G * kHeadDim / 2; e += kSelThreads) s_q[e] = qsrc[e];
+    for (int e = tid; e < G * kHeadDim / 2; e += kSelThreads)
+      s_q[e] = ((const uint32_t*)(q + q_row(sb, bi, h * G + e / (kHeadDim / 2))))[e % (kHeadDim / 2)];
     // the bound: maximum over the chunks' bounds (NaN bounds are skipped)
     if (tid < 64) {
       ev = wave_max_f32(ev);

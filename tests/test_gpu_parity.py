@@ -272,3 +272,47 @@ def test_profiling_counts_launches(gpu):
     assert cache.profileRead(_lib.KERNEL_SCORE)[1] == 4
     cache.profile(False)
     assert cache.profileRead(_lib.KERNEL_ATTEND) == (0.0, 0)
+
+
+@pytest.mark.parametrize("kv_bits", [0, 4])
+def test_prompt_cache_round_trip(gpu, tmp_path, kv_bits):
+    """savePromptCache / loadPromptCache (KVCache.swift:1244-1388) over real
+    layer caches: the reloaded caches export the same state and summaries
+    and decode bit-identically; the dense-compatible file loads into a
+    cache through its KVCache / QuantizedKVCache entry."""
+    import torch
+    from bsattn import loadPromptCache, savePromptCache
+    dt = "f16" if kv_bits else "bf16"
+    layers = []
+    for li in range(2):
+        w = make_workload(3400 + li, B=2, Hq=32, Hkv=8, T=700, Tb=64, dtype=dt, top_k=4)
+        c = new_cache(w, mbps=16, kv_bits=kv_bits)
+        fill(c, w, gpu)
+        layers.append((w, c))
+    path = str(tmp_path / "prompt.safetensors")
+    savePromptCache(path, [c for _, c in layers], {"model": "test"})
+
+    def make(i, cls, ms, state):
+        assert cls == "BlockSparseKVCache" and ms == layers[i][1].metaState
+        return new_cache(layers[i][0], mbps=16, kv_bits=kv_bits)
+
+    loaded, user = loadPromptCache(path, make)
+    assert user == {"model": "test"}
+    for (w, c), c2 in zip(layers, loaded):
+        for a, b in zip(c.state, c2.state):
+            assert torch.equal(a, b)
+        for b in range(w.B):
+            assert torch.equal(c.exportSummaries(b), c2.exportSummaries(b))
+        q = to_dev(w.q[:, :, None, :], w.dtype, gpu)
+        o1, o2 = c.decode(q, w.scale), c2.decode(q, w.scale)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2)
+    # the dense-compatible file: reference class names, same arrays
+    dpath = str(tmp_path / "dense.safetensors")
+    savePromptCache(dpath, [c for _, c in layers], dense_compatible=True)
+    want = "QuantizedKVCache" if kv_bits else "KVCache"
+    loaded, _ = loadPromptCache(dpath, lambda i, cls, ms, st: (cls == want or pytest.fail(cls))
+                                and new_cache(layers[i][0], mbps=16, kv_bits=kv_bits))
+    for (w, c), c2 in zip(layers, loaded):
+        for a, b in zip(c.state, c2.state):
+            assert torch.equal(a, b)
