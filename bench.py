@@ -100,7 +100,7 @@ def log(msg):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "pf"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=0, help="layer caches (0: the config's)")
@@ -495,6 +495,57 @@ def bench_loop(args):
     print(json.dumps(result), flush=True)
 
 
+def bench_prefill(args):
+    """Dense causal prefill attention of a 512-token chunk at the end of a
+    32768-token context (C2 geometry: B=8, Hq=32, Hkv=8, bf16, Tb=64), over
+    4 layer caches (4 GiB, beyond the 256 MB Infinity Cache).  MFMA-bound:
+    algorithmic FLOPs = 4 * D * sum over queries of the tokens they see."""
+    import torch
+    import bsattn
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, HQ, HKV, TB, T, L, LAYERS = 8, 32, 8, 64, 32768, 512, 4
+    g = torch.Generator(device=dev)
+    g.manual_seed(5005)
+    caches = []
+    for _ in range(LAYERS):
+        c = bsattn.BlockSparseKVCache(max_seqs=B, num_q_heads=HQ, num_kv_heads=HKV, head_dim=D,
+                                      block_size=TB, dtype=torch.bfloat16, top_k=32,
+                                      max_blocks_per_seq=T // TB + 2, device=0)
+        for b in range(B):
+            k = torch.randn(1, HKV, T, D, device=dev, generator=g).to(torch.bfloat16)
+            c.append(k, k, seq_ids=[b])
+        caches.append(c)
+    q = torch.randn(B, HQ, L, D, device=dev, generator=g).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    for i in range(args.warmup):
+        caches[i % LAYERS].prefill(q, scale)
+    torch.cuda.synchronize()
+    steps = args.steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        caches[i % LAYERS].prefill(q, scale)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    flops = 4.0 * D * B * HQ * sum(T - L + i + 1 for i in range(L))
+    tf = flops / (us * 1e-6) / 1e12
+    log(f"[bench] prefill chunk {L} at {T} ctx: {us:.1f} us/layer, {tf:.1f} TFLOP/s "
+        f"({100 * tf / 2500:.1f}% of 2.5 PFLOP/s bf16)")
+    print(json.dumps({
+        "metric": "dense causal prefill attention µs per layer, 512-token chunk at 32k ctx",
+        "value": round(us, 2), "unit": "us/layer", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic: torch RNG on device, N(0,1)",
+        "config": {"workload": "prefill chunk attention x4 distinct layer caches", "batch": B,
+                   "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": T, "chunk": L,
+                   "block_size": TB},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tf / 2500.0, 4), "traffic": None},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -504,6 +555,8 @@ def main():
         sys.exit(2)
     if args.config == "c4":
         bench_loop(args)
+    elif args.config == "pf":
+        bench_prefill(args)
     else:
         bench_layers(args, CONFIGS[args.config])
 

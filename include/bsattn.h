@@ -148,6 +148,16 @@ int bsattn_decode_multi(bsattn_cache* cache, const void* q,
                         int32_t n_query, float scale, void* out,
                         int32_t* idx_out, void* stream);
 
+/* Dense causal attention of the last n_query tokens of each listed sequence
+ * (a prefill chunk whose keys / values were appended): q / out
+ * [n_seqs, Hq, n_query, D]; query i of a sequence holding T tokens attends to
+ * tokens [0, T - n_query + i], as attentionWithCacheUpdate with L > 1 and
+ * the causal mask (AttentionUtils.swift:46-52, BaseKVCache.makeMask,
+ * KVCache.swift:160-174) computes over the whole cache.  16-bit caches. */
+int bsattn_prefill(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
+                   int32_t n_seqs, int32_t n_query, float scale, void* out,
+                   void* stream);
+
 /* Drops the last n_tokens of each listed sequence (clamped to its length);
  * writes the number trimmed per sequence to trimmed (host, may be NULL).
  * KVCacheSimple.trim (KVCache.swift:396-402). */
@@ -193,6 +203,7 @@ int bsattn_export_summaries(const bsattn_cache* cache, int32_t seq, void* out,
 #define BSATTN_KERNEL_COMBINE 3 /* split combine */
 #define BSATTN_KERNEL_APPEND 4  /* token append */
 #define BSATTN_KERNEL_SUMMARY 5 /* block summary refresh */
+#define BSATTN_KERNEL_PREFILL 6 /* dense causal prefill attention */
 int bsattn_profile_enable(bsattn_cache* cache, int32_t enable);
 int bsattn_profile_read(bsattn_cache* cache, int32_t kernel, double* total_ms,
                         int64_t* launches);

@@ -35,6 +35,7 @@ EXPORTS = (
     "bsattn_attend",
     "bsattn_decode",
     "bsattn_decode_multi",
+    "bsattn_prefill",
     "bsattn_trim",
     "bsattn_reset",
     "bsattn_copy",
@@ -45,7 +46,7 @@ EXPORTS = (
     "bsattn_profile_read",
 )
 
-KERNEL_SCORE, KERNEL_TOPK, KERNEL_ATTEND, KERNEL_COMBINE, KERNEL_APPEND, KERNEL_SUMMARY = range(6)
+KERNEL_SCORE, KERNEL_TOPK, KERNEL_ATTEND, KERNEL_COMBINE, KERNEL_APPEND, KERNEL_SUMMARY, KERNEL_PREFILL = range(7)
 
 
 class BsattnError(RuntimeError):
@@ -113,6 +114,7 @@ def lib() -> ctypes.CDLL:
         "bsattn_attend": (ctypes.c_int, [P, P, PI32, i32, P, ctypes.c_float, P, P]),
         "bsattn_decode": (ctypes.c_int, [P, P, PI32, i32, ctypes.c_float, P, P, P]),
         "bsattn_decode_multi": (ctypes.c_int, [P, P, PI32, i32, i32, ctypes.c_float, P, P, P]),
+        "bsattn_prefill": (ctypes.c_int, [P, P, PI32, i32, i32, ctypes.c_float, P, P]),
         "bsattn_trim": (ctypes.c_int, [P, PI32, i32, i32, PI32, P]),
         "bsattn_reset": (ctypes.c_int, [P, PI32, i32, P]),
         "bsattn_copy": (ctypes.c_int, [P, PP, P]),

@@ -14,7 +14,11 @@ import torch
 from .cache import BlockSparseKVCache
 
 
-MAX_QUERIES = 16  # query tokens per sequence of one multi-token pass
+# A pass of up to MAX_QUERIES tokens (the speculative-verify shape, L =
+# numDraft + 1) runs block-sparse, each query on its own prefix, so that its
+# outputs equal token-by-token decoding; longer passes (prefill chunks) run
+# dense causal attention, as the reference computes for L > 1.
+MAX_QUERIES = 16
 
 
 def attentionWithCacheUpdate(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
@@ -29,13 +33,14 @@ def attentionWithCacheUpdate(queries: torch.Tensor, keys: torch.Tensor, values: 
             raise ValueError("decode (L == 1) takes no mask (BaseKVCache.makeMask returns .none)")
         cache.append(keys, values)
         return cache.decode(queries, scale)
-    if L > MAX_QUERIES:
-        raise NotImplementedError(f"block-sparse attention serves decode and verify passes of up to "
-                                  f"{MAX_QUERIES} tokens; a {L}-token prefill is not provided")
     if mask != "causal":
         raise ValueError("a multi-token pass takes the causal mask (BaseKVCache.makeMask(n > 1))")
+    if L > MAX_QUERIES and cache.bits:
+        raise NotImplementedError("prefill attention over a quantized block-sparse cache is not provided")
     cache.append(keys, values)
-    return cache.decodeMulti(queries, scale)
+    if L <= MAX_QUERIES:
+        return cache.decodeMulti(queries, scale)
+    return cache.prefill(queries, scale)
 
 
 __all__ = ["attentionWithCacheUpdate"]

@@ -296,6 +296,19 @@ class BlockSparseKVCache:
                                         ctypes.c_float(scale), _ptr(out), idx_p, _stream(self.device)))
         return out
 
+    def prefill(self, queries: torch.Tensor, scale: float,
+                seq_ids: Optional[Sequence[int]] = None) -> torch.Tensor:
+        """Dense causal attention of the last L = queries.shape[2] tokens of
+        each sequence (a prefill chunk appended just before): query i of a
+        sequence holding T tokens attends to tokens [0, T - L + i], as the
+        reference's attentionWithCacheUpdate does for L > 1 with the causal
+        mask.  queries / result [B, Hq, L, D]; 16-bit caches."""
+        B = self._check_q(queries, multi=True)
+        out = torch.empty_like(queries)
+        check(lib().bsattn_prefill(self._h, _ptr(queries), i32_array(seq_ids), B, queries.shape[2],
+                                   ctypes.c_float(scale), _ptr(out), _stream(self.device)))
+        return out
+
     # -- kernel timing -------------------------------------------------------
     def profile(self, enable: bool = True) -> None:
         """Start (or stop) timing this cache's eager kernel launches; resets sums."""

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <climits>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -568,6 +569,43 @@ int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, 
   DeviceGuard dg(c->d.device);
   return run_entries(c, Op::Decode, q, entries(c, seqs, n_query), n_query * kHeadDim, nullptr, idx_out,
                      scale, out, (hipStream_t)stream);
+}
+
+int bsattn_prefill(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
+                   int32_t n_query, float scale, void* out, void* stream) {
+  if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (c->d.kv_bits != 0) return fail(BSATTN_ERR_INVALID, "prefill attention over a quantized cache is not provided");
+  if (n_query < 1) return fail(BSATTN_ERR_INVALID, "n_query must be >= 1");
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  for (int sq : seqs)
+    if (c->len[sq] < n_query)
+      return fail(BSATTN_ERR_INVALID, "sequence %d holds %d tokens, fewer than its %d queries", sq, c->len[sq],
+                  n_query);
+  DeviceGuard dg(c->d.device);
+  hipStream_t s = (hipStream_t)stream;
+  // q / out [n, Hq, L, D]: a launch takes whole sequences whose row offsets fit int32
+  const int64_t per_seq = (int64_t)c->geo.hq * n_query * kHeadDim;
+  const int step = (int)std::max<int64_t>(1, std::min<int64_t>(kMaxBatch, INT32_MAX / per_seq));
+  const int n = (int)seqs.size();
+  for (int i0 = 0; i0 < n; i0 += step) {
+    SeqBatch b{};
+    b.n = std::min(step, n - i0);
+    b.qhs = n_query * kHeadDim;
+    for (int i = 0; i < b.n; ++i) {
+      b.ids[i] = seqs[i0 + i];
+      b.len[i] = -1;
+      b.qoff[i] = (int32_t)(i * per_seq);
+    }
+    Timing tm[kProfKinds];
+    Timing* prof = prof_slots(c, s, tm);
+    hipError_t e = launch_prefill(c->geo, b, n_query, (const uint16_t*)q + i0 * per_seq, scale,
+                                  (uint16_t*)out + i0 * per_seq, s, prof);
+    prof_collect(c, prof);
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
+  }
+  return BSATTN_OK;
 }
 
 int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,

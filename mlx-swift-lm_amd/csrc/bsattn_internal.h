@@ -79,7 +79,7 @@ struct PatchBatch {
 // slot's events are set) and marks the slot used.
 enum ProfKind {
   kProfScore = 0, kProfTopk = 1, kProfAttend = 2, kProfCombine = 3, kProfAppend = 4,
-  kProfSummary = 5, kProfKinds = 6
+  kProfSummary = 5, kProfPrefill = 6, kProfKinds = 7
 };
 struct Timing {
   hipEvent_t start = nullptr, stop = nullptr;
@@ -129,6 +129,9 @@ int fused_select_limit(int top_k);
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                          int32_t* idx_out, int max_nc, float scale, void* out,
                          float* partials, hipStream_t s, Timing* prof);
+// dense causal attention of the last L tokens of each sequence (16-bit caches)
+hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
+                          void* out, hipStream_t s, Timing* prof);
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out,
                          void* v_out, hipStream_t s);
 hipError_t launch_export_quantized(const Geometry& g, const SeqBatch& b, int T,

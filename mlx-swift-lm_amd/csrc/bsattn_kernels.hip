@@ -553,6 +553,206 @@ hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, fl
   return attend_impl<true>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
 }
 
+// ---------------------------------------------------------------------------
+// dense causal attention for the last L tokens of each sequence (a prefill
+// chunk whose keys / values were appended): query token i of a sequence
+// holding T tokens sits at position T - L + i and attends to tokens
+// [0, T - L + i] (the causal mask BaseKVCache.makeMask gives for n > 1).
+// A wave owns R column sets of 16 MFMA columns, each column a (query token,
+// q head) pair (16 / G tokens x the G heads of kv head h), and streams the
+// K / V blocks from block 0 to its last token's block with an online
+// softmax per column:
+//   S^T[token][col] = K[token] . Q[col]        (A = K rows, B = Q^T)
+//   O^T[dim][col]  += V^T[dim] . P^T[col]      (A = V^T, B = P^T)
+// An MFMA's A and B operands take the same lane layout, so the
+// fragment-major K / V tiles and the P registers of the decode kernel serve
+// both products unchanged, and each lane holds the running max, sum and
+// O^T entries of its own column.  The R sets share every K / V load.
+// grid (ceil(L / (W * R * 16 / G)), Hkv, n)
+// ---------------------------------------------------------------------------
+template <int DT, int TB, int G, int R, int W>
+__global__ __launch_bounds__(64 * W, 1) void k_prefill(Geometry geo, SeqBatch sb, int L,
+                                                   const uint16_t* __restrict__ q, float sl2,
+                                                   uint16_t* __restrict__ out) {
+  constexpr int QPS = 16 / G;   // query tokens per column set
+  constexpr int NT = TB / 16;   // QK token tiles
+  constexpr int EPL = TB / 4;   // scores per lane
+  constexpr int KS2 = TB / 32;  // PV k-steps
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y, bi = blockIdx.z;
+  const int t0 = (blockIdx.x * W + wave) * R * QPS;  // the wave's first query token
+  if (t0 >= L) return;
+  const int seq = sb.ids[bi];
+  const int T = uniform(geo.meta[seq]);
+  const int head = h * G + n % G;
+  // column n of set r: query token t0 + r * QPS + n / G, at position pos[r]
+  int pos[R];
+  u32x4 qf[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int tq = t0 + r * QPS + n / G;
+    pos[r] = tq < L ? T - L + tq : -1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[r][s] = u32x4{0u, 0u, 0u, 0u};
+    if (tq < L) {
+      const uint16_t* src = q + q_row(sb, bi, head) + (size_t)tq * kHeadDim + 8 * g;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qf[r][s] = *(const u32x4*)(src + 32 * s);
+    }
+  }
+  const int last = T - L + min(L - 1, t0 + R * QPS - 1);  // the wave's last position
+  const int nblk = last / TB + 1;
+  const int32_t* bt = block_table(geo, seq);
+  float m[R], l[R];
+  f32x4 o[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[r][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll 1
+  for (int j = 0; j < nblk; ++j) {
+    const int page = uniform(bt[j]);
+    const int valid = min(TB, T - j * TB);
+    const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
+    const u32x4* Kf = (const u32x4*)(slab + geo.k_off) + lane;
+    const u32x4* Vf = (const u32x4*)(slab + geo.v_off) + lane;
+    u32x4 kf[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[t][s] = Kf[(t * 4 + s) * 64];
+    u32x4 vf[8][KS2];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < KS2; ++s2) vf[dt][s2] = Vf[(dt * KS2 + s2) * 64];
+    __builtin_amdgcn_sched_barrier(0);
+    // V of tokens past the sequence end (stale page data) is zeroed
+    if (valid < TB) {
+#pragma unroll
+      for (int s2 = 0; s2 < KS2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int u = 32 * s2 + 8 * g + 2 * jj;
+          const uint32_t mk = (u < valid ? 0x0000FFFFu : 0u) | (u + 1 < valid ? 0xFFFF0000u : 0u);
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) vf[dt][s2][jj] &= mk;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      f32x4 acc[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[t] = mfma16x16x32<DT>(kf[t][s], qf[r][s], acc[t]);
+      }
+      // scores (log2 domain), causal mask: token j*TB + tok_of(g, e) <= pos
+      float pv[EPL];
+      const int lim = pos[r] - j * TB;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * t + i;
+          pv[e] = tok_of(g, e) <= lim ? acc[t][i] * sl2 : -INFINITY;
+        }
+      float bm = pv[0];
+#pragma unroll
+      for (int e = 1; e < EPL; ++e) bm = fmaxf(bm, pv[e]);
+      bm = max_over_groups(bm);
+      // a column sees token 0 in block 0, so its maximum is finite from
+      // there on; a padded column (no query) stays at -inf and is not stored
+      const float mn = fmaxf(m[r], bm);
+      const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[r] - mn);
+      float ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        pv[e] = mn == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pv[e] - mn);
+        ps += pv[e];
+      }
+      ps = sum_over_groups(ps);
+      l[r] = l[r] * alpha + ps;
+      m[r] = mn;
+      // P^T operand: lane (column n, group g), k-step s2 -> tokens
+      // tok_of(g, 8 * s2 + 2 * jj (+1)); bf16 P is split into hi + lo
+      u32x4 pf[KS2], pl[KS2];
+#pragma unroll
+      for (int s2 = 0; s2 < KS2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float p0 = pv[8 * s2 + 2 * jj], p1 = pv[8 * s2 + 2 * jj + 1];
+          const uint32_t hi = cvt_pk<DT>(p0, p1);
+          pf[s2][jj] = hi;
+          if constexpr (DT == 1)
+            pl[s2][jj] = cvt_pk<1>(p0 - __uint_as_float(hi << 16), p1 - __uint_as_float(hi & 0xFFFF0000u));
+        }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        f32x4 a = o[r][dt];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] *= alpha;
+#pragma unroll
+        for (int s2 = 0; s2 < KS2; ++s2) {
+          a = mfma16x16x32<DT>(vf[dt][s2], pf[s2], a);
+          if constexpr (DT == 1) a = mfma16x16x32<DT>(vf[dt][s2], pl[s2], a);
+        }
+        o[r][dt] = a;
+      }
+    }
+  }
+  // O^T: lane (column n, group g) holds dims 16 dt + 4 g + i of its column
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (pos[r] < 0) continue;
+    const int tq = t0 + r * QPS + n / G;
+    const float inv = l[r] > 0.f ? 1.f / l[r] : 0.f;
+    uint16_t* dst = out + q_row(sb, bi, head) + (size_t)tq * kHeadDim + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint32_t lo = (uint32_t)from_f32<DT>(o[r][dt][0] * inv) | ((uint32_t)from_f32<DT>(o[r][dt][1] * inv) << 16);
+      const uint32_t hi = (uint32_t)from_f32<DT>(o[r][dt][2] * inv) | ((uint32_t)from_f32<DT>(o[r][dt][3] * inv) << 16);
+      *(uint2*)(dst + 16 * dt) = make_uint2(lo, hi);
+    }
+  }
+}
+
+template <int DT, int TB>
+static void prefill_dispatch(const Geometry& g, const SeqBatch& b, int L, const uint16_t* q, float sl2,
+                             uint16_t* out, hipStream_t s, Timing* prof) {
+  constexpr int W = 4, R = 2;
+  const int per_wg = W * R * (16 / g.group);
+  const dim3 grid((L + per_wg - 1) / per_wg, g.hkv, b.n), blk(64 * W);
+  const int kd = kProfPrefill;
+  switch (g.group) {
+    case 1: launch(k_prefill<DT, TB, 1, R, W>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 2: launch(k_prefill<DT, TB, 2, R, W>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 4: launch(k_prefill<DT, TB, 4, R, W>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 8: launch(k_prefill<DT, TB, 8, R, W>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    default: launch(k_prefill<DT, TB, 16, R, W>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+  }
+}
+
+hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
+                          void* out, hipStream_t s, Timing* prof) {
+  const float sl2 = scale * 1.4426950408889634f;
+  const uint16_t* qq = (const uint16_t*)q;
+  uint16_t* oo = (uint16_t*)out;
+  if (g.dtype == 0) {
+    if (g.tb == 64) prefill_dispatch<0, 64>(g, b, L, qq, sl2, oo, s, prof);
+    else prefill_dispatch<0, 32>(g, b, L, qq, sl2, oo, s, prof);
+  } else {
+    if (g.tb == 64) prefill_dispatch<1, 64>(g, b, L, qq, sl2, oo, s, prof);
+    else prefill_dispatch<1, 32>(g, b, L, qq, sl2, oo, s, prof);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out, void* v_out,
                          hipStream_t s) {
   dim3 grid((T + 15) / 16, g.hkv, b.n);

@@ -50,17 +50,6 @@ __device__ __forceinline__ u32x4 abs16x8(u32x4 v) {
   return u32x4{v[0] & 0x7FFF7FFFu, v[1] & 0x7FFF7FFFu, v[2] & 0x7FFF7FFFu, v[3] & 0x7FFF7FFFu};
 }
 
-// fmaxf over the wave's four 16-lane rows (lane l gets the maximum over
-// lanes l mod 16 + 16 r)
-__device__ __forceinline__ float max_rows(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const float y = fmaxf(__uint_as_float((uint32_t)a[0]), __uint_as_float((uint32_t)a[1]));
-  const uint32_t v = __float_as_uint(y);
-  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return fmaxf(__uint_as_float((uint32_t)b[0]), __uint_as_float((uint32_t)b[1]));
-}
-
 // fmaxf over the whole wave
 __device__ __forceinline__ float wave_max_f32(float x) {
   return __uint_as_float(wave_allreduce_u32(__float_as_uint(x), [](uint32_t a, uint32_t b) {
@@ -131,7 +120,7 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (4 * g + i < G) q1h = fmaxf(q1h, q1[i]);
-  const float q1max = max_rows(q1h);
+  const float q1max = max_over_groups(q1h);
   float emax = 0.0f;
   float* srow = score_row(geo, scores, bi, h);
 #pragma unroll
@@ -156,8 +145,8 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
         am = fmaxf(am, a[i]);
         bad = bad || __builtin_isnan(d[i]) || __builtin_isinf(d[i]);
       }
-    sc = max_rows(sc);
-    am = max_rows(am);
+    sc = max_over_groups(sc);
+    am = max_over_groups(am);
     // any non-finite head score makes the block's approximate score NaN
     const uint64_t bm = __ballot(bad);
     const bool any_bad = (((bm | (bm >> 16) | (bm >> 32) | (bm >> 48)) >> n) & 1ull) != 0ull;

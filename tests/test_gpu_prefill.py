@@ -1,0 +1,112 @@
+"""Dense causal prefill attention (bsattn_prefill): the last L tokens of
+each sequence attend causally to everything before them, as the reference's
+attentionWithCacheUpdate computes for L > 1 with the causal mask.  Every
+query is checked against the oracle's dense attention over its prefix."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from common import from_dev, log, make_workload, new_cache, output_error, to_dev
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _run(w, gpu, L, pre_lens=None):
+    """Caches holding each sequence minus its last L tokens, then the L
+    tokens appended and prefilled; returns (out [B, Hq, L, D] bits, q)."""
+    import torch
+    c = new_cache(w)
+    for b in range(w.B):
+        T = w.lens[b]
+        if T > L:
+            c.append(to_dev(np.ascontiguousarray(w.keys[b][None, :, :T - L]), w.dtype, gpu),
+                     to_dev(np.ascontiguousarray(w.values[b][None, :, :T - L]), w.dtype, gpu), seq_ids=[b])
+    nk = np.stack([w.keys[b][:, w.lens[b] - L:] for b in range(w.B)])
+    nv = np.stack([w.values[b][:, w.lens[b] - L:] for b in range(w.B)])
+    c.append(to_dev(nk, w.dtype, gpu), to_dev(nv, w.dtype, gpu))
+    qm = O.fill_normal(w.seed + 77, 0, 0, (w.B, w.Hq, L, w.D), w.dtype)
+    out = c.prefill(to_dev(qm, w.dtype, gpu), w.scale)
+    torch.cuda.synchronize()
+    return from_dev(out), qm, c
+
+
+def _check(w, got, qm, L, queries):
+    worst = 0.0
+    for b in range(w.B):
+        for i in queries:
+            pos = w.lens[b] - L + i
+            for h in range(w.Hkv):
+                ref = O.dense(qm[b, h * w.G:(h + 1) * w.G, i], w.keys[b][h][:pos + 1],
+                              w.values[b][h][:pos + 1], w.scale, w.dtype)
+                a = O.to_f32(got[b, h * w.G:(h + 1) * w.G, i], w.dtype).astype(np.float64)
+                err = output_error(a, ref, w.dtype)
+                assert err <= TOL, f"seq {b} query {i} head {h}: error {err:.3g}"
+                worst = max(worst, err)
+    return worst
+
+
+@pytest.mark.parametrize("dtype,Hq,Hkv,Tb,lens,L", [
+    ("bf16", 32, 8, 64, [3000, 2048], 100),
+    ("f16", 32, 8, 32, [1500, 1999], 77),
+    ("bf16", 64, 4, 64, [2600, 700], 64),     # G = 16: one query token per column set
+    ("f16", 8, 8, 64, [1100, 900], 40),       # G = 1: 16 query tokens per column set
+    ("bf16", 16, 2, 32, [640, 650], 33),      # G = 8
+])
+def test_prefill_matches_dense_attention(gpu, dtype, Hq, Hkv, Tb, lens, L):
+    log(f"[prefill] {dtype} G={Hq // Hkv} Tb={Tb} L={L}")
+    w = make_workload(7000 + Hq + Tb + L, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype=dtype,
+                      top_k=4, lens=lens, salient_frac=0.01)
+    got, qm, _ = _run(w, gpu, L)
+    err = _check(w, got, qm, L, sorted({0, 1, L // 2, L - 2, L - 1}))
+    log(f"[prefill] err={err:.3g}")
+
+
+def test_prefill_whole_prompt(gpu):
+    """The whole prompt in one pass from an empty cache (L = T): every
+    query checked, the first attends to itself only."""
+    w = make_workload(7100, B=2, Hq=32, Hkv=8, T=300, Tb=64, dtype="bf16", top_k=2, lens=[300, 300])
+    got, qm, c = _run(w, gpu, 300)
+    assert c.offset == 300
+    _check(w, got, qm, 300, range(0, 300, 7))
+    # the first query attends to token 0 only: output = v[0]
+    for b in range(w.B):
+        for hq in range(w.Hq):
+            assert np.array_equal(got[b, hq, 0], w.values[b][hq // w.G][0])
+
+
+def test_attention_with_cache_update_prefill(gpu):
+    import torch
+    from bsattn import attentionWithCacheUpdate
+    w = make_workload(7200, B=2, Hq=32, Hkv=8, T=500, Tb=64, dtype="bf16", top_k=2, lens=[500, 500])
+    L = 40
+    a = new_cache(w)
+    b = new_cache(w)
+    for c in (a, b):
+        c.append(to_dev(np.stack([k[:, :460] for k in w.keys]), "bf16", gpu),
+                 to_dev(np.stack([v[:, :460] for v in w.values]), "bf16", gpu))
+    nk = to_dev(np.stack([k[:, 460:] for k in w.keys]), "bf16", gpu)
+    nv = to_dev(np.stack([v[:, 460:] for v in w.values]), "bf16", gpu)
+    q = to_dev(O.fill_normal(7201, 0, 0, (2, 32, L, 128), "bf16"), "bf16", gpu)
+    o1 = attentionWithCacheUpdate(q, nk, nv, a, w.scale, mask="causal")
+    b.append(nk, nv)
+    o2 = b.prefill(q, w.scale)
+    torch.cuda.synchronize()
+    assert a.offset == 500 and torch.equal(o1, o2)
+
+
+def test_prefill_argument_errors(gpu):
+    import torch
+    from bsattn import BsattnError
+    w = make_workload(7300, B=1, Hq=32, Hkv=8, T=100, Tb=64, dtype="f16", top_k=2)
+    c = new_cache(w)
+    c.append(to_dev(w.keys[0][None], "f16", gpu), to_dev(w.values[0][None], "f16", gpu))
+    with pytest.raises(BsattnError):
+        c.prefill(torch.zeros((1, 32, 101, 128), dtype=torch.float16, device=gpu), 1.0)  # more queries than tokens
+    cq = new_cache(w, kv_bits=8)
+    cq.append(to_dev(w.keys[0][None], "f16", gpu), to_dev(w.values[0][None], "f16", gpu))
+    with pytest.raises(BsattnError):
+        cq.prefill(torch.zeros((1, 32, 50, 128), dtype=torch.float16, device=gpu), 1.0)  # quantized cache
