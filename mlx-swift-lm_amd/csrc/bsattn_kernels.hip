@@ -725,7 +725,7 @@ __global__ __launch_bounds__(64 * W, 1) void k_prefill(Geometry geo, SeqBatch sb
 template <int DT, int TB>
 static void prefill_dispatch(const Geometry& g, const SeqBatch& b, int L, const uint16_t* q, float sl2,
                              uint16_t* out, hipStream_t s, Timing* prof) {
-  constexpr int W = 4, R = 2;
+  constexpr int W = 4, R = 4;
   const int per_wg = W * R * (16 / g.group);
   const dim3 grid((L + per_wg - 1) / per_wg, g.hkv, b.n), blk(64 * W);
   const int kd = kProfPrefill;
