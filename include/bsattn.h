@@ -153,7 +153,9 @@ int bsattn_decode_multi(bsattn_cache* cache, const void* q,
  * [n_seqs, Hq, n_query, D]; query i of a sequence holding T tokens attends to
  * tokens [0, T - n_query + i], as attentionWithCacheUpdate with L > 1 and
  * the causal mask (AttentionUtils.swift:46-52, BaseKVCache.makeMask,
- * KVCache.swift:160-174) computes over the whole cache.  16-bit caches. */
+ * KVCache.swift:160-174) computes over the whole cache (for a quantized
+ * cache: quantizedScaledDotProductAttention with the causal mask,
+ * KVCache.swift:1533-1621). */
 int bsattn_prefill(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
                    int32_t n_seqs, int32_t n_query, float scale, void* out,
                    void* stream);

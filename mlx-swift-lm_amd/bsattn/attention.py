@@ -35,8 +35,6 @@ def attentionWithCacheUpdate(queries: torch.Tensor, keys: torch.Tensor, values: 
         return cache.decode(queries, scale)
     if mask != "causal":
         raise ValueError("a multi-token pass takes the causal mask (BaseKVCache.makeMask(n > 1))")
-    if L > MAX_QUERIES and cache.bits:
-        raise NotImplementedError("prefill attention over a quantized block-sparse cache is not provided")
     cache.append(keys, values)
     if L <= MAX_QUERIES:
         return cache.decodeMulti(queries, scale)

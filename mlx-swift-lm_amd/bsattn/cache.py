@@ -302,7 +302,7 @@ class BlockSparseKVCache:
         each sequence (a prefill chunk appended just before): query i of a
         sequence holding T tokens attends to tokens [0, T - L + i], as the
         reference's attentionWithCacheUpdate does for L > 1 with the causal
-        mask.  queries / result [B, Hq, L, D]; 16-bit caches."""
+        mask.  queries / result [B, Hq, L, D] (fp16 on a quantized cache)."""
         B = self._check_q(queries, multi=True)
         out = torch.empty_like(queries)
         check(lib().bsattn_prefill(self._h, _ptr(queries), i32_array(seq_ids), B, queries.shape[2],

@@ -574,7 +574,6 @@ int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, 
 int bsattn_prefill(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
                    int32_t n_query, float scale, void* out, void* stream) {
   if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
-  if (c->d.kv_bits != 0) return fail(BSATTN_ERR_INVALID, "prefill attention over a quantized cache is not provided");
   if (n_query < 1) return fail(BSATTN_ERR_INVALID, "n_query must be >= 1");
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);

@@ -129,9 +129,11 @@ int fused_select_limit(int top_k);
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                          int32_t* idx_out, int max_nc, float scale, void* out,
                          float* partials, hipStream_t s, Timing* prof);
-// dense causal attention of the last L tokens of each sequence (16-bit caches)
+// dense causal attention of the last L tokens of each sequence
 hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
                           void* out, hipStream_t s, Timing* prof);
+hipError_t launch_prefill_q(const Geometry& g, const SeqBatch& b, int L, const void* q, float sl2,
+                            void* out, hipStream_t s, Timing* prof);
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out,
                          void* v_out, hipStream_t s);
 hipError_t launch_export_quantized(const Geometry& g, const SeqBatch& b, int T,

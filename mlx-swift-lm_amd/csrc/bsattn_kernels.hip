@@ -741,6 +741,7 @@ static void prefill_dispatch(const Geometry& g, const SeqBatch& b, int L, const 
 hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
                           void* out, hipStream_t s, Timing* prof) {
   const float sl2 = scale * 1.4426950408889634f;
+  if (g.kv_bits != 0) return launch_prefill_q(g, b, L, q, sl2, out, s, prof);
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* oo = (uint16_t*)out;
   if (g.dtype == 0) {

@@ -106,7 +106,43 @@ def test_prefill_argument_errors(gpu):
     c.append(to_dev(w.keys[0][None], "f16", gpu), to_dev(w.values[0][None], "f16", gpu))
     with pytest.raises(BsattnError):
         c.prefill(torch.zeros((1, 32, 101, 128), dtype=torch.float16, device=gpu), 1.0)  # more queries than tokens
-    cq = new_cache(w, kv_bits=8)
-    cq.append(to_dev(w.keys[0][None], "f16", gpu), to_dev(w.values[0][None], "f16", gpu))
-    with pytest.raises(BsattnError):
-        cq.prefill(torch.zeros((1, 32, 50, 128), dtype=torch.float16, device=gpu), 1.0)  # quantized cache
+
+
+@pytest.mark.parametrize("bits,Hq,Hkv,Tb,lens,L", [
+    (4, 32, 8, 64, [2000, 1300], 90),
+    (8, 64, 4, 32, [1500, 800], 50),     # G = 16
+    (8, 16, 8, 64, [700, 900], 33),      # G = 2
+])
+def test_prefill_quantized_cache(gpu, bits, Hq, Hkv, Tb, lens, L):
+    """Prefill over an affine-quantized cache: each query against the
+    oracle's attention over the quantized keys / values of its prefix."""
+    import torch
+    GS = 64
+    log(f"[prefill-q] int{bits} G={Hq // Hkv} Tb={Tb} L={L}")
+    w = make_workload(7400 + bits + Hq + L, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype="f16",
+                      top_k=4, lens=lens)
+    c = new_cache(w, kv_bits=bits)
+    for b in range(w.B):
+        T = w.lens[b]
+        c.append(to_dev(np.ascontiguousarray(w.keys[b][None, :, :T - L]), "f16", gpu),
+                 to_dev(np.ascontiguousarray(w.values[b][None, :, :T - L]), "f16", gpu), seq_ids=[b])
+    c.append(to_dev(np.stack([w.keys[b][:, w.lens[b] - L:] for b in range(w.B)]), "f16", gpu),
+             to_dev(np.stack([w.values[b][:, w.lens[b] - L:] for b in range(w.B)]), "f16", gpu))
+    qm = O.fill_normal(w.seed + 78, 0, 0, (w.B, w.Hq, L, w.D), "f16")
+    got = from_dev(c.prefill(to_dev(qm, "f16", gpu), w.scale))
+    torch.cuda.synchronize()
+    worst = 0.0
+    for b in range(w.B):
+        kq = [O.quantize(w.keys[b][h], bits, GS) for h in range(w.Hkv)]
+        vq = [O.quantize(w.values[b][h], bits, GS) for h in range(w.Hkv)]
+        for i in sorted({0, 1, L // 2, L - 1}):
+            pos = w.lens[b] - L + i
+            idx = np.arange(pos // Tb + 1, dtype=np.int32)
+            for h in range(w.Hkv):
+                ref = O.attend_q(qm[b, h * w.G:(h + 1) * w.G, i], [a[:pos + 1] for a in kq[h]],
+                                 [a[:pos + 1] for a in vq[h]], Tb, bits, GS, idx, w.scale)
+                a = O.to_f32(got[b, h * w.G:(h + 1) * w.G, i], "f16").astype(np.float64)
+                err = output_error(a, ref, "f16")
+                assert err <= 1e-2, f"seq {b} query {i} head {h}: error {err:.3g}"
+                worst = max(worst, err)
+    log(f"[prefill-q] err={worst:.3g}")
