@@ -160,6 +160,25 @@ int bsattn_prefill(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
                    int32_t n_seqs, int32_t n_query, float scale, void* out,
                    void* stream);
 
+/* Graph-capturable decode loop.  bsattn_reserve takes the pages for
+ * n_tokens more tokens of each listed sequence now; bsattn_append_step then
+ * appends one token per listed sequence (k / v [n_seqs, Hkv, 1, D]) at the
+ * sequence's device-side length, writes the summary of a block it
+ * completes and advances that length, with no host bookkeeping, so a
+ * [bsattn_append_step, bsattn_decode] pair can be captured into a HIP graph
+ * and replayed once per step (a sequence whose reservation is used up
+ * takes no further tokens).  Until bsattn_sync copies the device-side
+ * lengths back (synchronizing the stream), calls that need exact token
+ * counts fail with BSATTN_ERR_INVALID; bsattn_decode / select / attend size
+ * their launches from the held pages and run.  16-bit caches.  (No
+ * reference counterpart: the reference's cache update is host-driven,
+ * KVCache.swift:328-371.) */
+int bsattn_reserve(bsattn_cache* cache, const int32_t* seq_ids,
+                   int32_t n_seqs, int32_t n_tokens, void* stream);
+int bsattn_append_step(bsattn_cache* cache, const void* k, const void* v,
+                       const int32_t* seq_ids, int32_t n_seqs, void* stream);
+int bsattn_sync(bsattn_cache* cache, void* stream);
+
 /* Drops the last n_tokens of each listed sequence (clamped to its length);
  * writes the number trimmed per sequence to trimmed (host, may be NULL).
  * KVCacheSimple.trim (KVCache.swift:396-402). */

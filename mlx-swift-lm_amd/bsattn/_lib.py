@@ -36,6 +36,9 @@ EXPORTS = (
     "bsattn_decode",
     "bsattn_decode_multi",
     "bsattn_prefill",
+    "bsattn_reserve",
+    "bsattn_append_step",
+    "bsattn_sync",
     "bsattn_trim",
     "bsattn_reset",
     "bsattn_copy",
@@ -115,6 +118,9 @@ def lib() -> ctypes.CDLL:
         "bsattn_decode": (ctypes.c_int, [P, P, PI32, i32, ctypes.c_float, P, P, P]),
         "bsattn_decode_multi": (ctypes.c_int, [P, P, PI32, i32, i32, ctypes.c_float, P, P, P]),
         "bsattn_prefill": (ctypes.c_int, [P, P, PI32, i32, i32, ctypes.c_float, P, P]),
+        "bsattn_reserve": (ctypes.c_int, [P, PI32, i32, i32, P]),
+        "bsattn_append_step": (ctypes.c_int, [P, P, P, PI32, i32, P]),
+        "bsattn_sync": (ctypes.c_int, [P, P]),
         "bsattn_trim": (ctypes.c_int, [P, PI32, i32, i32, PI32, P]),
         "bsattn_reset": (ctypes.c_int, [P, PI32, i32, P]),
         "bsattn_copy": (ctypes.c_int, [P, PP, P]),

@@ -143,6 +143,30 @@ class BlockSparseKVCache:
         check(lib().bsattn_append(self._h, _ptr(keys), _ptr(values), ids, B, L,
                                   _stream(self.device)))
 
+    # -- graph-capturable decode loop ------------------------------------------
+    def reserve(self, n_tokens: int, seq_ids: Optional[Sequence[int]] = None) -> None:
+        """Takes the pages for n_tokens more tokens of each sequence now, so
+        that appendStep needs no host work."""
+        ids = list(seq_ids) if seq_ids is not None else list(range(max(self.batchSize(), 1)))
+        check(lib().bsattn_reserve(self._h, i32_array(ids), len(ids), n_tokens, _stream(self.device)))
+
+    def appendStep(self, keys: torch.Tensor, values: torch.Tensor,
+                   seq_ids: Optional[Sequence[int]] = None) -> None:
+        """One token per sequence ([B, Hkv, 1, D]) at the device-side length,
+        which it advances: capturable in a CUDA/HIP graph and replayed once
+        per step (reserve first).  Until sync(), calls that need exact token
+        counts raise; decode runs."""
+        self._check_kv(keys, "keys")
+        self._check_kv(values, "values")
+        if keys.shape != values.shape or keys.shape[2] != 1:
+            raise ValueError("keys / values must both be [B, Hkv, 1, D]")
+        check(lib().bsattn_append_step(self._h, _ptr(keys), _ptr(values), i32_array(seq_ids), keys.shape[0],
+                                       _stream(self.device)))
+
+    def sync(self) -> None:
+        """Copies the device-side lengths back to the host view (waits for the stream)."""
+        check(lib().bsattn_sync(self._h, _stream(self.device)))
+
     def update(self, keys: torch.Tensor, values: torch.Tensor):
         """KVCache.update (KVCache.swift:328-371): append, then return all
         cached keys/values [B, Hkv, offset, D].  A quantized cache traps like

@@ -58,6 +58,9 @@ struct bsattn_cache {
   float* partials = nullptr;  // [rows][hq][nsplit][D + 2]
   float* err_ws = nullptr;    // [rows][hkv][mfma_err_stride]: MFMA score bounds
   std::vector<int32_t> len;
+  // set by bsattn_append_step: the device-side lengths may be ahead of `len`
+  // until bsattn_sync
+  bool stale = false;
   std::vector<std::vector<int32_t>> pages;
   std::vector<int32_t> free_pages;  // stack; back() is handed out next
   // opt-in per-kernel timing (bsattn_profile_*)
@@ -148,12 +151,19 @@ int flush_patches(bsattn_cache* c, std::vector<std::pair<int32_t, int32_t>>& p, 
   return BSATTN_OK;
 }
 
-int release_pages(bsattn_cache* c, int seq, int keep_blocks) {
+// device-side capacity of a sequence: tokens its pages hold
+void cap_patch(const bsattn_cache* c, int seq, std::vector<std::pair<int32_t, int32_t>>& patches) {
+  patches.emplace_back(c->geo.cap_off + seq, (int32_t)c->pages[seq].size() * c->d.block_size);
+}
+
+int release_pages(bsattn_cache* c, int seq, int keep_blocks,
+                  std::vector<std::pair<int32_t, int32_t>>& patches) {
   auto& pg = c->pages[seq];
   while ((int)pg.size() > keep_blocks) {
     c->free_pages.push_back(pg.back());
     pg.pop_back();
   }
+  cap_patch(c, seq, patches);
   return BSATTN_OK;
 }
 
@@ -182,6 +192,7 @@ int reserve_pages(bsattn_cache* c, const std::vector<int32_t>& seqs, int L,
       patches.emplace_back(c->geo.bt_off + s * c->d.max_blocks_per_seq + (int)pg.size(), p);
       pg.push_back(p);
     }
+    cap_patch(c, s, patches);
   }
   return BSATTN_OK;
 }
@@ -286,6 +297,7 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   g.mbps = d.max_blocks_per_seq;
   g.sstride = (g.mbps + 63) & ~63;
   g.bt_off = d.max_seqs;
+  g.cap_off = d.max_seqs * (1 + d.max_blocks_per_seq);
   // slab: K tile then V tile (16-bit elements, or b-bit codes), then for
   // quantized caches 16 B of scales / biases per token
   g.k_off = 0;
@@ -294,7 +306,7 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   g.slab_bytes = g.sb_off + (d.kv_bits ? (int64_t)d.block_size * 16 : 0);
   c->pool_bytes = (size_t)c->num_pages * g.hkv * g.slab_bytes;
   c->summ_bytes = (size_t)d.max_seqs * g.hkv * g.mbps * kHeadDim * 2;
-  c->meta_words = (size_t)d.max_seqs * (1 + d.max_blocks_per_seq);
+  c->meta_words = (size_t)d.max_seqs * (2 + d.max_blocks_per_seq);
   auto cleanup = [&](int code) {
     (void)hipFree(g.pool);
     (void)hipFree(g.summ);
@@ -359,10 +371,75 @@ int bsattn_cache_info(const bsattn_cache* c, bsattn_info* out) {
   return BSATTN_OK;
 }
 
+// Calls that need the exact token counts refuse while device-side appends
+// (bsattn_append_step) may have advanced them past the host's view.
+static int check_synced(const bsattn_cache* c) {
+  if (c->stale)
+    return fail(BSATTN_ERR_INVALID, "device-side lengths may be ahead of the host's view "
+                                    "(bsattn_append_step): call bsattn_sync first");
+  return BSATTN_OK;
+}
+
 int bsattn_seq_len(const bsattn_cache* c, int32_t seq, int32_t* out_len) {
   if (!c || !out_len) return fail(BSATTN_ERR_INVALID, "null argument");
   if (seq < 0 || seq >= c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "sequence id %d out of range", seq);
+  int rc = check_synced(c);
+  if (rc) return rc;
   *out_len = c->len[seq];
+  return BSATTN_OK;
+}
+
+int bsattn_reserve(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
+                   void* stream) {
+  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (n_tokens < 0) return fail(BSATTN_ERR_INVALID, "n_tokens must be >= 0");
+  std::vector<int32_t> seqs;
+  int rc = check_synced(c);
+  if (rc) return rc;
+  rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  DeviceGuard dg(c->d.device);
+  std::vector<std::pair<int32_t, int32_t>> patches;
+  rc = reserve_pages(c, seqs, n_tokens, patches);
+  if (rc) return rc;
+  return flush_patches(c, patches, (hipStream_t)stream);
+}
+
+int bsattn_append_step(bsattn_cache* c, const void* k, const void* v, const int32_t* seq_ids,
+                       int32_t n_seqs, void* stream) {
+  if (!c || !k || !v) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (c->d.kv_bits != 0)
+    return fail(BSATTN_ERR_INVALID, "device-side appends are provided for 16-bit caches");
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  DeviceGuard dg(c->d.device);
+  hipStream_t s = (hipStream_t)stream;
+  const size_t row = (size_t)c->geo.hkv * kHeadDim;  // elements per sequence
+  for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
+    AppendBatch ab{};
+    ab.n = std::min(kMaxBatch, n_seqs - i0);
+    ab.L = 1;
+    for (int i = 0; i < ab.n; ++i) ab.seq[i] = seqs[i0 + i];
+    Timing tm[kProfKinds];
+    Timing* prof = prof_slots(c, s, tm);
+    hipError_t e = launch_append_step(c->geo, ab, (const uint16_t*)k + i0 * row,
+                                      (const uint16_t*)v + i0 * row, s, prof);
+    prof_collect(c, prof);
+    if (e != hipSuccess) return hip_fail(e, "append step launch");
+  }
+  c->stale = true;
+  return BSATTN_OK;
+}
+
+int bsattn_sync(bsattn_cache* c, void* stream) {
+  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  DeviceGuard dg(c->d.device);
+  HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+  std::vector<int32_t> dev(c->d.max_seqs);
+  HIP_TRY(hipMemcpy(dev.data(), c->geo.meta, dev.size() * 4, hipMemcpyDeviceToHost), "hipMemcpy(lengths)");
+  c->len = dev;
+  c->stale = false;
   return BSATTN_OK;
 }
 
@@ -374,7 +451,9 @@ int append_impl(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t
                        hipStream_t s, F kernels) {
   if (n_tokens < 1) return fail(BSATTN_ERR_INVALID, "n_tokens must be >= 1 (got %d)", n_tokens);
   std::vector<int32_t> seqs;
-  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  int rc = check_synced(c);
+  if (rc) return rc;
+  rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
   std::vector<std::pair<int32_t, int32_t>> patches;
@@ -469,7 +548,12 @@ static std::vector<Entry> entries(const bsattn_cache* c, const std::vector<int32
   return es;
 }
 
-static int visible(const bsattn_cache* c, const Entry& e) { return e.len >= 0 ? e.len : c->len[e.seq]; }
+// Tokens an entry may see, for sizing launches: its own count, or every
+// token its pages hold (the device-side length, which graph-replayed appends
+// advance, never exceeds that); the kernels read the actual length.
+static int visible(const bsattn_cache* c, const Entry& e) {
+  return e.len >= 0 ? e.len : (int)c->pages[e.seq].size() * c->d.block_size;
+}
 
 // the launch batch for entries [e0, e0 + n); q / out offsets relative to entry e0
 static SeqBatch make_batch(const std::vector<Entry>& es, int e0, int n, int qhs) {
@@ -557,6 +641,7 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
 int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
                         int32_t n_query, float scale, void* out, int32_t* idx_out, void* stream) {
   if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(c)) return rs;
   if (n_query < 1 || n_query > kMaxQueries)
     return fail(BSATTN_ERR_INVALID, "n_query %d out of range [1, %d]", n_query, kMaxQueries);
   std::vector<int32_t> seqs;
@@ -574,6 +659,7 @@ int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, 
 int bsattn_prefill(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
                    int32_t n_query, float scale, void* out, void* stream) {
   if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(c)) return rs;
   if (n_query < 1) return fail(BSATTN_ERR_INVALID, "n_query must be >= 1");
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
@@ -610,6 +696,7 @@ int bsattn_prefill(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32
 int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
                 int32_t* trimmed, void* stream) {
   if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(c)) return rs;
   if (n_tokens < 0) return fail(BSATTN_ERR_INVALID, "n_tokens must be >= 0");
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
@@ -621,7 +708,7 @@ int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t
     const int t = std::min(c->len[sq], n_tokens);
     if (trimmed) trimmed[i] = t;
     c->len[sq] -= t;
-    release_pages(c, sq, (c->len[sq] + c->d.block_size - 1) / c->d.block_size);
+    release_pages(c, sq, (c->len[sq] + c->d.block_size - 1) / c->d.block_size, patches);
     patches.emplace_back(sq, c->len[sq]);
   }
   return flush_patches(c, patches, (hipStream_t)stream);
@@ -629,6 +716,7 @@ int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t
 
 int bsattn_reset(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* stream) {
   if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(c)) return rs;
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
@@ -636,7 +724,7 @@ int bsattn_reset(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* 
   std::vector<std::pair<int32_t, int32_t>> patches;
   for (int sq : seqs) {
     c->len[sq] = 0;
-    release_pages(c, sq, 0);
+    release_pages(c, sq, 0, patches);
     patches.emplace_back(sq, 0);
   }
   return flush_patches(c, patches, (hipStream_t)stream);
@@ -644,6 +732,7 @@ int bsattn_reset(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* 
 
 int bsattn_copy(const bsattn_cache* src, bsattn_cache** out, void* stream) {
   if (!src || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(src)) return rs;
   int rc = bsattn_cache_create(&src->d, out);
   if (rc) return rc;
   bsattn_cache* c = *out;
@@ -666,6 +755,7 @@ int bsattn_copy(const bsattn_cache* src, bsattn_cache** out, void* stream) {
 int bsattn_export(const bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* k_out,
                   void* v_out, void* stream) {
   if (!c || !k_out || !v_out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(c)) return rs;
   if (c->d.kv_bits != 0) return fail(BSATTN_ERR_INVALID, "quantized cache: use bsattn_export_quantized");
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
@@ -694,6 +784,7 @@ int bsattn_export_quantized(const bsattn_cache* c, const int32_t* seq_ids, int32
                             uint32_t* k_w, void* k_s, void* k_b, uint32_t* v_w, void* v_s,
                             void* v_b, void* stream) {
   if (!c || !k_w || !k_s || !k_b || !v_w || !v_s || !v_b) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(c)) return rs;
   if (c->d.kv_bits == 0) return fail(BSATTN_ERR_INVALID, "not a quantized cache (kv_bits 0): use bsattn_export");
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
@@ -723,6 +814,7 @@ int bsattn_export_quantized(const bsattn_cache* c, const int32_t* seq_ids, int32
 
 int bsattn_export_summaries(const bsattn_cache* c, int32_t seq, void* out, void* stream) {
   if (!c || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(c)) return rs;
   if (seq < 0 || seq >= c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "sequence id %d out of range", seq);
   const int nfull = c->len[seq] / c->d.block_size;
   if (nfull == 0) return BSATTN_OK;

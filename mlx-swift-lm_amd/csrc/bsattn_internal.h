@@ -33,13 +33,14 @@ struct Geometry {
   int32_t mbps;               // block-table width
   int32_t sstride;            // block-score row stride (mbps rounded up to 64)
   int32_t bt_off;             // offset of the block table inside meta
+  int32_t cap_off;            // offset of the per-sequence capacities (tokens of held pages)
   int64_t slab_bytes;         // bytes of one (page, kv head) slab
   // byte offsets inside a slab: K tile (or K codes), V tile (or V codes),
   // per-token scales / biases (quantized caches only)
   int64_t k_off, v_off, sb_off;
   uint8_t* pool;              // [num_pages][hkv] slabs
   uint16_t* summ;             // [max_seqs][hkv][mbps][D], by logical block
-  int32_t* meta;              // [max_seqs] lengths, then [max_seqs][mbps] pages
+  int32_t* meta;              // [max_seqs] lengths, [max_seqs][mbps] pages, [max_seqs] capacities
 };
 
 // A launch's batch entries: entry i is a query of sequence ids[i] that sees
@@ -94,6 +95,10 @@ hipError_t launch_append(const Geometry& g, const AppendBatch& ab, const void* k
                          const void* v, bool fuse_summary, hipStream_t s, Timing* prof);
 // quantized caches (bsattn_quant.hip): append from fp16 (quantize on append)
 // or from the MLX layout; block summaries of dequantized keys; attention
+// one token per listed sequence at its device-side length, then the lengths
+// advanced (no host bookkeeping: capturable in a HIP graph)
+hipError_t launch_append_step(const Geometry& g, const AppendBatch& ab, const void* k, const void* v,
+                              hipStream_t s, Timing* prof);
 hipError_t launch_append_q16(const Geometry& g, const AppendBatch& ab, const void* k,
                              const void* v, hipStream_t s, Timing* prof);
 hipError_t launch_append_quantized(const Geometry& g, const AppendBatch& ab,

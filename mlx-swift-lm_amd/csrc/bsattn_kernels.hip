@@ -64,13 +64,21 @@ __device__ __forceinline__ void summary16(const Geometry& geo, const uint16_t* _
 template <int DT>
 __global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
                                                 const uint16_t* __restrict__ k,
-                                                const uint16_t* __restrict__ v, bool fuse_summary) {
+                                                const uint16_t* __restrict__ v, bool fuse_summary,
+                                                bool device_len) {
   const int bi = blockIdx.z, h = blockIdx.y;
   const int tok = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int c = threadIdx.x & 15;
   if (tok >= ab.L) return;
   const int seq = ab.seq[bi];
-  const int pos = ab.old_len[bi] + tok;
+  // device_len: the position is the device-side length (one token; a
+  // sequence without a reserved page for it takes nothing)
+  int base = ab.old_len[bi];
+  if (device_len) {
+    base = geo.meta[seq];
+    if (base >= geo.meta[geo.cap_off + seq]) return;
+  }
+  const int pos = base + tok;
   const int blk = pos / geo.tb, slot = pos - blk * geo.tb;
   const int page = block_table(geo, seq)[blk];
   const size_t src = (((size_t)bi * geo.hkv + h) * ab.L + tok) * kHeadDim + 8 * c;
@@ -433,8 +441,30 @@ hipError_t launch_append(const Geometry& g, const AppendBatch& ab, const void* k
                          bool fuse_summary, hipStream_t s, Timing* prof) {
   dim3 grid((ab.L + 15) / 16, g.hkv, ab.n);
   const uint16_t *kk = (const uint16_t*)k, *vv = (const uint16_t*)v;
-  if (g.dtype == 0) launch(k_append<0>, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, kk, vv, fuse_summary);
-  else launch(k_append<1>, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, kk, vv, fuse_summary);
+  if (g.dtype == 0) launch(k_append<0>, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, kk, vv, fuse_summary, false);
+  else launch(k_append<1>, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, kk, vv, fuse_summary, false);
+  return hipGetLastError();
+}
+
+// advances the device-side length of each listed sequence by one token when
+// a reserved page held it (after k_append's device-length step)
+__global__ __launch_bounds__(64) void k_advance(Geometry geo, AppendBatch ab) {
+  for (int i = threadIdx.x; i < ab.n; i += 64) {
+    const int seq = ab.seq[i];
+    const int len = geo.meta[seq];
+    if (len < geo.meta[geo.cap_off + seq]) geo.meta[seq] = len + 1;
+  }
+}
+
+hipError_t launch_append_step(const Geometry& g, const AppendBatch& ab, const void* k, const void* v,
+                              hipStream_t s, Timing* prof) {
+  dim3 grid(1, g.hkv, ab.n);
+  const uint16_t *kk = (const uint16_t*)k, *vv = (const uint16_t*)v;
+  if (g.dtype == 0) launch(k_append<0>, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, kk, vv, true, true);
+  else launch(k_append<1>, grid, dim3(256), 0, s, prof, kProfAppend, g, ab, kk, vv, true, true);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, g, ab);
   return hipGetLastError();
 }
 

@@ -83,6 +83,9 @@ def test_null_arguments_are_errors():
     assert L.bsattn_decode(None, None, None, 1, ctypes.c_float(1.0), None, None, None) == -1
     assert L.bsattn_decode_multi(None, None, None, 1, 2, ctypes.c_float(1.0), None, None, None) == -1
     assert L.bsattn_prefill(None, None, None, 1, 64, ctypes.c_float(1.0), None, None) == -1
+    assert L.bsattn_reserve(None, None, 1, 1, None) == -1
+    assert L.bsattn_append_step(None, None, None, None, 1, None) == -1
+    assert L.bsattn_sync(None, None) == -1
     assert L.bsattn_select(None, None, None, 1, None, None) == -1
     assert L.bsattn_cache_info(None, None) == -1
     assert L.bsattn_append_quantized(None, None, None, None, None, None, None, None, 1, 1, None) == -1
