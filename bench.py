@@ -475,6 +475,29 @@ def bench_loop(args):
             total += ms * 1e3 / steps
     cache.profile(False)
     log(f"[bench] c4: {us_step:.2f} us/step eager, kernels {total:.2f} us/step")
+    # the same steps as a HIP graph: reserve pages, capture one [appendStep,
+    # decode] step, replay it per step with that step's inputs copied in
+    cache.trim(steps, list(range(B)))
+    cache.reserve(steps + 1, list(range(B)))
+    kb, vb, qb = kn[args.warmup].clone(), vn[args.warmup].clone(), qs[args.warmup].clone()
+    cache.appendStep(kb, vb)  # warm-up (one extra token)
+    cache.decode(qb, scale)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cache.appendStep(kb, vb)
+        cache.decode(qb, scale)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, args.warmup + steps):
+        kb.copy_(kn[i])
+        vb.copy_(vn[i])
+        qb.copy_(qs[i])
+        graph.replay()
+    torch.cuda.synchronize()
+    us_graph = (time.perf_counter() - t0) * 1e6 / steps
+    cache.sync()
+    log(f"[bench] c4: {us_graph:.2f} us/step as a replayed HIP graph (inputs copied in per step)")
     nsel = K + 2
     gather = int(B * HKV * nsel * TB * 2 * D * 2)
     result = {
@@ -489,6 +512,7 @@ def bench_loop(args):
                    "sink_blocks": 1, "recent_blocks": 1, "pages": pages,
                    "timing": "eager wall clock per step (ctypes launches included)"},
         "kernels_us_per_step": kern, "kernel_us_per_step_total": round(total, 3),
+        "graph_us_per_step": round(us_graph, 3),
         "gather_bytes_per_step": gather,
         "gather_GBps_at_kernel_time": round(gather / (total * 1e-6) / 1e9, 1) if total else None,
     }
