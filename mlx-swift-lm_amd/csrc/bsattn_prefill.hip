@@ -1,0 +1,299 @@
+// bsattn_prefill.hip -- gfx950 (CDNA4) dense causal attention of a prefill
+// chunk over a 16-bit block-sparse cache (the quantized caches' version is
+// in bsattn_quant.hip).
+//
+// Built with -fno-honor-nans -mno-amdgpu-ieee: the scores are MFMA results
+// (never signalling NaNs), so max trees compile to v_max3_f32 without the
+// operand quieting IEEE mode asks for.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+// (the shared header's NaN-aware helpers are not used here)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wnan-infinity-disabled"
+#include "bsattn_device.h"
+#pragma clang diagnostic pop
+
+namespace bsattn {
+
+// ---------------------------------------------------------------------------
+// dense causal attention for the last L tokens of each sequence (a prefill
+// chunk whose keys / values were appended): query token i of a sequence
+// holding T tokens sits at position T - L + i and attends to tokens
+// [0, T - L + i] (the causal mask BaseKVCache.makeMask gives for n > 1).
+// A wave owns R column sets of 16 MFMA columns, each column a (query token,
+// q head) pair (16 / G tokens x the G heads of kv head h); the workgroup's
+// W waves take consecutive tokens of one (sequence, kv head) and stream its
+// K / V blocks from block 0 to the last one any of them sees, with an online
+// softmax per column:
+//   S^T[token][col] = K[token] . Q[col]        (A = K rows, B = Q^T)
+//   O^T[dim][col]  += V^T[dim] . P^T[col]      (A = V^T, B = P^T)
+// An MFMA's A and B operands take the same lane layout, so the
+// fragment-major K / V tiles and the P registers of the decode kernel serve
+// both products unchanged, and each lane holds the running max, sum and
+// O^T entries of its own column.
+// The K / V blocks are streamed in units of 32 tokens (a block of 32, or
+// half of a block of 64: 8 K and 8 V fragments of 1 KiB), each loaded from
+// memory once per workgroup into one of two 16 KiB LDS buffers (every wave
+// fetches 16 / W fragments): the loads of unit u + 1 are in flight while the
+// workgroup computes unit u from the other buffer.  A wave reads each
+// fragment from LDS once and applies it to all R column sets.
+// The workgroups of one (sequence, kv head) read the same blocks, so the
+// flat workgroup index is remapped to give them consecutive indices within
+// one XCD (workgroups are dealt to the 8 XCDs in turn): they then share that
+// XCD's L2 instead of fetching every block into all eight.
+// grid (ceil(L / (W * R * 16 / G)), Hkv, n)
+// ---------------------------------------------------------------------------
+template <int DT, int TB, int G, int R, int W, int OCC>
+__global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch sb, int L,
+                                                   const uint16_t* __restrict__ q, float sl2,
+                                                   uint16_t* __restrict__ out) {
+  constexpr int QPS = 16 / G;   // query tokens per column set
+  constexpr int KS2 = TB / 32;  // 32-token units (PV k-steps) of a block
+  constexpr int FPW = 16 / W;   // fragments of a unit each wave fetches
+  static_assert(16 % W == 0 && (W == 1 || 8 % W == 0), "fragments split evenly over the waves");
+  // the running maximum a column's weights are taken against is raised only
+  // when a block's maximum exceeds it by more than 2^kLazy: the weights then
+  // stay below 2^kLazy, and the rescaling of O^T (a pass over its registers)
+  // is skipped for most blocks; O^T / l is unchanged by the choice
+  constexpr float kLazy = 8.f;
+  __shared__ __align__(16) u32x4 s_kv0[16 * 64], s_kv1[16 * 64];
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  // XCD-grouped workgroup order (a bijection on [0, total))
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int total = gx * gy * gridDim.z;
+  const int flat = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const int even = total & ~7;
+  const int lid = flat < even ? (flat & 7) * (even >> 3) + (flat >> 3) : flat;
+  const int bx = lid % gx, h = (lid / gx) % gy, bi = lid / (gx * gy);
+  const int twg = bx * W * R * QPS;     // the workgroup's first query token
+  const int t0 = twg + wave * R * QPS;  // this wave's
+  const bool active = t0 < L;
+  const int seq = sb.ids[bi];
+  const int T = uniform(geo.meta[seq]);
+  const int head = h * G + n % G;
+  // scores are taken as (K . Q') * |sl2| with Q' = Q * sign(sl2): the sign
+  // flip is exact, and a positive factor lets the block maximum be found on
+  // the raw products
+  const uint32_t qflip = sl2 < 0.f ? 0x80008000u : 0u;
+  const float sc = fabsf(sl2);
+  // column n of set r: query token t0 + r * QPS + n / G, at position pos[r];
+  // a padding column (no query token) has Q = 0, sees every token and is not
+  // stored
+  int pos[R];
+  u32x4 qf[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int tq = t0 + r * QPS + n / G;
+    pos[r] = tq < L ? T - L + tq : T;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[r][s] = u32x4{0u, 0u, 0u, 0u};
+    if (tq < L) {
+      const uint16_t* src = q + q_row(sb, bi, head) + (size_t)tq * kHeadDim + 8 * g;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qf[r][s] = *(const u32x4*)(src + 32 * s) ^ qflip;
+    }
+  }
+  const int last = T - L + min(L - 1, twg + W * R * QPS - 1);  // the workgroup's last position
+  const int nunit = last / 32 + 1;
+  // units below nfull are whole and visible to every column of the wave
+  const int nfull = (T - L + t0 + 1) / 32;
+  const int32_t* bt = block_table(geo, seq);
+  // this wave's fragments of unit u go straight from memory into LDS
+  // (global_load_lds: lane i's 16 bytes land at dst + 16 i).  Buffer slot
+  // f = wave + i * W: K fragment 8 hh + f of the block for f < 8 (QK tiles
+  // 2 hh, 2 hh + 1), V fragment (f - 8) * KS2 + hh (dims 16 (f - 8) ..,
+  // PV k-step hh) for f >= 8, where hh = u % KS2
+  auto fetch = [&](int u, u32x4* buf) __attribute__((always_inline)) {
+    const int page = uniform(bt[u / KS2]), hh = u % KS2;
+    const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
+    const u32x4* Kf = (const u32x4*)(slab + geo.k_off) + (8 * hh + wave) * 64 + lane;
+    const u32x4* Vf = (const u32x4*)(slab + geo.v_off) + (wave * KS2 + hh) * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < FPW; ++i)
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(i < 8 / W ? Kf + i * W * 64 : Vf + (i - 8 / W) * W * KS2 * 64),
+          (__attribute__((address_space(3))) void*)(buf + (wave + i * W) * 64), 16, 0, 0);
+  };
+  float m[R], l[R], thr[R];
+  f32x4 o[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    m[r] = -INFINITY;
+    thr[r] = -INFINITY;
+    l[r] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[r][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // unit u from LDS (tokens 32 u .. 32 u + 31 of the sequence); MASK: the
+  // causal limit and the sequence end apply
+  auto unit = [&](int u, const u32x4* kv, auto mask_tag) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    f32x4 acc[R][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      u32x4 kf[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[s] = kv[(t * 4 + s) * 64];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[r][t] = mfma16x16x32<DT>(kf[s], qf[r][s], acc[r][t]);
+      }
+    }
+    // P^T operand: lane (column n, group g) -> tokens 32 u + tok_of(g,
+    // 2 jj (+1)); bf16 P is split into hi + lo
+    u32x4 pf[R], pl[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float x[8];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * t + i] = acc[r][t][i];
+      if constexpr (MASK) {
+        // causal: token 32 u + tok_of(g, e) <= pos (which is below T)
+        const int lim = pos[r] - 32 * u;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = tok_of(g, e) <= lim ? x[e] : -INFINITY;
+      }
+      // the column's maximum is needed only when some lane's scores pass
+      // the raising threshold thr = (m + kLazy) / sc
+      const float lm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      if (__builtin_amdgcn_ballot_w64(lm > thr[r])) {
+        // every column sees token 0 in block 0, so bm is finite there
+        const float bm = max_over_groups(lm) * sc;
+        const bool raise = bm > m[r] + kLazy;
+        const float mn = raise ? bm : m[r];
+        const float alpha = __builtin_amdgcn_exp2f(m[r] - mn);  // 0 from -inf
+        l[r] *= alpha;
+        m[r] = mn;
+        thr[r] = (mn + kLazy) / sc;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[r][dt][i] *= alpha;
+      }
+      float ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -m[r]));
+        ps += x[e];
+      }
+      l[r] += ps;  // this lane's tokens; the column's groups are summed at the end
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float p0 = x[2 * jj], p1 = x[2 * jj + 1];
+        const uint32_t hi = cvt_pk<DT>(p0, p1);
+        pf[r][jj] = hi;
+        if constexpr (DT == 1)
+          pl[r][jj] = cvt_pk<1>(p0 - __uint_as_float(hi << 16), p1 - __uint_as_float(hi & 0xFFFF0000u));
+      }
+    }
+    const int valid = min(32, T - 32 * u);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      u32x4 vf = kv[(8 + dt) * 64];
+      if constexpr (MASK) {
+        // V of tokens past the sequence end (stale page data) is zeroed
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int tk = 8 * g + 2 * jj;
+          vf[jj] &= (tk < valid ? 0x0000FFFFu : 0u) | (tk + 1 < valid ? 0xFFFF0000u : 0u);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        o[r][dt] = mfma16x16x32<DT>(vf, pf[r], o[r][dt]);
+        if constexpr (DT == 1) o[r][dt] = mfma16x16x32<DT>(vf, pl[r], o[r][dt]);
+      }
+    }
+  };
+  // unit u is read from buffer u & 1 while unit u + 1 is loaded into the
+  // other one, which held unit u - 1: every wave finished that before the
+  // barrier ending the previous step.  Every wave takes nunit steps (one
+  // barrier each); a wave past the last query token only fetches.
+  auto step = [&](int u, const u32x4* cur, u32x4* nxt, auto act, auto mask_tag) __attribute__((always_inline)) {
+    if (u + 1 < nunit) fetch(u + 1, nxt);
+    if constexpr (decltype(act)::value) unit(u, cur + lane, mask_tag);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS loads have landed
+    __syncthreads();
+  };
+  // the mask-free units in pairs (fixed buffers, no branch between the
+  // products of consecutive units), then the rest one by one
+  auto run = [&](auto act) __attribute__((always_inline)) {
+    const int npair = min(nfull, nunit) & ~1;
+    int u = 0;
+#pragma unroll 1
+    for (; u < npair; u += 2) {
+      step(u, s_kv0, s_kv1, act, std::false_type{});
+      step(u + 1, s_kv1, s_kv0, act, std::false_type{});
+    }
+#pragma unroll 1
+    for (; u < nunit; ++u) {
+      const u32x4* cur = (u & 1) ? s_kv1 : s_kv0;
+      u32x4* nxt = (u & 1) ? s_kv0 : s_kv1;
+      if (u < nfull) step(u, cur, nxt, act, std::false_type{});
+      else step(u, cur, nxt, act, std::true_type{});
+    }
+  };
+  fetch(0, s_kv0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+  if (active) run(std::true_type{});
+  else run(std::false_type{});
+  if (!active) return;
+  // O^T: lane (column n, group g) holds dims 16 dt + 4 g + i of its column
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float lt = sum_over_groups(l[r]);
+    const int tq = t0 + r * QPS + n / G;
+    if (tq >= L) continue;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    uint16_t* dst = out + q_row(sb, bi, head) + (size_t)tq * kHeadDim + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint32_t lo = (uint32_t)from_f32<DT>(o[r][dt][0] * inv) | ((uint32_t)from_f32<DT>(o[r][dt][1] * inv) << 16);
+      const uint32_t hi = (uint32_t)from_f32<DT>(o[r][dt][2] * inv) | ((uint32_t)from_f32<DT>(o[r][dt][3] * inv) << 16);
+      *(uint2*)(dst + 16 * dt) = make_uint2(lo, hi);
+    }
+  }
+}
+
+template <int DT, int TB>
+static void prefill_dispatch(const Geometry& g, const SeqBatch& b, int L, const uint16_t* q, float sl2,
+                             uint16_t* out, hipStream_t s, Timing* prof) {
+  constexpr int W = 4, R = 2, OCC = 2;
+  const int per_wg = W * R * (16 / g.group);
+  const dim3 grid((L + per_wg - 1) / per_wg, g.hkv, b.n), blk(64 * W);
+  const int kd = kProfPrefill;
+  switch (g.group) {
+    case 1: launch(k_prefill<DT, TB, 1, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 2: launch(k_prefill<DT, TB, 2, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 4: launch(k_prefill<DT, TB, 4, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 8: launch(k_prefill<DT, TB, 8, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    default: launch(k_prefill<DT, TB, 16, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+  }
+}
+
+hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
+                          void* out, hipStream_t s, Timing* prof) {
+  const float sl2 = scale * 1.4426950408889634f;
+  if (g.kv_bits != 0) return launch_prefill_q(g, b, L, q, sl2, out, s, prof);
+  const uint16_t* qq = (const uint16_t*)q;
+  uint16_t* oo = (uint16_t*)out;
+  if (g.dtype == 0) {
+    if (g.tb == 64) prefill_dispatch<0, 64>(g, b, L, qq, sl2, oo, s, prof);
+    else prefill_dispatch<0, 32>(g, b, L, qq, sl2, oo, s, prof);
+  } else {
+    if (g.tb == 64) prefill_dispatch<1, 64>(g, b, L, qq, sl2, oo, s, prof);
+    else prefill_dispatch<1, 32>(g, b, L, qq, sl2, oo, s, prof);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace bsattn
