@@ -247,6 +247,24 @@ def recall_report(cfg: Config, cache, q, idx, seqs):
                     "the group's q heads"}
 
 
+def replay_distribution(run, reps: int, per: int):
+    """p10 / p50 / p90 of `reps` individually event-timed calls of `run`
+    (one step each), in µs per unit of `per` units per step."""
+    import numpy as np
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    for a, b in ev:
+        a.record()
+        run()
+        b.record()
+    torch.cuda.synchronize()
+    us = np.array([a.elapsed_time(b) * 1e3 / per for a, b in ev])
+    p10, p50, p90 = np.percentile(us, [10, 50, 90])
+    return {"p10": round(float(p10), 3), "p50": round(float(p50), 3), "p90": round(float(p90), 3),
+            "reps": reps}
+
+
 def bench_layers(args, cfg: Config):
     import torch
     import bsattn
@@ -295,6 +313,9 @@ def bench_layers(args, cfg: Config):
     ms_per_step = (time.perf_counter() - tg) * 1e3 / args.steps
     us_per_layer = ms_per_step * 1e3 / L
     log(f"[bench] graph: {us_per_layer:.2f} us/layer-step")
+    dist = replay_distribution(graph.replay, max(args.steps, 100), L)
+    log(f"[bench] per-step replays: p10 / p50 / p90 = {dist['p10']} / {dist['p50']} / {dist['p90']} "
+        f"us/layer-step")
 
     if args.copy_calibration:
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
@@ -401,6 +422,7 @@ def bench_layers(args, cfg: Config):
         "decode_kernels_us": decode_kernels,
         "layer_step_GBps": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "eager_us_per_layer_step": round(eager_ms * 1e3 / L, 3),
+        "us_per_layer_step_distribution": dist,
         "cpu_baseline": cpu,
     }
     if recall is not None:
@@ -488,14 +510,22 @@ def bench_loop(args):
         cache.appendStep(kb, vb)
         cache.decode(qb, scale)
     torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(args.warmup, args.warmup + steps):
         kb.copy_(kn[i])
         vb.copy_(vn[i])
         qb.copy_(qs[i])
+        ev[i - args.warmup][0].record()
         graph.replay()
+        ev[i - args.warmup][1].record()
     torch.cuda.synchronize()
     us_graph = (time.perf_counter() - t0) * 1e6 / steps
+    reps = np.array([a.elapsed_time(b) * 1e3 for a, b in ev])
+    p10, p50, p90 = np.percentile(reps, [10, 50, 90])
+    dist = {"p10": round(float(p10), 3), "p50": round(float(p50), 3), "p90": round(float(p90), 3),
+            "reps": steps, "what": "GPU time of one replayed step (input copies excluded)"}
     cache.sync()
     log(f"[bench] c4: {us_graph:.2f} us/step as a replayed HIP graph (inputs copied in per step)")
     nsel = K + 2
@@ -513,6 +543,7 @@ def bench_loop(args):
                    "timing": "eager wall clock per step (ctypes launches included)"},
         "kernels_us_per_step": kern, "kernel_us_per_step_total": round(total, 3),
         "graph_us_per_step": round(us_graph, 3),
+        "graph_step_us_distribution": dist,
         "gather_bytes_per_step": gather,
         "gather_GBps_at_kernel_time": round(gather / (total * 1e-6) / 1e9, 1) if total else None,
     }
@@ -553,6 +584,8 @@ def bench_prefill(args):
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / steps
+    turn = iter(range(1 << 30))
+    dist = replay_distribution(lambda: caches[next(turn) % LAYERS].prefill(q, scale), steps, 1)
     flops = 4.0 * D * B * HQ * sum(T - L + i + 1 for i in range(L))
     tf = flops / (us * 1e-6) / 1e12
     log(f"[bench] prefill chunk {L} at {T} ctx: {us:.1f} us/layer, {tf:.1f} TFLOP/s "
@@ -567,6 +600,7 @@ def bench_prefill(args):
                    "block_size": TB},
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tf / 2500.0, 4), "traffic": None},
+        "us_per_layer_distribution": dist,
     }), flush=True)
 
 
