@@ -23,7 +23,12 @@ Other workloads (one JSON line each, not the headline):
   --config c4  decode loop with appends: B=32, fp16, lengths U[8192, 65536],
                pages of the sequences interleaved in the pool, 256 steps of
                (append one token per sequence, score + top-32 + attend);
-               eager, since every append changes host-side page tables.
+               eager, since every append changes host-side page tables;
+  --config pf  dense causal prefill attention of a 512-token chunk at the end
+               of 32768 tokens (B=8, Hq=32, Hkv=8, bf16), MFMA-bound;
+  --config pfq the same over int4 affine caches (fp16);
+  --config mq  speculative verify at the default geometry: decodeMulti of 4
+               query tokens per sequence, against 4 single-token decodes.
 
 roofline: the gather + attention kernel (k_attend / k_attend_q via
 bsattn_attend on precomputed indices), timed with HIP start/stop events
@@ -100,7 +105,7 @@ def log(msg):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "pf"])
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "pf", "pfq", "mq"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=0, help="layer caches (0: the config's)")
@@ -550,28 +555,30 @@ def bench_loop(args):
     print(json.dumps(result), flush=True)
 
 
-def bench_prefill(args):
+def bench_prefill(args, bits=0):
     """Dense causal prefill attention of a 512-token chunk at the end of a
-    32768-token context (C2 geometry: B=8, Hq=32, Hkv=8, bf16, Tb=64), over
-    4 layer caches (4 GiB, beyond the 256 MB Infinity Cache).  MFMA-bound:
-    algorithmic FLOPs = 4 * D * sum over queries of the tokens they see."""
+    32768-token context (C2 geometry: B=8, Hq=32, Hkv=8, Tb=64; bf16 caches,
+    or with bits = 4 MLX-affine int4 caches, group 64, fp16), over 4 layer
+    caches (beyond the 256 MB Infinity Cache).  MFMA-bound: algorithmic
+    FLOPs = 4 * D * sum over queries of the tokens they see."""
     import torch
     import bsattn
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     B, HQ, HKV, TB, T, L, LAYERS = 8, 32, 8, 64, 32768, 512, 4
+    dt = torch.float16 if bits else torch.bfloat16
     g = torch.Generator(device=dev)
-    g.manual_seed(5005)
+    g.manual_seed(5005 + bits)
     caches = []
     for _ in range(LAYERS):
         c = bsattn.BlockSparseKVCache(max_seqs=B, num_q_heads=HQ, num_kv_heads=HKV, head_dim=D,
-                                      block_size=TB, dtype=torch.bfloat16, top_k=32,
+                                      block_size=TB, dtype=dt, kv_bits=bits, top_k=32,
                                       max_blocks_per_seq=T // TB + 2, device=0)
         for b in range(B):
-            k = torch.randn(1, HKV, T, D, device=dev, generator=g).to(torch.bfloat16)
+            k = torch.randn(1, HKV, T, D, device=dev, generator=g).to(dt)
             c.append(k, k, seq_ids=[b])
         caches.append(c)
-    q = torch.randn(B, HQ, L, D, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, HQ, L, D, device=dev, generator=g).to(dt)
     scale = 1.0 / math.sqrt(D)
     for i in range(args.warmup):
         caches[i % LAYERS].prefill(q, scale)
@@ -588,19 +595,79 @@ def bench_prefill(args):
     dist = replay_distribution(lambda: caches[next(turn) % LAYERS].prefill(q, scale), steps, 1)
     flops = 4.0 * D * B * HQ * sum(T - L + i + 1 for i in range(L))
     tf = flops / (us * 1e-6) / 1e12
-    log(f"[bench] prefill chunk {L} at {T} ctx: {us:.1f} us/layer, {tf:.1f} TFLOP/s "
-        f"({100 * tf / 2500:.1f}% of 2.5 PFLOP/s bf16)")
+    kind = f"int{bits} affine" if bits else "bf16"
+    log(f"[bench] prefill chunk {L} at {T} ctx ({kind} cache): {us:.1f} us/layer, {tf:.1f} TFLOP/s "
+        f"({100 * tf / 2500:.1f}% of 2.5 PFLOP/s dense 16-bit)")
     print(json.dumps({
-        "metric": "dense causal prefill attention µs per layer, 512-token chunk at 32k ctx",
+        "metric": f"dense causal prefill attention µs per layer, 512-token chunk at 32k ctx, {kind} cache",
         "value": round(us, 2), "unit": "us/layer", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(us / 1e3, 4), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic: torch RNG on device, N(0,1)",
+        "vs_baseline": None, "dtype": "f16 (int4 KV)" if bits else "bf16",
+        "data": "synthetic: torch RNG on device, N(0,1)",
         "config": {"workload": "prefill chunk attention x4 distinct layer caches", "batch": B,
                    "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": T, "chunk": L,
-                   "block_size": TB},
+                   "block_size": TB, "kv": kind},
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tf / 2500.0, 4), "traffic": None},
         "us_per_layer_distribution": dist,
+    }), flush=True)
+
+
+def bench_multi(args, cfg: Config, L: int = 4):
+    """Speculative verify at the C2 geometry: decodeMulti of L query tokens per
+    sequence (each selects its own blocks over its own prefix), over the
+    config's distinct layer caches, as a replayed HIP graph; against L
+    single-token decodes of the same layer caches."""
+    import torch
+    import bsattn
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    NL = args.layers or cfg.layers
+    layers = [make_layer(cfg, i, dev, torch, bsattn) for i in range(NL)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(7007)
+    qm = torch.randn(cfg.B, cfg.HQ, L, D, device=dev, generator=g).to(torch_dtype(torch, cfg))
+    scale = 1.0 / math.sqrt(D)
+
+    def timed(step):
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e6 / args.steps / NL, replay_distribution(
+            graph.replay, max(args.steps, 50), NL)
+
+    multi_us, dist = timed(lambda: [c.decodeMulti(qm, scale) for c, _ in layers])
+    qs = [qm[:, :, i:i + 1].contiguous() for i in range(L)]
+    single_us, _ = timed(lambda: [c.decode(qq, scale) for c, _ in layers for qq in qs])
+    log(f"[bench] mq: {L} query tokens per sequence: {multi_us:.2f} us/layer-step "
+        f"(L single decodes: {single_us:.2f})")
+    print(json.dumps({
+        "metric": f"block-sparse multi-token decode (speculative verify, L={L}) µs per layer-step",
+        "value": round(multi_us, 3), "unit": "us/layer-step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(multi_us * NL / 1e3, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": cfg.dtype,
+        "data": "synthetic: torch RNG on device, K/V ~ N(0,1), random-init q",
+        "config": {"workload": f"decodeMulti x{NL} distinct layer caches", "batch": cfg.B,
+                   "q_heads": cfg.HQ, "kv_heads": cfg.HKV, "head_dim": D, "context": cfg.T,
+                   "block_size": cfg.TB, "top_k": cfg.top_k, "query_tokens": L},
+        "single_decodes_us_per_layer_step": round(single_us, 3),
+        "us_per_layer_step_distribution": dist,
     }), flush=True)
 
 
@@ -615,6 +682,10 @@ def main():
         bench_loop(args)
     elif args.config == "pf":
         bench_prefill(args)
+    elif args.config == "pfq":
+        bench_prefill(args, bits=4)
+    elif args.config == "mq":
+        bench_multi(args, CONFIGS["c2"])
     else:
         bench_layers(args, CONFIGS[args.config])
 
