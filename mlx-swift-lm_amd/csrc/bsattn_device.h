@@ -503,6 +503,31 @@ __host__ __device__ inline int sb_entry(int tb, int tok) {
   return ((tok >> 3) & 3) * (tb >> 2) + 8 * (tok >> 5) + (tok & 7);
 }
 
+// int4 word (element e in nibble q_nib(e)) -> 8 fp16 values 1 + c/16, in
+// element order: pair k = elements 2k, 2k+1 = nibbles k, k+4
+__device__ __forceinline__ u32x4 nib_to_f16(uint32_t w) {
+  constexpr uint32_t M = 0x03C003C0u, ONE = 0x3C003C00u;
+  return u32x4{((w << 6) & M) | ONE, ((w << 2) & M) | ONE, ((w >> 2) & M) | ONE,
+               ((w >> 6) & M) | ONE};
+}
+
+// two int8 words (element e in byte e) -> 8 fp16 values 1024 + c: each
+// byte becomes the low byte of an fp16 whose high byte is 0x64
+__device__ __forceinline__ u32x4 byte_to_f16(uint32_t lo, uint32_t hi) {
+  constexpr uint32_t H = 0x64646464u;
+  return u32x4{__builtin_amdgcn_perm(H, lo, 0x04010400u), __builtin_amdgcn_perm(H, lo, 0x04030402u),
+               __builtin_amdgcn_perm(H, hi, 0x04010400u), __builtin_amdgcn_perm(H, hi, 0x04030402u)};
+}
+
+template <int KB>
+struct QCode {
+  static constexpr float OFF = KB == 4 ? 1.0f : 1024.0f;  // value of code 0
+  static constexpr float INV_UNIT = KB == 4 ? 16.0f : 1.0f;  // 1 / value step
+  static constexpr int KF = KB / 4;                          // K fragments per token tile
+  static constexpr int DPF = 16 / KB;                        // dim tiles per V fragment
+  static constexpr int WPR = kHeadDim * KB / 32;             // MLX words per token row
+};
+
 // ---------------------------------------------------------------------------
 // attention workgroup plumbing shared by the 16-bit and quantized kernels.
 // A workgroup is W waves = W consecutive selected slots of one (sequence,

@@ -137,8 +137,6 @@ hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, fl
 // dense causal attention of the last L tokens of each sequence
 hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
                           void* out, hipStream_t s, Timing* prof);
-hipError_t launch_prefill_q(const Geometry& g, const SeqBatch& b, int L, const void* q, float sl2,
-                            void* out, hipStream_t s, Timing* prof);
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out,
                          void* v_out, hipStream_t s);
 hipError_t launch_export_quantized(const Geometry& g, const SeqBatch& b, int T,

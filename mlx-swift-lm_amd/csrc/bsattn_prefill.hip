@@ -40,13 +40,20 @@ namespace bsattn {
 // fetches 16 / W fragments): the loads of unit u + 1 are in flight while the
 // workgroup computes unit u from the other buffer.  A wave reads each
 // fragment from LDS once and applies it to all R column sets.
+// Affine-quantized caches (KB = 4 / 8 bits, fp16 q / out): a unit's codes
+// and scales / biases are loaded raw into LDS (4.5 / 8.5 KiB) and
+// dequantized once per workgroup into the 16-bit fragment layout above, as
+// fp16 values fl16(scale * code + bias) (one packed fused multiply-add per
+// pair, so each is the correctly rounded dequantized value); the rest runs
+// as for an fp16 cache.  The raw loads run two units ahead: in step u the
+// workgroup loads unit u + 2, dequantizes unit u + 1 and computes unit u.
 // The workgroups of one (sequence, kv head) read the same blocks, so the
 // flat workgroup index is remapped to give them consecutive indices within
 // one XCD (workgroups are dealt to the 8 XCDs in turn): they then share that
 // XCD's L2 instead of fetching every block into all eight.
 // grid (ceil(L / (W * R * 16 / G)), Hkv, n)
 // ---------------------------------------------------------------------------
-template <int DT, int TB, int G, int R, int W, int OCC>
+template <int DT, int TB, int G, int R, int W, int OCC, int KB>
 __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch sb, int L,
                                                    const uint16_t* __restrict__ q, float sl2,
                                                    uint16_t* __restrict__ out) {
@@ -54,12 +61,17 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
   constexpr int KS2 = TB / 32;  // 32-token units (PV k-steps) of a block
   constexpr int FPW = 16 / W;   // fragments of a unit each wave fetches
   static_assert(16 % W == 0 && (W == 1 || 8 % W == 0), "fragments split evenly over the waves");
+  static_assert(KB == 0 || (DT == 0 && W == 4), "quantized caches: fp16, four waves");
+  // raw quantized unit: K code fragments (2 tiles x KB / 4), V code fragments
+  // (8 dim tiles / (16 / KB) per fragment), then 32 scale / bias entries
+  constexpr int RKF = KB / 2, RVF = KB / 2, RAWF = RKF + RVF;
   // the running maximum a column's weights are taken against is raised only
   // when a block's maximum exceeds it by more than 2^kLazy: the weights then
   // stay below 2^kLazy, and the rescaling of O^T (a pass over its registers)
   // is skipped for most blocks; O^T / l is unchanged by the choice
   constexpr float kLazy = 8.f;
   __shared__ __align__(16) u32x4 s_kv0[16 * 64], s_kv1[16 * 64];
+  __shared__ __align__(16) u32x4 s_raw0[KB ? RAWF * 64 + 32 : 1], s_raw1[KB ? RAWF * 64 + 32 : 1];
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   // XCD-grouped workgroup order (a bijection on [0, total))
@@ -117,6 +129,94 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
       __builtin_amdgcn_global_load_lds(
           (const void*)(i < 8 / W ? Kf + i * W * 64 : Vf + (i - 8 / W) * W * KS2 * 64),
           (__attribute__((address_space(3))) void*)(buf + (wave + i * W) * 64), 16, 0, 0);
+  };
+  // raw quantized unit u: slots f = wave + i * W; K fragment hh * RKF + f of
+  // the block for f < RKF (QK tiles 2 hh, 2 hh + 1), V fragment
+  // (f - RKF) * KS2 + hh for f >= RKF; the unit's scale / bias entries for
+  // tokens 8 g' + e (g' = 0..3, e = 0..7) go to entries 8 g' + e, loaded by
+  // lanes 0..31 of the last wave
+  auto fetch_raw = [&](int u, u32x4* buf) __attribute__((always_inline)) {
+    const int page = uniform(bt[u / KS2]), hh = u % KS2;
+    const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
+    const u32x4* Kf = (const u32x4*)(slab + geo.k_off) + lane;
+    const u32x4* Vf = (const u32x4*)(slab + geo.v_off) + lane;
+#pragma unroll
+    for (int i = 0; i < RAWF / W; ++i) {
+      const int f = wave + i * W;
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(f < RKF ? Kf + (hh * RKF + f) * 64 : Vf + ((f - RKF) * KS2 + hh) * 64),
+          (__attribute__((address_space(3))) void*)(buf + f * 64), 16, 0, 0);
+    }
+    if (wave == W - 1 && lane < 32) {
+      const u32x4* Sf = (const u32x4*)(slab + geo.sb_off) + (lane >> 3) * (TB / 4) + 8 * hh + (lane & 7);
+      __builtin_amdgcn_global_load_lds((const void*)Sf,
+                                       (__attribute__((address_space(3))) void*)(buf + RAWF * 64), 16, 0, 0);
+    }
+  };
+  // dequantize a raw unit into the fp16 fragment layout: wave 0 / 1 writes
+  // the 4 K fragments of QK tile 0 / 1 (one token per lane), wave 2 / 3 the
+  // V fragments of dim tiles 0..3 / 4..7 (8 tokens per lane)
+  auto dequant = [&](const u32x4* raw, u32x4* kv) __attribute__((always_inline)) {
+    using QC = QCode<KB>;
+    const u32x4* ent = raw + RAWF * 64;  // scale / bias entry of token x of the unit
+    // f16 pairs (s * c + b): c from the f16 values OFF + c / INV_UNIT exactly
+    auto deq = [&](u32x4 hv, const uint32_t* sp, const uint32_t* bp) __attribute__((always_inline)) {
+      const f16x2 unit2 = {(_Float16)QC::INV_UNIT, (_Float16)QC::INV_UNIT};
+      const f16x2 off2 = {(_Float16)(-QC::OFF * QC::INV_UNIT), (_Float16)(-QC::OFF * QC::INV_UNIT)};
+      u32x4 r;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        // (a vector element is copied out first: __builtin_bit_cast of
+        // hv[k] itself reads element 0 with this compiler)
+        const uint32_t w = hv[k];
+        const f16x2 c = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, w), unit2, off2);
+        r[k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, sp[k]), c,
+                                                                       __builtin_bit_cast(f16x2, bp[k])));
+      }
+      return r;
+    };
+    if (wave < 2) {
+      // row m of QK tile t is token 8 (m / 4) + 4 t + m % 4 of the unit (the
+      // tile's MFMA output rows then land on tok_of(g, 4 t + i))
+      const int t = wave, m = lane & 15;
+      const u32x4 e = ent[8 * (m >> 2) + 4 * t + (m & 3)];
+      // (k scale, k bias) of dim group 0 / 1 in both halves
+      const uint32_t s0 = __builtin_amdgcn_perm(e[0], e[0], 0x01000100u), s1 = __builtin_amdgcn_perm(e[0], e[0], 0x03020302u);
+      const uint32_t b0 = __builtin_amdgcn_perm(e[1], e[1], 0x01000100u), b1 = __builtin_amdgcn_perm(e[1], e[1], 0x03020302u);
+      u32x4 rw[2];
+#pragma unroll
+      for (int f = 0; f < RKF / 2; ++f) rw[f] = raw[(t * (RKF / 2) + f) * 64 + lane];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        u32x4 hv;
+        if constexpr (KB == 4) hv = nib_to_f16(rw[0][s]);
+        else hv = byte_to_f16(rw[s >> 1][2 * (s & 1)], rw[s >> 1][2 * (s & 1) + 1]);
+        const uint32_t sp[4] = {s < 2 ? s0 : s1, s < 2 ? s0 : s1, s < 2 ? s0 : s1, s < 2 ? s0 : s1};
+        const uint32_t bp[4] = {s < 2 ? b0 : b1, s < 2 ? b0 : b1, s < 2 ? b0 : b1, s < 2 ? b0 : b1};
+        kv[(t * 4 + s) * 64 + lane] = deq(hv, sp, bp);
+      }
+    } else {
+      const int half = wave - 2;  // dim group of dim tiles 4 half .. 4 half + 3
+      // (v scale, v bias) of tokens 8 g + 2 k, 8 g + 2 k + 1 as f16 pairs
+      uint32_t sp[4], bp[4];
+      const uint32_t sel = half ? 0x07060302u : 0x05040100u;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const u32x4 e0 = ent[8 * g + 2 * k], e1 = ent[8 * g + 2 * k + 1];
+        sp[k] = __builtin_amdgcn_perm(e1[2], e0[2], sel);
+        bp[k] = __builtin_amdgcn_perm(e1[3], e0[3], sel);
+      }
+      u32x4 rw[2];
+#pragma unroll
+      for (int f = 0; f < RVF / 2; ++f) rw[f] = raw[(RKF + half * (RVF / 2) + f) * 64 + lane];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        u32x4 hv;
+        if constexpr (KB == 4) hv = nib_to_f16(rw[0][d]);
+        else hv = byte_to_f16(rw[d >> 1][2 * (d & 1)], rw[d >> 1][2 * (d & 1) + 1]);
+        kv[(8 + 4 * half + d) * 64 + lane] = deq(hv, sp, bp);
+      }
+    }
   };
   float m[R], l[R], thr[R];
   f32x4 o[R][8];
@@ -213,12 +313,22 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
       }
     }
   };
-  // unit u is read from buffer u & 1 while unit u + 1 is loaded into the
-  // other one, which held unit u - 1: every wave finished that before the
-  // barrier ending the previous step.  Every wave takes nunit steps (one
-  // barrier each); a wave past the last query token only fetches.
-  auto step = [&](int u, const u32x4* cur, u32x4* nxt, auto act, auto mask_tag) __attribute__((always_inline)) {
-    if (u + 1 < nunit) fetch(u + 1, nxt);
+  // 16-bit: unit u is read from buffer u & 1 while unit u + 1 is loaded
+  // into the other one, which held unit u - 1: every wave finished that
+  // before the barrier ending the previous step.  Quantized: raw buffer
+  // u & 1 (unit u, dequantized in the previous step) takes the loads of unit
+  // u + 2 while raw buffer (u + 1) & 1 is dequantized into fp16 buffer
+  // (u + 1) & 1 (which held unit u - 1).  Every wave takes nunit steps (one
+  // barrier each); a wave past the last query token only loads (and
+  // dequantizes).
+  auto step = [&](int u, const u32x4* cur, u32x4* nxt, u32x4* raw_ld, const u32x4* raw_dq, auto act,
+                  auto mask_tag) __attribute__((always_inline)) {
+    if constexpr (KB == 0) {
+      if (u + 1 < nunit) fetch(u + 1, nxt);
+    } else {
+      if (u + 2 < nunit) fetch_raw(u + 2, raw_ld);
+      if (u + 1 < nunit) dequant(raw_dq, nxt);
+    }
     if constexpr (decltype(act)::value) unit(u, cur + lane, mask_tag);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS loads have landed
     __syncthreads();
@@ -230,20 +340,32 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
     int u = 0;
 #pragma unroll 1
     for (; u < npair; u += 2) {
-      step(u, s_kv0, s_kv1, act, std::false_type{});
-      step(u + 1, s_kv1, s_kv0, act, std::false_type{});
+      step(u, s_kv0, s_kv1, s_raw0, s_raw1, act, std::false_type{});
+      step(u + 1, s_kv1, s_kv0, s_raw1, s_raw0, act, std::false_type{});
     }
 #pragma unroll 1
     for (; u < nunit; ++u) {
-      const u32x4* cur = (u & 1) ? s_kv1 : s_kv0;
-      u32x4* nxt = (u & 1) ? s_kv0 : s_kv1;
-      if (u < nfull) step(u, cur, nxt, act, std::false_type{});
-      else step(u, cur, nxt, act, std::true_type{});
+      const bool odd = u & 1;
+      const u32x4* cur = odd ? s_kv1 : s_kv0;
+      u32x4* nxt = odd ? s_kv0 : s_kv1;
+      u32x4* raw_ld = odd ? s_raw1 : s_raw0;
+      const u32x4* raw_dq = odd ? s_raw0 : s_raw1;
+      if (u < nfull) step(u, cur, nxt, raw_ld, raw_dq, act, std::false_type{});
+      else step(u, cur, nxt, raw_ld, raw_dq, act, std::true_type{});
     }
   };
-  fetch(0, s_kv0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  __syncthreads();
+  if constexpr (KB == 0) {
+    fetch(0, s_kv0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+  } else {
+    fetch_raw(0, s_raw0);
+    if (nunit > 1) fetch_raw(1, s_raw1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    dequant(s_raw0, s_kv0);
+    __syncthreads();
+  }
   if (active) run(std::true_type{});
   else run(std::false_type{});
   if (!active) return;
@@ -264,7 +386,7 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
   }
 }
 
-template <int DT, int TB>
+template <int DT, int TB, int KB>
 static void prefill_dispatch(const Geometry& g, const SeqBatch& b, int L, const uint16_t* q, float sl2,
                              uint16_t* out, hipStream_t s, Timing* prof) {
   constexpr int W = 4, R = 2, OCC = 2;
@@ -272,26 +394,31 @@ static void prefill_dispatch(const Geometry& g, const SeqBatch& b, int L, const 
   const dim3 grid((L + per_wg - 1) / per_wg, g.hkv, b.n), blk(64 * W);
   const int kd = kProfPrefill;
   switch (g.group) {
-    case 1: launch(k_prefill<DT, TB, 1, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
-    case 2: launch(k_prefill<DT, TB, 2, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
-    case 4: launch(k_prefill<DT, TB, 4, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
-    case 8: launch(k_prefill<DT, TB, 8, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
-    default: launch(k_prefill<DT, TB, 16, R, W, OCC>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 1: launch(k_prefill<DT, TB, 1, R, W, OCC, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 2: launch(k_prefill<DT, TB, 2, R, W, OCC, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 4: launch(k_prefill<DT, TB, 4, R, W, OCC, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    case 8: launch(k_prefill<DT, TB, 8, R, W, OCC, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
+    default: launch(k_prefill<DT, TB, 16, R, W, OCC, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
   }
 }
 
 hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
                           void* out, hipStream_t s, Timing* prof) {
   const float sl2 = scale * 1.4426950408889634f;
-  if (g.kv_bits != 0) return launch_prefill_q(g, b, L, q, sl2, out, s, prof);
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* oo = (uint16_t*)out;
-  if (g.dtype == 0) {
-    if (g.tb == 64) prefill_dispatch<0, 64>(g, b, L, qq, sl2, oo, s, prof);
-    else prefill_dispatch<0, 32>(g, b, L, qq, sl2, oo, s, prof);
+  if (g.kv_bits == 4) {
+    if (g.tb == 64) prefill_dispatch<0, 64, 4>(g, b, L, qq, sl2, oo, s, prof);
+    else prefill_dispatch<0, 32, 4>(g, b, L, qq, sl2, oo, s, prof);
+  } else if (g.kv_bits == 8) {
+    if (g.tb == 64) prefill_dispatch<0, 64, 8>(g, b, L, qq, sl2, oo, s, prof);
+    else prefill_dispatch<0, 32, 8>(g, b, L, qq, sl2, oo, s, prof);
+  } else if (g.dtype == 0) {
+    if (g.tb == 64) prefill_dispatch<0, 64, 0>(g, b, L, qq, sl2, oo, s, prof);
+    else prefill_dispatch<0, 32, 0>(g, b, L, qq, sl2, oo, s, prof);
   } else {
-    if (g.tb == 64) prefill_dispatch<1, 64>(g, b, L, qq, sl2, oo, s, prof);
-    else prefill_dispatch<1, 32>(g, b, L, qq, sl2, oo, s, prof);
+    if (g.tb == 64) prefill_dispatch<1, 64, 0>(g, b, L, qq, sl2, oo, s, prof);
+    else prefill_dispatch<1, 32, 0>(g, b, L, qq, sl2, oo, s, prof);
   }
   return hipGetLastError();
 }

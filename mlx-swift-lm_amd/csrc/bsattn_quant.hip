@@ -36,31 +36,6 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 __device__ __forceinline__ float lo_f(uint32_t w) { return h2f(w & 0xFFFFu); }
 __device__ __forceinline__ float hi_f(uint32_t w) { return h2f(w >> 16); }
 
-// int4 word (element e in nibble q_nib(e)) -> 8 fp16 values 1 + c/16, in
-// element order: pair k = elements 2k, 2k+1 = nibbles k, k+4
-__device__ __forceinline__ u32x4 nib_to_f16(uint32_t w) {
-  constexpr uint32_t M = 0x03C003C0u, ONE = 0x3C003C00u;
-  return u32x4{((w << 6) & M) | ONE, ((w << 2) & M) | ONE, ((w >> 2) & M) | ONE,
-               ((w >> 6) & M) | ONE};
-}
-
-// two int8 words (element e in byte e) -> 8 fp16 values 1024 + c: each
-// byte becomes the low byte of an fp16 whose high byte is 0x64
-__device__ __forceinline__ u32x4 byte_to_f16(uint32_t lo, uint32_t hi) {
-  constexpr uint32_t H = 0x64646464u;
-  return u32x4{__builtin_amdgcn_perm(H, lo, 0x04010400u), __builtin_amdgcn_perm(H, lo, 0x04030402u),
-               __builtin_amdgcn_perm(H, hi, 0x04010400u), __builtin_amdgcn_perm(H, hi, 0x04030402u)};
-}
-
-template <int KB>
-struct QCode {
-  static constexpr float OFF = KB == 4 ? 1.0f : 1024.0f;  // value of code 0
-  static constexpr float INV_UNIT = KB == 4 ? 16.0f : 1.0f;  // 1 / value step
-  static constexpr int KF = KB / 4;                          // K fragments per token tile
-  static constexpr int DPF = 16 / KB;                        // dim tiles per V fragment
-  static constexpr int WPR = kHeadDim * KB / 32;             // MLX words per token row
-};
-
 // A operand of QK token tile t, k-step s, from the tile's K fragments
 template <int KB>
 __device__ __forceinline__ u32x4 k_operand(const u32x4* kf, int s) {
@@ -574,227 +549,6 @@ hipError_t launch_attend_q(const Geometry& g, const SeqBatch& b, const void* q, 
   else attend_q_sel<false>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
   return hipGetLastError();
 }
-
-// ---------------------------------------------------------------------------
-// dense causal prefill attention over quantized blocks: the 16-bit
-// k_prefill's structure (columns = (query token, q head) pairs, O^T =
-// V^T . P^T so each lane owns its column's softmax state) with the
-// dequantisation folded into the MFMAs as in the decode kernel.  The raw
-// code product, sum_t P_g and sum_t p v_bias_g accumulate across blocks
-// (each rescaled with the running maximum) and the affine correction is
-// applied once at the end.  q / out are fp16.
-// grid (ceil(L / (W * R * 16 / G)), Hkv, n)
-// ---------------------------------------------------------------------------
-template <int TB, int G, int R, int W, int KB>
-__global__ __launch_bounds__(64 * W, 1) void k_prefill_q(Geometry geo, SeqBatch sb, int L,
-                                                     const uint16_t* __restrict__ q, float sl2,
-                                                     uint16_t* __restrict__ out) {
-  using QC = QCode<KB>;
-  constexpr int QPS = 16 / G;   // query tokens per column set
-  constexpr int NT = TB / 16;   // QK token tiles
-  constexpr int EPL = TB / 4;   // scores per lane
-  constexpr int KS2 = TB / 32;  // PV k-steps
-  constexpr int KF = QC::KF;
-  constexpr int NVF = (8 / QC::DPF) * KS2;  // V fragments
-  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int n = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y, bi = blockIdx.z;
-  const int t0 = (blockIdx.x * W + wave) * R * QPS;
-  if (t0 >= L) return;
-  const int seq = sb.ids[bi];
-  const int T = uniform(geo.meta[seq]);
-  const int head = h * G + n % G;
-  const u32x4 ones = u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
-  int pos[R];
-  u32x4 qf[R][4];
-  float q0[R], q1[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int tq = t0 + r * QPS + n / G;
-    pos[r] = tq < L ? T - L + tq : -1;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qf[r][s] = u32x4{0u, 0u, 0u, 0u};
-    if (tq < L) {
-      const uint16_t* src = q + q_row(sb, bi, head) + (size_t)tq * kHeadDim + 8 * g;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qf[r][s] = *(const u32x4*)(src + 32 * s);
-    }
-    // Q_g = sum of the column's q over dim group g (every accumulator entry)
-    f32x4 a0 = mfma_f16(ones, qf[r][0], f32x4{0.f, 0.f, 0.f, 0.f});
-    a0 = mfma_f16(ones, qf[r][1], a0);
-    f32x4 a1 = mfma_f16(ones, qf[r][2], f32x4{0.f, 0.f, 0.f, 0.f});
-    a1 = mfma_f16(ones, qf[r][3], a1);
-    q0[r] = a0[0];
-    q1[r] = a1[0];
-  }
-  const int last = T - L + min(L - 1, t0 + R * QPS - 1);
-  const int nblk = last / TB + 1;
-  const int32_t* bt = block_table(geo, seq);
-  float m[R], l[R];
-  f32x4 raw[R][8], ps[R][2], vb[R][2];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    m[r] = -INFINITY;
-    l[r] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) raw[r][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int x = 0; x < 2; ++x) ps[r][x] = vb[r][x] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-#pragma unroll 1
-  for (int j = 0; j < nblk; ++j) {
-    const int page = uniform(bt[j]);
-    const int valid = min(TB, T - j * TB);
-    const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
-    const u32x4* Kf = (const u32x4*)(slab + geo.k_off) + lane;
-    const u32x4* Vf = (const u32x4*)(slab + geo.v_off) + lane;
-    const u32x4* Sf = (const u32x4*)(slab + geo.sb_off) + g * EPL;
-    u32x4 kf[NT][KF];
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int f = 0; f < KF; ++f) kf[t][f] = Kf[(t * KF + f) * 64];
-    u32x4 vf[NVF];
-#pragma unroll
-    for (int i = 0; i < NVF; ++i) vf[i] = Vf[i * 64];
-    u32x4 sbv[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) sbv[e] = Sf[e];
-    __builtin_amdgcn_sched_barrier(0);
-    // no stale scale / bias of tokens past the sequence end reaches PV
-    if (valid < TB) {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e)
-        if (tok_of(g, e) >= valid) sbv[e] = u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float q0c = q0[r] * (QC::OFF * QC::INV_UNIT), q1c = q1[r] * (QC::OFF * QC::INV_UNIT);
-      const int lim = pos[r] - j * TB;
-      float pv[EPL];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        f32x4 r0 = f32x4{0.f, 0.f, 0.f, 0.f}, r1 = r0;
-        r0 = mfma_f16(k_operand<KB>(kf[t], 0), qf[r][0], r0);
-        r0 = mfma_f16(k_operand<KB>(kf[t], 1), qf[r][1], r0);
-        r1 = mfma_f16(k_operand<KB>(kf[t], 2), qf[r][2], r1);
-        r1 = mfma_f16(k_operand<KB>(kf[t], 3), qf[r][3], r1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int e = 4 * t + i;
-          const u32x4& f = sbv[e];
-          const float d0 = __builtin_fmaf(r0[i], QC::INV_UNIT, -q0c);
-          const float d1 = __builtin_fmaf(r1[i], QC::INV_UNIT, -q1c);
-          float sc = lo_f(f[0]) * d0;
-          sc = __builtin_fmaf(lo_f(f[1]), q0[r], sc);
-          sc = __builtin_fmaf(hi_f(f[0]), d1, sc);
-          sc = __builtin_fmaf(hi_f(f[1]), q1[r], sc);
-          pv[e] = tok_of(g, e) <= lim ? sc * sl2 : -INFINITY;
-        }
-      }
-      float bm = pv[0];
-#pragma unroll
-      for (int e = 1; e < EPL; ++e) bm = fmaxf(bm, pv[e]);
-      bm = max_over_groups(bm);
-      const float mn = fmaxf(m[r], bm);
-      const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[r] - mn);
-      float psum = 0.f;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        pv[e] = mn == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pv[e] - mn);
-        psum += pv[e];
-      }
-      psum = sum_over_groups(psum);
-      l[r] = l[r] * alpha + psum;
-      m[r] = mn;
-      // B operands: P_g = p * v_scale_g and p * v_bias_g per dim group
-      u32x4 pa0[KS2], pa1[KS2], pb0[KS2], pb1[KS2];
-#pragma unroll
-      for (int s2 = 0; s2 < KS2; ++s2)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int e0 = 8 * s2 + 2 * jj, e1 = e0 + 1;
-          const float p0 = pv[e0], p1 = pv[e1];
-          const u32x4 &f0 = sbv[e0], &f1 = sbv[e1];
-          pa0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[2]), p1 * lo_f(f1[2]));
-          pa1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[2]), p1 * hi_f(f1[2]));
-          pb0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[3]), p1 * lo_f(f1[3]));
-          pb1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[3]), p1 * hi_f(f1[3]));
-        }
-#pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          ps[r][x][i] *= alpha;
-          vb[r][x][i] *= alpha;
-        }
-#pragma unroll
-      for (int s2 = 0; s2 < KS2; ++s2) {
-        ps[r][0] = mfma_f16(ones, pa0[s2], ps[r][0]);
-        ps[r][1] = mfma_f16(ones, pa1[s2], ps[r][1]);
-        vb[r][0] = mfma_f16(ones, pb0[s2], vb[r][0]);
-        vb[r][1] = mfma_f16(ones, pb1[s2], vb[r][1]);
-      }
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        f32x4 a = raw[r][dt];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] *= alpha;
-#pragma unroll
-        for (int s2 = 0; s2 < KS2; ++s2) a = mfma_f16(v_operand<KB, KS2>(vf, dt, s2), dt < 4 ? pa0[s2] : pa1[s2], a);
-        raw[r][dt] = a;
-      }
-    }
-  }
-  // O^T: lane (column n, group g) holds dims 16 dt + 4 g + i of its column
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if (pos[r] < 0) continue;
-    const int tq = t0 + r * QPS + n / G;
-    const float inv = l[r] > 0.f ? 1.f / l[r] : 0.f;
-    uint16_t* dst = out + q_row(sb, bi, head) + (size_t)tq * kHeadDim + 4 * g;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const f32x4& pg = dt < 4 ? ps[r][0] : ps[r][1];
-      const f32x4& vg = dt < 4 ? vb[r][0] : vb[r][1];
-      float o[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(raw[r][dt][i] - QC::OFF * pg[i], QC::INV_UNIT, vg[i]) * inv;
-      *(uint2*)(dst + 16 * dt) = make_uint2(pack2<0>(o[0], o[1]), pack2<0>(o[2], o[3]));
-    }
-  }
-}
-
-template <int TB, int KB>
-static void prefill_q_dispatch(const Geometry& g, const SeqBatch& b, int L, const uint16_t* q, float sl2,
-                               uint16_t* out, hipStream_t s, Timing* prof) {
-  constexpr int W = 4, R = 2;
-  const int per_wg = W * R * (16 / g.group);
-  const dim3 grid((L + per_wg - 1) / per_wg, g.hkv, b.n), blk(64 * W);
-  const int kd = kProfPrefill;
-  switch (g.group) {
-    case 1: launch(k_prefill_q<TB, 1, R, W, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
-    case 2: launch(k_prefill_q<TB, 2, R, W, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
-    case 4: launch(k_prefill_q<TB, 4, R, W, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
-    case 8: launch(k_prefill_q<TB, 8, R, W, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
-    default: launch(k_prefill_q<TB, 16, R, W, KB>, grid, blk, 0, s, prof, kd, g, b, L, q, sl2, out); break;
-  }
-}
-
-hipError_t launch_prefill_q(const Geometry& g, const SeqBatch& b, int L, const void* q, float sl2,
-                            void* out, hipStream_t s, Timing* prof) {
-  const uint16_t* qq = (const uint16_t*)q;
-  uint16_t* oo = (uint16_t*)out;
-  if (g.kv_bits == 4) {
-    if (g.tb == 64) prefill_q_dispatch<64, 4>(g, b, L, qq, sl2, oo, s, prof);
-    else prefill_q_dispatch<32, 4>(g, b, L, qq, sl2, oo, s, prof);
-  } else {
-    if (g.tb == 64) prefill_q_dispatch<64, 8>(g, b, L, qq, sl2, oo, s, prof);
-    else prefill_q_dispatch<32, 8>(g, b, L, qq, sl2, oo, s, prof);
-  }
-  return hipGetLastError();
-}
-
 
 hipError_t launch_export_quantized(const Geometry& g, const SeqBatch& b, int T, uint32_t* kw,
                                    void* ks, void* kb, uint32_t* vw, void* vs, void* vb,
