@@ -146,6 +146,41 @@ def test_decode_loop_with_appends(gpu):
     log(f"[decode-loop] worst err={worst:.3g}")
 
 
+def test_config4_decode_loop_full(gpu):
+    """B=32 sequences of U[8192, 65536] tokens (stream 4), their pages
+    interleaved in the pool, Hq=32, Hkv=8, fp16, top-32 + sink + recent; 256
+    decode steps, each appending one token per sequence: selected blocks and
+    outputs against the oracle after steps 1, 128 and 256 (every head), block
+    summaries after the last."""
+    import torch
+    seed, steps, Tb = 1004, 256, 64
+    lens0 = [O.uniform_int(seed, 4, b, 8192, 65536) for b in range(32)]
+    total = [l + steps for l in lens0]
+    log("[config4] generating")
+    w = make_workload(seed, B=32, Hq=32, Hkv=8, T=max(total), Tb=Tb, dtype="f16", top_k=32, lens=total)
+
+    def view(cur):
+        ws = Workload(w.seed, w.B, w.Hq, w.Hkv, w.D, Tb, "f16", list(cur), w.top_k, w.ns, w.nr)
+        ws.q = w.q
+        ws.keys = [w.keys[b][:, :cur[b]] for b in range(w.B)]
+        ws.values = [w.values[b][:, :cur[b]] for b in range(w.B)]
+        return ws
+
+    cache = new_cache(w)
+    fill(cache, view(lens0), gpu, chunk=4096)
+    worst = 0.0
+    for s in range(steps):
+        cur = [l + s + 1 for l in lens0]
+        k = np.stack([w.keys[b][:, cur[b] - 1:cur[b]] for b in range(w.B)])
+        v = np.stack([w.values[b][:, cur[b] - 1:cur[b]] for b in range(w.B)])
+        cache.append(to_dev(k, "f16", gpu), to_dev(v, "f16", gpu))
+        if s + 1 in (1, 128, steps):
+            log(f"[config4] step {s + 1}")
+            worst = max(worst, run_and_check(cache, view(cur), gpu, check_summaries=(s + 1 == steps)))
+    torch.cuda.synchronize()
+    log(f"[config4] worst err={worst:.3g}")
+
+
 def test_cache_contract_export_copy_trim(gpu):
     """Structural contract of the reference's KVCacheTests
     (Tests/MLXLMTests/KVCacheTests.swift:15-180): state round trip, copy()

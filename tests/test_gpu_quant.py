@@ -203,6 +203,21 @@ def test_config3_int4_full(gpu):
     log(f"[config3] err={err:.3g}")
 
 
+def test_config5_int8_wide_group_full(gpu):
+    """B=8, Hq=64, Hkv=4 (GQA 16), 262144 tokens in 32-token blocks (8192
+    blocks per head), int8 group 64, top-128 + sink + 4 recent: every head
+    against the oracle (the MFMA-band scoring and the workgroup selection at
+    full size)."""
+    log("[config5] generating")
+    w = make_workload(1005, B=8, Hq=64, Hkv=4, T=262144, Tb=32, dtype="f16", top_k=128, nr=4)
+    cache = new_cache(w, kv_bits=8)
+    fill(cache, w, gpu)
+    log("[config5] oracle")
+    kq, vq = quantize_all(w, 8)
+    err = run_and_check_q(cache, w, gpu, 8, kq, vq)
+    log(f"[config5] err={err:.3g}")
+
+
 def test_quantized_decode_loop_with_appends(gpu):
     """Decode steps that append one token per sequence (crossing block
     boundaries, so summaries refresh) on an int4 cache."""
