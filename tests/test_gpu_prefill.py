@@ -112,6 +112,7 @@ def test_prefill_argument_errors(gpu):
     (4, 32, 8, 64, [2000, 1300], 90),
     (8, 64, 4, 32, [1500, 800], 50),     # G = 16
     (8, 16, 8, 64, [700, 900], 33),      # G = 2
+    (4, 32, 8, 32, [310, 97], 70),       # int4 in 32-token blocks; idle waves in the last workgroup
 ])
 def test_prefill_quantized_cache(gpu, bits, Hq, Hkv, Tb, lens, L):
     """Prefill over an affine-quantized cache: each query against the
