@@ -399,6 +399,7 @@ int bsattn_reserve(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int3
   rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   std::vector<std::pair<int32_t, int32_t>> patches;
   rc = reserve_pages(c, seqs, n_tokens, patches);
   if (rc) return rc;
@@ -414,6 +415,7 @@ int bsattn_append_step(bsattn_cache* c, const void* k, const void* v, const int3
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   hipStream_t s = (hipStream_t)stream;
   const size_t row = (size_t)c->geo.hkv * kHeadDim;  // elements per sequence
   for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
@@ -435,6 +437,7 @@ int bsattn_append_step(bsattn_cache* c, const void* k, const void* v, const int3
 int bsattn_sync(bsattn_cache* c, void* stream) {
   if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
   std::vector<int32_t> dev(c->d.max_seqs);
   HIP_TRY(hipMemcpy(dev.data(), c->geo.meta, dev.size() * 4, hipMemcpyDeviceToHost), "hipMemcpy(lengths)");
@@ -456,6 +459,7 @@ int append_impl(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t
   rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   std::vector<std::pair<int32_t, int32_t>> patches;
   rc = reserve_pages(c, seqs, n_tokens, patches);
   if (rc) return rc;
@@ -612,6 +616,7 @@ int bsattn_select(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   return run_entries(c, Op::Select, q, entries(c, seqs, 1), kHeadDim, nullptr, idx_out, 0.0f, nullptr,
                      (hipStream_t)stream);
 }
@@ -623,6 +628,7 @@ int bsattn_attend(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   return run_entries(c, Op::Attend, q, entries(c, seqs, 1), kHeadDim, idx, nullptr, scale, out,
                      (hipStream_t)stream);
 }
@@ -634,6 +640,7 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   return run_entries(c, Op::Decode, q, entries(c, seqs, 1), kHeadDim, nullptr, idx_out, scale, out,
                      (hipStream_t)stream);
 }
@@ -652,6 +659,7 @@ int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, 
       return fail(BSATTN_ERR_INVALID, "sequence %d holds %d tokens, fewer than its %d queries", sq, c->len[sq],
                   n_query);
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   return run_entries(c, Op::Decode, q, entries(c, seqs, n_query), n_query * kHeadDim, nullptr, idx_out,
                      scale, out, (hipStream_t)stream);
 }
@@ -669,6 +677,7 @@ int bsattn_prefill(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32
       return fail(BSATTN_ERR_INVALID, "sequence %d holds %d tokens, fewer than its %d queries", sq, c->len[sq],
                   n_query);
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   hipStream_t s = (hipStream_t)stream;
   // q / out [n, Hq, L, D]: a launch takes whole sequences whose row offsets fit int32
   const int64_t per_seq = (int64_t)c->geo.hq * n_query * kHeadDim;
@@ -702,6 +711,7 @@ int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   std::vector<std::pair<int32_t, int32_t>> patches;
   for (int i = 0; i < n_seqs; ++i) {
     const int sq = seqs[i];
@@ -721,6 +731,7 @@ int bsattn_reset(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* 
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   std::vector<std::pair<int32_t, int32_t>> patches;
   for (int sq : seqs) {
     c->len[sq] = 0;
@@ -737,6 +748,7 @@ int bsattn_copy(const bsattn_cache* src, bsattn_cache** out, void* stream) {
   if (rc) return rc;
   bsattn_cache* c = *out;
   DeviceGuard dg(src->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", src->d.device);
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if ((e = hipMemcpyAsync(c->geo.pool, src->geo.pool, src->pool_bytes, hipMemcpyDeviceToDevice, s)) != hipSuccess ||
@@ -765,6 +777,7 @@ int bsattn_export(const bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs,
     if (c->len[sq] != T) return fail(BSATTN_ERR_INVALID, "listed sequences hold different token counts");
   if (T == 0) return BSATTN_OK;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   const size_t row = (size_t)c->geo.hkv * T * kHeadDim * 2;
   for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
     SeqBatch b{};
@@ -794,6 +807,7 @@ int bsattn_export_quantized(const bsattn_cache* c, const int32_t* seq_ids, int32
     if (c->len[sq] != T) return fail(BSATTN_ERR_INVALID, "listed sequences hold different token counts");
   if (T == 0) return BSATTN_OK;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   const size_t rows = (size_t)c->geo.hkv * T;
   const size_t words = kHeadDim * c->d.kv_bits / 32, groups = kHeadDim / c->d.group_size;
   for (int i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
@@ -819,6 +833,7 @@ int bsattn_export_summaries(const bsattn_cache* c, int32_t seq, void* out, void*
   const int nfull = c->len[seq] / c->d.block_size;
   if (nfull == 0) return BSATTN_OK;
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   HIP_TRY(launch_export_summaries(c->geo, seq, nfull, out, (hipStream_t)stream), "export summaries launch");
   return BSATTN_OK;
 }
@@ -826,6 +841,7 @@ int bsattn_export_summaries(const bsattn_cache* c, int32_t seq, void* out, void*
 int bsattn_profile_enable(bsattn_cache* c, int32_t enable) {
   if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   int rc = prof_drain(c);
   if (rc) return rc;
   for (int k = 0; k < kProfKinds; ++k) {
@@ -840,6 +856,7 @@ int bsattn_profile_read(bsattn_cache* c, int32_t kernel, double* total_ms, int64
   if (!c || !total_ms || !launches) return fail(BSATTN_ERR_INVALID, "null argument");
   if (kernel < 0 || kernel >= kProfKinds) return fail(BSATTN_ERR_INVALID, "unknown kernel id %d", kernel);
   DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   int rc = prof_drain(c);
   if (rc) return rc;
   *total_ms = c->prof_ms[kernel];
