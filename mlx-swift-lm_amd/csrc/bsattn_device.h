@@ -312,6 +312,19 @@ __device__ __forceinline__ uint32_t wave_kth_key(const uint32_t (&key)[S], int n
       wave_lds_order();
       const bool valid = lane < cnt;
       const uint32_t x = valid ? small[lane] : 0u;
+      if (cnt <= 16) {
+        // few keys: each lane counts the keys above and at its own; the
+        // need-th largest is the key with gt < need <= ge
+        int gt = 0, ge = 0;
+        for (int jj = 0; jj < cnt; ++jj) {
+          const uint32_t xj = (uint32_t)__builtin_amdgcn_readlane((int)x, jj);
+          gt += xj > x;
+          ge += xj >= x;
+        }
+        const int src = __ffsll((unsigned long long)__ballot(valid && gt < need && need <= ge)) - 1;
+        wave_lds_order();  // the scratch may be reused right after
+        return (uint32_t)__builtin_amdgcn_readlane((int)x, src);
+      }
       const uint32_t mn = wave_min_u32(valid ? x : 0xFFFFFFFFu), mx = wave_max_u32(x);
       const uint32_t off = x - mn;
       uint32_t t = 0u;
