@@ -56,9 +56,11 @@ __device__ __forceinline__ void summary16(const Geometry& geo, const uint16_t* _
 
 // ---------------------------------------------------------------------------
 // append: 16 tokens x 16 lanes (8 dims each) per workgroup.  With
-// fuse_summary (one token per sequence), the 16 lanes of a token that fills
-// its block also write the block's summary: every K chunk a lane folds was
-// written by that lane itself or by an earlier launch.
+// fuse_summary (one token per sequence: the workgroup's token 0), a token
+// that fills its block also writes the block's summary: the whole workgroup
+// loads the block's other keys into LDS in one round of loads (the new key
+// comes from the registers of the lanes that wrote it), and its 16 lanes then
+// fold the block in token order from LDS, as summary16 does from memory.
 // grid (ceil(L/16), Hkv, n)
 // ---------------------------------------------------------------------------
 template <int DT>
@@ -66,10 +68,10 @@ __global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
                                                 const uint16_t* __restrict__ k,
                                                 const uint16_t* __restrict__ v, bool fuse_summary,
                                                 bool device_len) {
+  __shared__ u32x4 s_blk[64][16];  // the filled block's keys, [token][8-dim chunk]
   const int bi = blockIdx.z, h = blockIdx.y;
-  const int tok = blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int c = threadIdx.x & 15;
-  if (tok >= ab.L) return;
+  const int tg = threadIdx.x >> 4, c = threadIdx.x & 15;
+  const int tok = blockIdx.x * 16 + tg;
   const int seq = ab.seq[bi];
   // device_len: the position is the device-side length (one token; a
   // sequence without a reserved page for it takes nothing)
@@ -78,23 +80,52 @@ __global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
     base = geo.meta[seq];
     if (base >= geo.meta[geo.cap_off + seq]) return;
   }
-  const int pos = base + tok;
-  const int blk = pos / geo.tb, slot = pos - blk * geo.tb;
-  const int page = block_table(geo, seq)[blk];
-  const size_t src = (((size_t)bi * geo.hkv + h) * ab.L + tok) * kHeadDim + 8 * c;
-  const u32x4 kr = *(const u32x4*)(k + src);
-  const u32x4 vr = *(const u32x4*)(v + src);
-  uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
-  // dims 8c .. 8c+7 of a key are 16 contiguous bytes of the K tile
-  uint16_t* Kt = (uint16_t*)(slab + geo.k_off);
-  *(u32x4*)(Kt + k_elem(slot, 8 * c)) = kr;
-  uint16_t* Vt = (uint16_t*)(slab + geo.v_off);
+  const int32_t* bt = block_table(geo, seq);
+  u32x4 kr = u32x4{0u, 0u, 0u, 0u};
+  if (tok < ab.L) {
+    const int pos = base + tok;
+    const int blk = pos / geo.tb, slot = pos - blk * geo.tb;
+    const int page = bt[blk];
+    const size_t src = (((size_t)bi * geo.hkv + h) * ab.L + tok) * kHeadDim + 8 * c;
+    kr = *(const u32x4*)(k + src);
+    const u32x4 vr = *(const u32x4*)(v + src);
+    uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
+    // dims 8c .. 8c+7 of a key are 16 contiguous bytes of the K tile
+    uint16_t* Kt = (uint16_t*)(slab + geo.k_off);
+    *(u32x4*)(Kt + k_elem(slot, 8 * c)) = kr;
+    uint16_t* Vt = (uint16_t*)(slab + geo.v_off);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t w = vr[e >> 1];
-    Vt[v_elem(geo.tb, slot, 8 * c + e)] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xFFFFu));
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t w = vr[e >> 1];
+      Vt[v_elem(geo.tb, slot, 8 * c + e)] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xFFFFu));
+    }
   }
-  if (fuse_summary && slot == geo.tb - 1) summary16<DT>(geo, Kt, c, summary_row(geo, seq, h, blk));
+  if (!fuse_summary) return;
+  // the workgroup's token 0 (the only one) fills its block: uniform branch
+  const int blk = base / geo.tb;
+  if (base - blk * geo.tb != geo.tb - 1) return;
+  const int page = bt[blk];
+  const uint16_t* Kt =
+      (const uint16_t*)(geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes + geo.k_off);
+  // keys 0 .. Tb-2 were written by earlier launches; key Tb-1 is kr of tg 0
+  for (int t = tg; t < geo.tb - 1; t += 16) s_blk[t][c] = *(const u32x4*)(Kt + k_elem(t, 8 * c));
+  if (tg == 0) s_blk[geo.tb - 1][c] = kr;
+  __syncthreads();
+  if (tg != 0) return;
+  float acc[8];
+  unpack8<DT>(s_blk[0][c], acc);
+  for (int t = 1; t < geo.tb; ++t) {
+    float x[8];
+    unpack8<DT>(s_blk[t][c], x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = __fadd_rn(acc[e], x[e]);
+  }
+  const float inv = 1.0f / (float)geo.tb;
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack2<DT>(__fmul_rn(acc[2 * e], inv), __fmul_rn(acc[2 * e + 1], inv));
+  *(u32x4*)(summary_row(geo, seq, h, blk) + 8 * c) = o;
 }
 
 // ---------------------------------------------------------------------------
