@@ -72,6 +72,13 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
   constexpr float kLazy = 8.f;
   __shared__ __align__(16) u32x4 s_kv0[16 * 64], s_kv1[16 * 64];
   __shared__ __align__(16) u32x4 s_raw0[KB ? RAWF * 64 + 32 : 1], s_raw1[KB ? RAWF * 64 + 32 : 1];
+  // bf16 caches: the unit's V as fp16 (exact for |v| < 65520 down to the
+  // fp16 normal range) for an fp16 PV product without the hi / lo split of
+  // P; s_big[u & 1] flags a unit holding a value fp16 cannot take (its PV
+  // then runs in bf16 with P as hi + lo)
+  constexpr bool CV = KB == 0 && DT == 1;
+  __shared__ __align__(16) u32x4 s_v16[CV ? 8 * 64 : 1];
+  __shared__ int s_big[2];
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   // XCD-grouped workgroup order (a bijection on [0, total))
@@ -229,9 +236,12 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
     for (int dt = 0; dt < 8; ++dt) o[r][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   // unit u from LDS (tokens 32 u .. 32 u + 31 of the sequence); MASK: the
-  // causal limit and the sequence end apply
-  auto unit = [&](int u, const u32x4* kv, auto mask_tag) __attribute__((always_inline)) {
+  // causal limit and the sequence end apply.  PDT: type of the PV product
+  // (P and V); when it differs from DT, V comes from the fp16 copy vkv.
+  auto unit = [&](int u, const u32x4* kv, const u32x4* vkv, auto mask_tag, auto pdt_tag)
+      __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr int PDT = decltype(pdt_tag)::value;
     f32x4 acc[R][2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -248,6 +258,7 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
     // P^T operand: lane (column n, group g) -> tokens 32 u + tok_of(g,
     // 2 jj (+1)); bf16 P is split into hi + lo
     u32x4 pf[R], pl[R];
+    (void)pl;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float x[8];
@@ -288,16 +299,16 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const float p0 = x[2 * jj], p1 = x[2 * jj + 1];
-        const uint32_t hi = cvt_pk<DT>(p0, p1);
+        const uint32_t hi = cvt_pk<PDT>(p0, p1);
         pf[r][jj] = hi;
-        if constexpr (DT == 1)
+        if constexpr (PDT == 1)
           pl[r][jj] = cvt_pk<1>(p0 - __uint_as_float(hi << 16), p1 - __uint_as_float(hi & 0xFFFF0000u));
       }
     }
     const int valid = min(32, T - 32 * u);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      u32x4 vf = kv[(8 + dt) * 64];
+      u32x4 vf = PDT == DT ? kv[(8 + dt) * 64] : vkv[dt * 64];
       if constexpr (MASK) {
         // V of tokens past the sequence end (stale page data) is zeroed
 #pragma unroll
@@ -308,8 +319,8 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        o[r][dt] = mfma16x16x32<DT>(vf, pf[r], o[r][dt]);
-        if constexpr (DT == 1) o[r][dt] = mfma16x16x32<DT>(vf, pl[r], o[r][dt]);
+        o[r][dt] = mfma16x16x32<PDT>(vf, pf[r], o[r][dt]);
+        if constexpr (PDT == 1) o[r][dt] = mfma16x16x32<PDT>(vf, pl[r], o[r][dt]);
       }
     }
   };
@@ -329,7 +340,33 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
       if (u + 2 < nunit) fetch_raw(u + 2, raw_ld);
       if (u + 1 < nunit) dequant(raw_dq, nxt);
     }
-    if constexpr (decltype(act)::value) unit(u, cur + lane, mask_tag);
+    if constexpr (CV) {
+      // V of unit u to fp16 (two fragment lanes per thread); a bf16 value of
+      // magnitude >= 65536 (or inf / NaN) flags the unit
+      bool big = false;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int it = threadIdx.x + 256 * i;
+        const u32x4 w = cur[(8 + (it >> 6)) * 64 + (it & 63)];
+        u32x4 h;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t x = w[k];
+          big |= (x & 0x7FFFu) >= 0x4780u || ((x >> 16) & 0x7FFFu) >= 0x4780u;
+          h[k] = cvt_pk<0>(__uint_as_float(x << 16), __uint_as_float(x & 0xFFFF0000u));
+        }
+        s_v16[it] = h;
+      }
+      if (__builtin_amdgcn_ballot_w64(big) != 0 && lane == 0) s_big[u & 1] = 1;
+      if (threadIdx.x == 0) s_big[(u + 1) & 1] = 0;  // last read in step u - 1
+      __syncthreads();
+      if constexpr (decltype(act)::value) {
+        if (s_big[u & 1]) unit(u, cur + lane, s_v16 + lane, mask_tag, std::integral_constant<int, 1>{});
+        else unit(u, cur + lane, s_v16 + lane, mask_tag, std::integral_constant<int, 0>{});
+      }
+    } else if constexpr (decltype(act)::value) {
+      unit(u, cur + lane, nullptr, mask_tag, std::integral_constant<int, DT>{});
+    }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS loads have landed
     __syncthreads();
   };
@@ -355,6 +392,7 @@ __global__ __launch_bounds__(64 * W, OCC) void k_prefill(Geometry geo, SeqBatch 
     }
   };
   if constexpr (KB == 0) {
+    if (threadIdx.x == 0) s_big[0] = 0;
     fetch(0, s_kv0);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();

@@ -7,7 +7,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from common import from_dev, log, make_workload, new_cache, output_error, to_dev
+from common import from_dev, log, make_workload, new_cache, output_error, to_dev, ulp
 import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -63,6 +63,36 @@ def test_prefill_matches_dense_attention(gpu, dtype, Hq, Hkv, Tb, lens, L):
     got, qm, _ = _run(w, gpu, L)
     err = _check(w, got, qm, L, sorted({0, 1, L // 2, L - 2, L - 1}))
     log(f"[prefill] err={err:.3g}")
+
+
+def test_prefill_bf16_values_beyond_fp16(gpu):
+    """bf16 V values fp16 cannot hold (|v| >= 65536, scaled by 2^17 on a few
+    tokens): the units holding them take the bf16 PV path, the others the
+    fp16 one; every checked query against the oracle."""
+    log("[prefill] bf16 V beyond the fp16 range")
+    L = 64
+    w = make_workload(7700, B=2, Hq=32, Hkv=8, T=1500, Tb=64, dtype="bf16", top_k=4, lens=[1500, 1400])
+    for b in range(w.B):
+        v = O.to_f32(w.values[b], "bf16")
+        rows = np.arange(37, w.lens[b], 211)          # a few tokens in several units
+        v[:, rows, :] *= 2.0 ** 17
+        w.values[b] = O.from_f32(v, "bf16")
+    got, qm, _ = _run(w, gpu, L)
+    # the error bound scales with sum_i p_i |v_i|, which the oracle's dense
+    # attention over |V| gives; for unit-scale values it is the plain TOL
+    worst = 0.0
+    for b in range(w.B):
+        for i in sorted({0, 1, L // 2, L - 1}):
+            pos = w.lens[b] - L + i
+            for h in range(w.Hkv):
+                qh, kh, vh = qm[b, h * w.G:(h + 1) * w.G, i], w.keys[b][h][:pos + 1], w.values[b][h][:pos + 1]
+                ref = O.dense(qh, kh, vh, w.scale, w.dtype)
+                mag = O.dense(qh, kh, vh & np.uint16(0x7FFF), w.scale, w.dtype)
+                a = O.to_f32(got[b, h * w.G:(h + 1) * w.G, i], w.dtype).astype(np.float64)
+                err = float(np.max((np.abs(a - ref) - 0.5 * ulp(ref, w.dtype)) / np.maximum(1.0, mag)))
+                assert err <= TOL, f"seq {b} query {i} head {h}: relative error {err:.3g}"
+                worst = max(worst, err)
+    log(f"[prefill] relative err={worst:.3g}")
 
 
 def test_prefill_whole_prompt(gpu):
