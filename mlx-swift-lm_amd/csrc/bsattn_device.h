@@ -424,6 +424,263 @@ __device__ __forceinline__ void wave_topk(const WaveCand& wc, int c0, int nc, in
   else wave_topk_s<16>(wc, c0, nc, K, sel_blk, sel_page, ws);
 }
 
+// ---------------------------------------------------------------------------
+// workgroup-wide top-K inside the attention workgroup, for candidate sets
+// up to 64 * W * kWgKeys: the same selection as wave_topk (K largest keys,
+// ties to the lower index), with the candidates spread over all W waves so
+// that no wave holds more than kWgKeys per lane.  Slot k of wave w, lane l
+// holds candidate c0 + 64 (W k + w) + l, so S = ceil(nc / (64 W)) slots
+// carry every candidate and the waves share them evenly.  The histogram
+// passes of wave_kth_key run on one LDS histogram that all waves fill;
+// every wave then reads the whole histogram and reaches the same decision,
+// so only the fills and the small-set compaction need barriers.
+// ---------------------------------------------------------------------------
+constexpr int kWgKeys = 8;
+// LDS words: histogram, small set, small-set count, per-wave lo / hi, and
+// per-(slot, wave) counts of keys above / at the threshold
+constexpr int kWgScratch = kWaveBins + 64 + 4 + 2 * 16 + 2 * 64;
+
+struct WgCand {
+  float score[kWgKeys];
+  int page[kWgKeys];
+};
+template <int W>
+__device__ __forceinline__ void wg_cand_load(const float* __restrict__ srow,
+                                             const int32_t* __restrict__ bt, int c0, int mbps,
+                                             int wave, WgCand& wc) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < kWgKeys; ++k) {
+    const int j = c0 + 64 * (W * k + wave) + lane;
+    wc.score[k] = j < mbps ? srow[j] : 0.0f;
+    wc.page[k] = (bt != nullptr && j < mbps) ? bt[j] : 0;
+  }
+}
+
+template <int S, int W>
+__device__ __forceinline__ uint32_t wg_kth_key(const uint32_t (&key)[S], const bool (&real)[S], int K,
+                                               uint32_t* ws) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  uint32_t* hist = ws;
+  uint32_t* small = ws + kWaveBins;
+  uint32_t* small_n = small + 64;
+  uint32_t* xlo = small_n + 4;
+  uint32_t* xhi = xlo + 16;
+  uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+#pragma unroll
+  for (int k = 0; k < S; ++k)
+    if (real[k]) {
+      lo = min(lo, key[k]);
+      hi = max(hi, key[k]);
+    }
+  lo = wave_min_u32(lo);
+  hi = wave_max_u32(hi);
+  if (lane == 0) {
+    xlo[wave] = lo;
+    xhi[wave] = hi;
+  }
+  __syncthreads();
+  lo = xlo[0];
+  hi = xhi[0];
+#pragma unroll
+  for (int w = 1; w < W; ++w) {
+    lo = min(lo, xlo[w]);
+    hi = max(hi, xhi[w]);
+  }
+  int need = K;
+  bool by_value = true;
+#pragma unroll 1
+  while (true) {
+    if (lo == hi) return lo;
+    const float vlo = key_value(lo), span = key_value(hi) - vlo;
+    const bool use_v = by_value && __builtin_isfinite(vlo) && __builtin_isfinite(span) && span > 0.0f;
+    const float scale = use_v ? (float)(kWaveBins - 1) / span : 0.0f;
+    const int sh = use_v ? 0 : max(0, 32 - __clz(hi - lo) - 10);
+    auto bin = [&](uint32_t k) -> int {
+      return use_v ? min(kWaveBins - 1, (int)((key_value(k) - vlo) * scale)) : (int)((k - lo) >> sh);
+    };
+    // every wave's previous reads of the histogram and exchange words are
+    // done before they are cleared (barrier at the end of the pass)
+    for (int i = threadIdx.x; i < kWaveBins / 4; i += 64 * W) ((u32x4*)hist)[i] = u32x4{0u, 0u, 0u, 0u};
+    if (threadIdx.x == 0) *small_n = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < S; ++k)
+      if (real[k] && key[k] >= lo && key[k] <= hi) atomicAdd(&hist[bin(key[k])], 1u);
+    __syncthreads();
+    constexpr int BPL = kWaveBins / 64;
+    const u32x4* r4 = (const u32x4*)(hist + kWaveBins - BPL * (lane + 1));
+    uint32_t c[BPL];
+#pragma unroll
+    for (int i = 0; i < BPL / 4; ++i) {
+      const u32x4 v = r4[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c[BPL - 1 - (4 * i + e)] = v[e];
+    }
+    int lsum = 0;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) lsum += (int)c[j];
+    const int incl = wave_scan_incl(lsum);
+    const int excl = incl - lsum;
+    const bool mine = excl < need && need <= incl;
+    int b_star = 0, abv = 0, cnt = 0;
+    if (mine) {
+      int cum = excl;
+#pragma unroll
+      for (int j = 0; j < BPL; ++j) {
+        if (cum < need && need <= cum + (int)c[j]) {
+          b_star = kWaveBins - 1 - BPL * lane - j;
+          abv = cum;
+          cnt = (int)c[j];
+        }
+        cum += (int)c[j];
+      }
+    }
+    const int src = __ffsll((unsigned long long)__ballot(mine)) - 1;
+    b_star = __builtin_amdgcn_readlane(b_star, src);
+    abv = __builtin_amdgcn_readlane(abv, src);
+    cnt = __builtin_amdgcn_readlane(cnt, src);
+    need -= abv;
+    if (!use_v && sh == 0) return lo + (uint32_t)b_star;  // one-value bin
+    if (cnt <= 64) {
+      // the bin's keys from every wave, in any order
+      int mine_n = 0;
+      uint64_t m[S];
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        m[k] = __ballot(real[k] && key[k] >= lo && key[k] <= hi && bin(key[k]) == b_star);
+        mine_n += __popcll(m[k]);
+      }
+      uint32_t base = 0u;
+      if (lane == 0 && mine_n > 0) base = atomicAdd(small_n, (uint32_t)mine_n);
+      base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        if ((m[k] >> lane) & 1ull) small[base + __popcll(m[k] & below)] = key[k];
+        base += __popcll(m[k]);
+      }
+      __syncthreads();
+      const bool valid = lane < cnt;
+      const uint32_t x = valid ? small[lane] : 0u;
+      uint32_t tau;
+      if (cnt <= 16) {
+        int gt = 0, ge = 0;
+        for (int jj = 0; jj < cnt; ++jj) {
+          const uint32_t xj = (uint32_t)__builtin_amdgcn_readlane((int)x, jj);
+          gt += xj > x;
+          ge += xj >= x;
+        }
+        const int s2 = __ffsll((unsigned long long)__ballot(valid && gt < need && need <= ge)) - 1;
+        tau = (uint32_t)__builtin_amdgcn_readlane((int)x, s2);
+      } else {
+        const uint32_t mn = wave_min_u32(valid ? x : 0xFFFFFFFFu), mx = wave_max_u32(x);
+        const uint32_t off = x - mn;
+        uint32_t t = 0u;
+        for (int bit = mx == mn ? -1 : 31 - __clz(mx - mn); bit >= 0; --bit) {
+          const uint32_t cand = t | (1u << bit);
+          if (__popcll(__ballot(valid && off >= cand)) >= need) t = cand;
+        }
+        tau = mn + t;
+      }
+      __syncthreads();  // the scratch may be reused right after
+      return tau;
+    }
+    if (use_v) {
+      uint32_t nlo = 0xFFFFFFFFu, nhi = 0u;
+#pragma unroll
+      for (int k = 0; k < S; ++k)
+        if (real[k] && key[k] >= lo && key[k] <= hi && bin(key[k]) == b_star) {
+          nlo = min(nlo, key[k]);
+          nhi = max(nhi, key[k]);
+        }
+      nlo = wave_min_u32(nlo);
+      nhi = wave_max_u32(nhi);
+      if (lane == 0) {
+        xlo[wave] = nlo;
+        xhi[wave] = nhi;
+      }
+      __syncthreads();
+      lo = xlo[0];
+      hi = xhi[0];
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        lo = min(lo, xlo[w]);
+        hi = max(hi, xhi[w]);
+      }
+    } else {
+      const uint32_t nlo = lo + ((uint32_t)b_star << sh);
+      const uint32_t span_k = (1u << sh) - 1u;
+      hi = (hi - nlo < span_k) ? hi : nlo + span_k;
+      lo = nlo;
+    }
+    by_value = false;
+    __syncthreads();
+  }
+}
+
+// Top-K of candidates c0 .. c0+nc-1 (nc <= 64 * W * S, nc > K > 0) held as
+// wg_cand_load left them; writes the K chosen block indices, ascending, to
+// sel_blk and their pages to sel_page.  Every wave of the workgroup calls
+// it (it contains workgroup barriers); ws: kWgScratch words of LDS.
+template <int S, int W>
+__device__ __forceinline__ void wg_topk_s(const WgCand& wc, int c0, int nc, int K, int* sel_blk,
+                                          int* sel_page, uint32_t* ws) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t key[S];
+  bool real[S];
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    real[k] = 64 * (W * k + wave) + lane < nc;
+    key[k] = real[k] ? score_key(wc.score[k]) : 0u;
+  }
+  const uint32_t tau = wg_kth_key<S, W>(key, real, K, ws);
+  // per-(slot, wave) counts of keys above and at tau, in candidate order
+  uint32_t* cgt = ws + kWaveBins + 64 + 4 + 32;
+  uint32_t* ceq = cgt + 64;
+  uint64_t gtm[S], eqm[S];
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    gtm[k] = __ballot(real[k] && key[k] > tau);
+    eqm[k] = __ballot(real[k] && key[k] == tau);
+    if (lane == 0) {
+      cgt[W * k + wave] = (uint32_t)__popcll(gtm[k]);
+      ceq[W * k + wave] = (uint32_t)__popcll(eqm[k]);
+    }
+  }
+  __syncthreads();
+  // exclusive prefix over the S * W (slot, wave) groups, one group per lane
+  const int gi = lane < S * W ? (int)cgt[lane] : 0, ei = lane < S * W ? (int)ceq[lane] : 0;
+  const int ginc = wave_scan_incl(gi), einc = wave_scan_incl(ei);
+  const int gt_total = __builtin_amdgcn_readlane(ginc, 63);
+  const int krem = K - gt_total;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    const int f = W * k + wave;
+    const int gpre = __builtin_amdgcn_readlane(ginc - gi, f);
+    const int epre = __builtin_amdgcn_readlane(einc - ei, f);
+    const bool gt = (gtm[k] >> lane) & 1ull, eq = (eqm[k] >> lane) & 1ull;
+    const int eb = epre + __popcll(eqm[k] & below);
+    const bool take = gt || (eq && eb < krem);
+    if (take) {
+      const int pos = gpre + __popcll(gtm[k] & below) + min(eb, krem);
+      sel_blk[pos] = c0 + 64 * f + lane;
+      if (sel_page) sel_page[pos] = wc.page[k];
+    }
+  }
+}
+
+// S = smallest power of two with 64 * W * S >= nc (nc <= 64 * W * kWgKeys)
+template <int W>
+__device__ __forceinline__ void wg_topk(const WgCand& wc, int c0, int nc, int K, int* sel_blk,
+                                        int* sel_page, uint32_t* ws) {
+  if (nc <= 64 * W) wg_topk_s<1, W>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else if (nc <= 128 * W) wg_topk_s<2, W>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else if (nc <= 256 * W) wg_topk_s<4, W>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else wg_topk_s<8, W>(wc, c0, nc, K, sel_blk, sel_page, ws);
+}
+
 // Block in output slot p of the selection for nb blocks: sinks [0, ns),
 // then the K ranked candidates (sel), then recent [nb - nr, nb); when the
 // candidates do not outnumber K every block is kept.
@@ -547,10 +804,11 @@ struct QCode {
 // kv head); wave w of split `split` handles slot split * W + w.
 // ---------------------------------------------------------------------------
 // Block (j) and physical page of this wave's slot, -1 when the slot is empty.
-// SEL: the selection is computed here from the block scores (wave 0 runs
-// wave_topk for the sequence and kv head, loading the candidates' block-table
-// entries alongside their scores, and shares blocks and pages through
-// s_sel / s_selp); forced slots load their page before the selection is
+// SEL 1 / 2: the selection is computed here from the block scores (1: wave 0
+// runs wave_topk over up to 64 * kSelKeysPerLane candidates; 2: every wave
+// runs wg_topk over up to 64 * W * kWgKeys), the candidates' block-table
+// entries loaded alongside their scores, blocks and pages shared through
+// s_sel / s_selp; forced slots load their page before the selection is
 // known.  Split 0 then writes the selected indices to idx (if not null).
 // Otherwise the block is jg (given_index); -1 and indices past the
 // sequence's last block contribute nothing.  Contains a workgroup barrier
@@ -561,12 +819,13 @@ __device__ __forceinline__ int given_index(const Geometry& geo, const int32_t* _
   return slot < geo.nsel_max ? idx[((size_t)bi * geo.hkv + h) * geo.nsel_max + slot] : -1;
 }
 
-template <int TB, int W, bool SEL>
+template <int TB, int W, int SEL>
 __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, int seq, int len,
                                             int split, int wave, int lane,
                                             int32_t* __restrict__ idx, int jg,
-                                            const WaveCand* wc, int* s_sel, int* s_selp,
-                                            uint32_t* s_ws, int& j_out, int& page_out) {
+                                            const WaveCand* wc, const WgCand* wgc, int* s_sel,
+                                            int* s_selp, uint32_t* s_ws, int& j_out,
+                                            int& page_out) {
   const int slot = split * W + wave;
   int j = -1, page = -1;
   if constexpr (SEL) {
@@ -580,8 +839,9 @@ __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, 
       j = selected_block(slot, nb, ranked, geo.ns, geo.nr, K, s_sel);
       if (j >= 0) page = uniform(bt[j]);
     }
-    if (ranked && K > 0) {  // one wave selects, the workgroup shares the result
-      if (wave == 0) wave_topk(*wc, c0, nc, K, s_sel, s_selp, s_ws);
+    if (ranked && K > 0) {  // the workgroup shares the selection through LDS
+      if constexpr (SEL == 2) wg_topk<W>(*wgc, c0, nc, K, s_sel, s_selp, s_ws);
+      else if (wave == 0) wave_topk(*wc, c0, nc, K, s_sel, s_selp, s_ws);
       __syncthreads();
       if (picked) {
         j = s_sel[slot - geo.ns];

@@ -108,7 +108,7 @@ hipError_t launch_append_quantized(const Geometry& g, const AppendBatch& ab,
 hipError_t launch_summary_q(const Geometry& g, const SummaryBatch& sb, int max_count,
                             hipStream_t s, Timing* prof);
 hipError_t launch_attend_q(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
-                           const float* scores, bool fused_select, float sl2, void* out,
+                           const float* scores, int sel_mode, float sl2, void* out,
                            float* partials, hipStream_t s, Timing* prof);
 hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
                           hipStream_t s, Timing* prof);

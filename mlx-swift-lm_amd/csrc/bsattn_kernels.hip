@@ -238,15 +238,16 @@ __global__ __launch_bounds__(64) void k_topk(Geometry geo, SeqBatch sb,
 // and every K/V load of a wave is issued before the first wait (a scheduling
 // barrier keeps the compiler from interleaving them with the MFMAs).
 // bf16: P is split into hi + lo bf16 parts (two MFMAs) for ~16-bit P.
-// SEL: the selection is computed here from the block scores (wave 0 runs
-// wave_topk for the sequence and kv head, loading the candidates' block-table
-// entries alongside their scores, and shares blocks and pages through LDS)
-// instead of being read from idx; split 0 then writes the selected indices
-// to idx (if not null).
+// SEL 1 / 2: the selection is computed here from the block scores instead
+// of being read from idx (1: wave 0 runs wave_topk; 2: all W waves run
+// wg_topk, each holding a share of the candidates), loading the candidates'
+// block-table entries alongside their scores and sharing blocks and pages
+// through LDS; split 0 then writes the selected indices to idx (if not
+// null).  SEL 0: the blocks are read from idx.
 // With more than one split, each workgroup writes an unnormalised partial
 // (o, m, l) for k_combine.  grid (nsplit, Hkv, n)
 // ---------------------------------------------------------------------------
-template <int DT, int TB, int G, int W, bool SEL>
+template <int DT, int TB, int G, int W, int SEL>
 __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
                                                    const uint16_t* __restrict__ q,
                                                    int32_t* __restrict__ idx,
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   __shared__ float s_o[W][G][kHeadDim];
   __shared__ int s_sel[SEL ? kSelMaxK : 1];
   __shared__ int s_selp[SEL ? kSelMaxK : 1];
-  __shared__ __align__(16) uint32_t s_ws[SEL ? kWaveScratch : 4];
+  __shared__ __align__(16) uint32_t s_ws[SEL == 2 ? kWgScratch : SEL ? kWaveScratch : 4];
   const int split = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
@@ -279,14 +280,18 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   // the selecting wave loads every candidate's score and page before the
   // sequence length is known
   WaveCand wc;
-  if constexpr (SEL) {
+  WgCand wgc;
+  if constexpr (SEL == 1) {
     if (wave == 0)
       wave_cand_load(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns,
                      geo.mbps, wc);
+  } else if constexpr (SEL == 2) {
+    wg_cand_load<W>(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns, geo.mbps, wave,
+                    wgc);
   }
   const int len = uniform(entry_len(geo, sb, bi, seq));
   int j, page;
-  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, jg, &wc, s_sel, s_selp, s_ws, j,
+  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, jg, &wc, &wgc, s_sel, s_selp, s_ws, j,
                           page);
   if (j >= 0) {
     const int valid = min(TB, len - j * TB);
@@ -562,7 +567,7 @@ hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, fl
   return hipGetLastError();
 }
 
-template <int DT, int TB, bool SEL>
+template <int DT, int TB, int SEL>
 static void attend_dispatch(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
                             int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
                             hipStream_t s, Timing* prof) {
@@ -578,7 +583,7 @@ static void attend_dispatch(const Geometry& g, dim3 grid, const SeqBatch& b, con
   }
 }
 
-template <bool SEL>
+template <int SEL>
 static hipError_t attend_impl(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
                               const float* scores, float scale, void* out, float* partials,
                               hipStream_t s, Timing* prof) {
@@ -608,18 +613,26 @@ static hipError_t attend_impl(const Geometry& g, const SeqBatch& b, const void* 
 
 hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
                          float scale, void* out, float* partials, hipStream_t s, Timing* prof) {
-  return attend_impl<false>(g, b, q, const_cast<int32_t*>(idx), nullptr, scale, out, partials, s,
+  return attend_impl<0>(g, b, q, const_cast<int32_t*>(idx), nullptr, scale, out, partials, s,
                             prof);
 }
 
-int fused_select_limit(int top_k) { return top_k <= kSelMaxK ? 64 * kSelKeysPerLane : 0; }
+int fused_select_limit(int top_k) {
+  return top_k <= kSelMaxK ? 64 * std::max(kWaves * kWgKeys, kSelKeysPerLane) : 0;
+}
 
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                          int32_t* idx_out, int max_nc, float scale, void* out,
                          float* partials, hipStream_t s, Timing* prof) {
   hipError_t e = score_exact(g, b, q, scores, max_nc, s, prof);
   if (e != hipSuccess) return e;
-  return attend_impl<true>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
+  // every wave of the workgroup takes a share of the candidates (measured
+  // faster than one wave selecting, also for 510 candidates: the per-key
+  // work of each pass shrinks W-fold for a few workgroup barriers); with
+  // few waves per workgroup, one wave's larger capacity is used beyond that
+  if (max_nc <= 64 * kWaves * kWgKeys)
+    return attend_impl<2>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
+  return attend_impl<1>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
 }
 
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out, void* v_out,

@@ -268,7 +268,7 @@ __global__ __launch_bounds__(128) void k_summary_q(Geometry geo, SummaryBatch sb
 // the MFMAs as described at the top of this file.  q / out are fp16.
 // grid (nsplit, Hkv, n)
 // ---------------------------------------------------------------------------
-template <int TB, int G, int W, bool SEL, int KB>
+template <int TB, int G, int W, int SEL, int KB>
 __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch sb,
                                                      const uint16_t* __restrict__ q,
                                                      int32_t* __restrict__ idx,
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
   __shared__ float s_o[W][G][kHeadDim];
   __shared__ int s_sel[SEL ? kSelMaxK : 1];
   __shared__ int s_selp[SEL ? kSelMaxK : 1];
-  __shared__ __align__(16) uint32_t s_ws[SEL ? kWaveScratch : 4];
+  __shared__ __align__(16) uint32_t s_ws[SEL == 2 ? kWgScratch : SEL ? kWaveScratch : 4];
   const int split = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
@@ -304,14 +304,18 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
   // the selecting wave loads every candidate's score and page before the
   // sequence length is known
   WaveCand wc;
-  if constexpr (SEL) {
+  WgCand wgc;
+  if constexpr (SEL == 1) {
     if (wave == 0)
       wave_cand_load(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns,
                      geo.mbps, wc);
+  } else if constexpr (SEL == 2) {
+    wg_cand_load<W>(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns, geo.mbps, wave,
+                    wgc);
   }
   const int len = uniform(entry_len(geo, sb, bi, seq));
   int j, page;
-  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, jg, &wc, s_sel, s_selp, s_ws, j,
+  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, jg, &wc, &wgc, s_sel, s_selp, s_ws, j,
                           page);
   if (j >= 0) {
     const int valid = min(TB, len - j * TB);
@@ -510,7 +514,7 @@ hipError_t launch_summary_q(const Geometry& g, const SummaryBatch& sb, int max_c
   return hipGetLastError();
 }
 
-template <int TB, bool SEL, int KB>
+template <int TB, int SEL, int KB>
 static void attend_q_group(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
                            int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
                            hipStream_t s, Timing* prof) {
@@ -526,7 +530,7 @@ static void attend_q_group(const Geometry& g, dim3 grid, const SeqBatch& b, cons
   }
 }
 
-template <bool SEL>
+template <int SEL>
 static void attend_q_sel(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
                          int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
                          hipStream_t s, Timing* prof) {
@@ -540,13 +544,14 @@ static void attend_q_sel(const Geometry& g, dim3 grid, const SeqBatch& b, const 
 }
 
 hipError_t launch_attend_q(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
-                           const float* scores, bool fused_select, float sl2, void* out,
+                           const float* scores, int sel_mode, float sl2, void* out,
                            float* partials, hipStream_t s, Timing* prof) {
   const dim3 grid(g.nsplit, g.hkv, b.n);
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* oo = (uint16_t*)out;
-  if (fused_select) attend_q_sel<true>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
-  else attend_q_sel<false>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+  if (sel_mode == 1) attend_q_sel<1>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+  else if (sel_mode == 2) attend_q_sel<2>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+  else attend_q_sel<0>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
   return hipGetLastError();
 }
 

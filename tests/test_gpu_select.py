@@ -147,3 +147,49 @@ def test_near_equal_scores(gpu, dtype, Hq, Hkv, Tb, K, scale):
     fill(cache, w, gpu)
     err = check(cache, w, gpu)
     log(f"[near-equal] {dtype} G={Hq // Hkv} err={err:.3g}")
+
+
+@pytest.mark.parametrize("case", ["plain", "ties", "near"])
+def test_decode_workgroup_selection(gpu, case):
+    """Decode with 1029 - 2048 candidate blocks: the selection runs inside the
+    attention workgroup with every wave holding a share of the candidates.
+    Indices (written by the decode itself) bit-exact against the oracle for
+    ordinary, all-tied / duplicated and near-equal scores; outputs within
+    the tolerance."""
+    import torch
+    Tb = 64
+    lens = [Tb * 2050, Tb * 1030 + 5, Tb * 1800 - 3]      # 2048, 1029, 1797 candidates
+    w = make_workload(5500 + len(case), B=len(lens), Hq=8, Hkv=2, T=max(lens), Tb=Tb, dtype="bf16",
+                      top_k=40, ns=1, nr=1, lens=lens, salient_frac=0.01 if case == "plain" else 0.0)
+    rng = np.random.default_rng(len(case))
+    for h in range(w.Hkv):
+        if case == "ties":
+            blk = w.keys[0][h][:Tb].copy()
+            for j in range(lens[0] // Tb):
+                w.keys[0][h][j * Tb:(j + 1) * Tb] = blk
+            for b in (1, 2):
+                nbf = lens[b] // Tb
+                for src in rng.choice(nbf - 10, 6, replace=False) + 5:
+                    for dst in rng.choice(nbf - 10, 25, replace=False) + 5:
+                        w.keys[b][h][dst * Tb:(dst + 1) * Tb] = w.keys[b][h][src * Tb:(src + 1) * Tb]
+        elif case == "near":
+            for b in range(w.B):
+                base = rng.standard_normal(128)
+                noise = rng.standard_normal((w.keys[b][h].shape[0], 128)) * 1e-3
+                w.keys[b][h][:] = O.from_f32((base[None, :] + noise).astype(np.float32), w.dtype)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    q = to_dev(w.q[:, :, None, :], w.dtype, gpu)
+    idx_ref, out_ref = oracle_decode(w)
+    idx = torch.full((w.B, w.Hkv, idx_ref.shape[2]), -7, dtype=torch.int32, device=gpu)
+    out = cache.decode(q, w.scale, idx_out=idx)
+    torch.cuda.synchronize()
+    got = idx.cpu().numpy()
+    bad = np.argwhere(got != idx_ref)
+    assert bad.size == 0, f"selected blocks differ at {bad[:5]}"
+    a = from_dev(out).reshape(w.B, w.Hq, w.D)
+    err = output_error(O.to_f32(a, w.dtype).astype(np.float64), out_ref, w.dtype)
+    assert err <= TOL, f"output error {err:.3g}"
+    if case == "ties":
+        assert list(got[0, 0][:41]) == list(range(41))
+    log(f"[wg-select] {case} err={err:.3g}")
