@@ -22,8 +22,10 @@ Other workloads (one JSON line each, not the headline):
                attention mass on two sequences of layer 0;
   --config c4  decode loop with appends: B=32, fp16, lengths U[8192, 65536],
                pages of the sequences interleaved in the pool, 256 steps of
-               (append one token per sequence, score + top-32 + attend);
-               eager, since every append changes host-side page tables;
+               (append one token per sequence, score + top-32 + attend) as
+               one appendDecode call each (append + scoring in one launch;
+               the two-call figure is reported beside it); eager, since
+               every append changes host-side page tables;
   --config pf  dense causal prefill attention of a 512-token chunk at the end
                of 32768 tokens (B=8, Hq=32, Hkv=8, bf16), MFMA-bound;
   --config pfq the same over int4 affine caches (fp16);
@@ -112,6 +114,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
+    ap.add_argument("--counters", action="store_true",
+                    help="short run for hardware-counter profiling (rocprofv3 --pmc): build the "
+                         "layer caches, run --steps eager decode steps and --steps given-index "
+                         "attention passes over every layer, no graph, timing or CPU legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 256 MiB device copy (a known-traffic dispatch "
                          "for scaling hardware byte counters)")
@@ -297,6 +303,15 @@ def bench_layers(args, cfg: Config):
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - te) * 1e3 / args.steps
     log(f"[bench] eager: {eager_ms * 1e3 / L:.2f} us/layer-step")
+    if args.counters:
+        idx = [cache.selectBlocks(q) for cache, q in layers]
+        for _ in range(args.steps):
+            for (cache, q), ii in zip(layers, idx):
+                cache.attend(q, ii, scale)
+        torch.cuda.synchronize()
+        log(f"[bench] counters run done: {args.steps} decode steps and {args.steps} given-index "
+            f"attention passes over {L} layers")
+        return
 
     # graph of one step (all layers)
     s = torch.cuda.Stream()
@@ -473,27 +488,35 @@ def bench_loop(args):
     vn = torch.randn(steps + args.warmup, B, HKV, 1, D, device=dev, generator=g).half()
     qs = torch.randn(steps + args.warmup, B, HQ, 1, D, device=dev, generator=g).half()
     scale = 1.0 / math.sqrt(D)
+    # a step = attentionWithCacheUpdate's decode step: appendDecode (append +
+    # score in one launch, then select + attend + combine)
     for i in range(args.warmup):
-        cache.append(kn[i], vn[i])
-        cache.decode(qs[i], scale)
+        cache.appendDecode(kn[i], vn[i], qs[i], scale)
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, args.warmup + steps):
+        cache.appendDecode(kn[i], vn[i], qs[i], scale)
+    torch.cuda.synchronize()
+    us_step = (time.perf_counter() - t0) * 1e6 / steps
+    # the same steps as two calls (append, then decode)
+    cache.trim(steps, list(range(B)))
     t0 = time.perf_counter()
     for i in range(args.warmup, args.warmup + steps):
         cache.append(kn[i], vn[i])
         cache.decode(qs[i], scale)
     torch.cuda.synchronize()
-    us_step = (time.perf_counter() - t0) * 1e6 / steps
+    us_two = (time.perf_counter() - t0) * 1e6 / steps
+    log(f"[bench] c4: {us_step:.2f} us/step (appendDecode), {us_two:.2f} (append + decode)")
     # kernel time per step: the same steps again (trimmed back first), profiled
     cache.trim(steps, list(range(B)))
     cache.profile(True)
     for i in range(args.warmup, args.warmup + steps):
-        cache.append(kn[i], vn[i])
-        cache.decode(qs[i], scale)
+        cache.appendDecode(kn[i], vn[i], qs[i], scale)
     torch.cuda.synchronize()
     kern = {}
     total = 0.0
     names = {"append": bsattn._lib.KERNEL_APPEND, "summary": bsattn._lib.KERNEL_SUMMARY,
-             "score": bsattn._lib.KERNEL_SCORE, "topk": bsattn._lib.KERNEL_TOPK,
+             "append+score": bsattn._lib.KERNEL_SCORE, "topk": bsattn._lib.KERNEL_TOPK,
              "attend": bsattn._lib.KERNEL_ATTEND, "combine": bsattn._lib.KERNEL_COMBINE}
     for name, kind in names.items():
         ms, n = cache.profileRead(kind)
@@ -545,7 +568,9 @@ def bench_loop(args):
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
                    "lengths": [int(x) for x in lens], "block_size": TB, "top_k": K,
                    "sink_blocks": 1, "recent_blocks": 1, "pages": pages,
-                   "timing": "eager wall clock per step (ctypes launches included)"},
+                   "timing": "eager wall clock per step (ctypes launches included)",
+                   "step_call": "appendDecode (append + scoring in one launch)"},
+        "two_calls_us_per_step": round(us_two, 3),
         "kernels_us_per_step": kern, "kernel_us_per_step_total": round(total, 3),
         "graph_us_per_step": round(us_graph, 3),
         "graph_step_us_distribution": dist,

@@ -135,6 +135,18 @@ int bsattn_decode(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
                   int32_t n_seqs, float scale, void* out, int32_t* idx_out,
                   void* stream);
 
+/* One decode step of attentionWithCacheUpdate (AttentionUtils.swift:37-77
+ * with L = 1: cache.update(keys:values:), KVCache.swift:328-371, then the
+ * decode attention, AttentionUtils.swift:68-75) in one call: appends one
+ * token per listed sequence (k, v [n_seqs, Hkv, 1, D]) and decodes q
+ * [n_seqs, Hq, 1, D] over the caches that now hold it -> out; idx_out as
+ * in bsattn_decode.  Same results, bit for bit, as bsattn_append followed
+ * by bsattn_decode; on a 16-bit cache the append and the block scoring
+ * share one launch. */
+int bsattn_append_decode(bsattn_cache* cache, const void* k, const void* v,
+                         const void* q, const int32_t* seq_ids, int32_t n_seqs,
+                         float scale, void* out, int32_t* idx_out, void* stream);
+
 /* Decode of n_query (1..16) query tokens per sequence whose n_query keys /
  * values were appended last: the speculative-verify pass of
  * Evaluate.swift:862-870 (L = numDraft + 1 under a causal mask).  q / out

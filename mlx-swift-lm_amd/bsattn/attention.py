@@ -31,8 +31,7 @@ def attentionWithCacheUpdate(queries: torch.Tensor, keys: torch.Tensor, values: 
     if L == 1:
         if mask not in ("none", None):
             raise ValueError("decode (L == 1) takes no mask (BaseKVCache.makeMask returns .none)")
-        cache.append(keys, values)
-        return cache.decode(queries, scale)
+        return cache.appendDecode(keys, values, queries, scale)
     if mask != "causal":
         raise ValueError("a multi-token pass takes the causal mask (BaseKVCache.makeMask(n > 1))")
     cache.append(keys, values)

@@ -298,6 +298,32 @@ class BlockSparseKVCache:
                                   ctypes.c_float(scale), _ptr(out), idx_p, _stream(self.device)))
         return out
 
+    def appendDecode(self, keys: torch.Tensor, values: torch.Tensor, queries: torch.Tensor,
+                     scale: float, seq_ids: Optional[Sequence[int]] = None,
+                     idx_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One decode step (attentionWithCacheUpdate with L = 1): appends
+        keys / values [B, Hkv, 1, D] and decodes queries [B, Hq, 1, D] over
+        the caches that now hold them; the same results as append() then
+        decode(), with the append and the block scoring in one launch where
+        the cache allows it."""
+        self._check_kv(keys, "keys")
+        self._check_kv(values, "values")
+        if keys.shape != values.shape or keys.shape[2] != 1:
+            raise ValueError("keys and values must both be [B, Hkv, 1, D]")
+        B = self._check_q(queries)
+        if keys.shape[0] != B:
+            raise ValueError("keys / values and queries disagree on B")
+        out = torch.empty_like(queries)
+        idx_p = None
+        if idx_out is not None:
+            if idx_out.dtype != torch.int32 or tuple(idx_out.shape) != (B, self.desc.num_kv_heads, self.nselMax):
+                raise ValueError("idx_out must be int32 [B, Hkv, nselMax]")
+            idx_p = _ptr(idx_out)
+        check(lib().bsattn_append_decode(self._h, _ptr(keys), _ptr(values), _ptr(queries),
+                                         i32_array(seq_ids), B, ctypes.c_float(scale), _ptr(out),
+                                         idx_p, _stream(self.device)))
+        return out
+
     def decodeMulti(self, queries: torch.Tensor, scale: float,
                     seq_ids: Optional[Sequence[int]] = None,
                     idx_out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -645,6 +645,67 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
                      (hipStream_t)stream);
 }
 
+int bsattn_append_decode(bsattn_cache* c, const void* k, const void* v, const void* q,
+                         const int32_t* seq_ids, int32_t n_seqs, float scale, void* out,
+                         int32_t* idx_out, void* stream) {
+  if (!c || !k || !v || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(c)) return rs;
+  std::vector<int32_t> seqs;
+  int rc = seq_list(c, seq_ids, n_seqs, seqs);
+  if (rc) return rc;
+  const Geometry& g = c->geo;
+  const int tb = c->d.block_size;
+  int max_nc = 0;
+  // (create requires recent_blocks >= 1: the block a token completes is never scored)
+  bool one_launch = c->d.kv_bits == 0 && n_seqs <= kMaxBatch;
+  for (int sq : seqs) {
+    if ((int64_t)c->len[sq] + 1 > (int64_t)c->d.max_blocks_per_seq * tb) one_launch = false;
+    else max_nc = std::max(max_nc, candidates(g, c->len[sq] + 1));
+  }
+  one_launch = one_launch && max_nc <= fused_select_limit(g.top_k);
+  if (!one_launch) {
+    rc = bsattn_append(c, k, v, seq_ids, n_seqs, 1, stream);
+    if (rc) return rc;
+    return bsattn_decode(c, q, seq_ids, n_seqs, scale, out, idx_out, stream);
+  }
+  DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
+  hipStream_t s = (hipStream_t)stream;
+  std::vector<std::pair<int32_t, int32_t>> patches;
+  rc = reserve_pages(c, seqs, 1, patches);
+  if (rc) return rc;
+  for (int sq : seqs) patches.emplace_back(sq, c->len[sq] + 1);
+  if (patches.size() > (size_t)kMaxPatch) {  // applied by a launch of their own
+    rc = flush_patches(c, patches, s);
+    if (rc) return rc;
+  }
+  PatchBatch pb{};
+  pb.n = (int32_t)patches.size();
+  for (int i = 0; i < pb.n; ++i) {
+    pb.idx[i] = patches[i].first;
+    pb.val[i] = patches[i].second;
+  }
+  SeqBatch b{};
+  StepPages sp{};
+  b.n = n_seqs;
+  b.qhs = kHeadDim;
+  for (int i = 0; i < n_seqs; ++i) {
+    const int sq = seqs[i];
+    b.ids[i] = sq;
+    b.len[i] = c->len[sq] + 1;
+    b.qoff[i] = (int32_t)((int64_t)i * g.hq * kHeadDim);
+    sp.page[i] = c->pages[sq][c->len[sq] / tb];
+  }
+  Timing tm[kProfKinds];
+  Timing* prof = prof_slots(c, s, tm);
+  hipError_t e = launch_append_decode(g, b, sp, pb, k, v, q, c->scores, idx_out, max_nc, scale, out,
+                                     c->partials, s, prof);
+  prof_collect(c, prof);
+  if (e != hipSuccess) return hip_fail(e, "append-decode launch");
+  for (int sq : seqs) c->len[sq] += 1;
+  return BSATTN_OK;
+}
+
 int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
                         int32_t n_query, float scale, void* out, int32_t* idx_out, void* stream) {
   if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");

@@ -821,12 +821,11 @@ __device__ __forceinline__ int given_index(const Geometry& geo, const int32_t* _
 
 template <int TB, int W, int SEL>
 __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, int seq, int len,
-                                            int split, int wave, int lane,
+                                            int slot, bool first, int wave, int lane,
                                             int32_t* __restrict__ idx, int jg,
                                             const WaveCand* wc, const WgCand* wgc, int* s_sel,
                                             int* s_selp, uint32_t* s_ws, int& j_out,
                                             int& page_out) {
-  const int slot = split * W + wave;
   int j = -1, page = -1;
   if constexpr (SEL) {
     const int nb = len > 0 ? (len + TB - 1) / TB : 0;
@@ -848,7 +847,7 @@ __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, 
         page = s_selp[slot - geo.ns];
       }
     }
-    if (idx != nullptr && split == 0 && wave == 0) {
+    if (idx != nullptr && first) {
       int32_t* row = idx + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
       for (int p = lane; p < geo.nsel_max; p += 64)
         row[p] = selected_block(p, nb, ranked, geo.ns, geo.nr, K, s_sel);

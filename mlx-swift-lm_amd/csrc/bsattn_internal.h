@@ -75,6 +75,11 @@ struct PatchBatch {
   int32_t val[kMaxPatch];
 };
 
+// page of the block that receives entry i's new token (launch_append_decode)
+struct StepPages {
+  int32_t page[kMaxBatch];
+};
+
 // Opt-in per-kernel profiling: a launcher given a Timing array records the
 // start/stop events of slot `kind` around that kernel's dispatch (when the
 // slot's events are set) and marks the slot used.
@@ -134,6 +139,18 @@ int fused_select_limit(int top_k);
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                          int32_t* idx_out, int max_nc, float scale, void* out,
                          float* partials, hipStream_t s, Timing* prof);
+hipError_t launch_decode_attend(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                                int32_t* idx_out, int max_nc, float scale, void* out,
+                                float* partials, hipStream_t s, Timing* prof);
+// one decode step of a 16-bit cache with one new token per entry (b.len =
+// the lengths after it): the patches pb, the appends (k / v [n, Hkv, 1, D]
+// into the pages sp) and the scoring in one launch, then the selection +
+// attention (+ combine) launches of launch_decode.  Requires max_nc <=
+// fused_select_limit(top_k) (and recent >= 1, which every cache has).
+hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
+                                const PatchBatch& pb, const void* k, const void* v, const void* q,
+                                float* scores, int32_t* idx_out, int max_nc, float scale,
+                                void* out, float* partials, hipStream_t s, Timing* prof);
 // dense causal attention of the last L tokens of each sequence
 hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
                           void* out, hipStream_t s, Timing* prof);

@@ -63,30 +63,25 @@ __device__ __forceinline__ void summary16(const Geometry& geo, const uint16_t* _
 // fold the block in token order from LDS, as summary16 does from memory.
 // grid (ceil(L/16), Hkv, n)
 // ---------------------------------------------------------------------------
+// Body of one append workgroup: tokens blockIdx.x * 16 .. +15 of entry bi,
+// kv head h, starting at position base.  page_given >= 0 is the page of the
+// (single) token's block, passed by a caller that patches the block table in
+// the same launch; otherwise the page is read from the block table.
 template <int DT>
-__global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
-                                                const uint16_t* __restrict__ k,
-                                                const uint16_t* __restrict__ v, bool fuse_summary,
-                                                bool device_len) {
-  __shared__ u32x4 s_blk[64][16];  // the filled block's keys, [token][8-dim chunk]
-  const int bi = blockIdx.z, h = blockIdx.y;
+__device__ __forceinline__ void append_body(const Geometry& geo, int seq, int bi, int h, int L,
+                                            int base, int page_given,
+                                            const uint16_t* __restrict__ k,
+                                            const uint16_t* __restrict__ v, bool fuse_summary,
+                                            u32x4 (*s_blk)[16]) {
   const int tg = threadIdx.x >> 4, c = threadIdx.x & 15;
   const int tok = blockIdx.x * 16 + tg;
-  const int seq = ab.seq[bi];
-  // device_len: the position is the device-side length (one token; a
-  // sequence without a reserved page for it takes nothing)
-  int base = ab.old_len[bi];
-  if (device_len) {
-    base = geo.meta[seq];
-    if (base >= geo.meta[geo.cap_off + seq]) return;
-  }
   const int32_t* bt = block_table(geo, seq);
   u32x4 kr = u32x4{0u, 0u, 0u, 0u};
-  if (tok < ab.L) {
+  if (tok < L) {
     const int pos = base + tok;
     const int blk = pos / geo.tb, slot = pos - blk * geo.tb;
-    const int page = bt[blk];
-    const size_t src = (((size_t)bi * geo.hkv + h) * ab.L + tok) * kHeadDim + 8 * c;
+    const int page = page_given >= 0 ? page_given : bt[blk];
+    const size_t src = (((size_t)bi * geo.hkv + h) * L + tok) * kHeadDim + 8 * c;
     kr = *(const u32x4*)(k + src);
     const u32x4 vr = *(const u32x4*)(v + src);
     uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
@@ -104,7 +99,7 @@ __global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
   // the workgroup's token 0 (the only one) fills its block: uniform branch
   const int blk = base / geo.tb;
   if (base - blk * geo.tb != geo.tb - 1) return;
-  const int page = bt[blk];
+  const int page = page_given >= 0 ? page_given : bt[blk];
   const uint16_t* Kt =
       (const uint16_t*)(geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes + geo.k_off);
   // keys 0 .. Tb-2 were written by earlier launches; key Tb-1 is kr of tg 0
@@ -126,6 +121,24 @@ __global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
   for (int e = 0; e < 4; ++e)
     o[e] = pack2<DT>(__fmul_rn(acc[2 * e], inv), __fmul_rn(acc[2 * e + 1], inv));
   *(u32x4*)(summary_row(geo, seq, h, blk) + 8 * c) = o;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_append(Geometry geo, AppendBatch ab,
+                                                const uint16_t* __restrict__ k,
+                                                const uint16_t* __restrict__ v, bool fuse_summary,
+                                                bool device_len) {
+  __shared__ u32x4 s_blk[64][16];  // the filled block's keys, [token][8-dim chunk]
+  const int bi = blockIdx.z, h = blockIdx.y;
+  const int seq = ab.seq[bi];
+  // device_len: the position is the device-side length (one token; a
+  // sequence without a reserved page for it takes nothing)
+  int base = ab.old_len[bi];
+  if (device_len) {
+    base = geo.meta[seq];
+    if (base >= geo.meta[geo.cap_off + seq]) return;
+  }
+  append_body<DT>(geo, seq, bi, h, ab.L, base, -1, k, v, fuse_summary, s_blk);
 }
 
 // ---------------------------------------------------------------------------
@@ -154,12 +167,11 @@ __global__ __launch_bounds__(64) void k_summary(Geometry geo, SummaryBatch sb) {
 // workgroups, half the serial work per thread).  grid (chunks, Hkv, n)
 // ---------------------------------------------------------------------------
 template <int DT, int G, int CH>
-__global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
-                                               const uint16_t* __restrict__ q,
-                                               float* __restrict__ scores) {
+__device__ __forceinline__ void score_body(const Geometry& geo, const SeqBatch& sb,
+                                           const uint16_t* __restrict__ q,
+                                           float* __restrict__ scores, int chunk, int h, int bi) {
   constexpr int P = CH / 16;
   const int tid = threadIdx.x;
-  const int chunk = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int seq = sb.ids[bi];
   const int c = tid & 15;
   const int j0 = geo.ns + chunk * CH + (tid >> 4);
@@ -195,6 +207,41 @@ __global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
       if (c == 0) srow[j] = best;
     }
   }
+}
+
+template <int DT, int G, int CH>
+__global__ __launch_bounds__(256) void k_score(Geometry geo, SeqBatch sb,
+                                               const uint16_t* __restrict__ q,
+                                               float* __restrict__ scores) {
+  score_body<DT, G, CH>(geo, sb, q, scores, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// ---------------------------------------------------------------------------
+// One decode step's append and scoring in one launch (attentionWithCacheUpdate
+// with one new token per sequence): workgroups x = 0 append entry bi's token
+// to kv head h (writing the summary of the block it completes), the rest
+// score candidate chunk x - 1.  The host patches of this step (lengths,
+// capacities, table entries of new pages) are applied here by workgroup
+// (0, 0, 0) for the launches that follow; nothing in this launch reads them:
+// the append takes its position and page from the arguments, the scoring
+// takes each entry's length from sb, and the block an append completes is
+// the newest block, which is forced (recent >= 1) and never scored.
+// grid (chunks + 1, Hkv, n)
+// ---------------------------------------------------------------------------
+template <int DT, int G, int CH>
+__global__ __launch_bounds__(256) void k_append_score(Geometry geo, SeqBatch sb, StepPages sp,
+                                                      PatchBatch pb, const uint16_t* __restrict__ k,
+                                                      const uint16_t* __restrict__ v,
+                                                      const uint16_t* __restrict__ q,
+                                                      float* __restrict__ scores) {
+  __shared__ u32x4 s_blk[64][16];
+  const int h = blockIdx.y, bi = blockIdx.z;
+  if (blockIdx.x == 0) {
+    if (h == 0 && bi == 0 && (int)threadIdx.x < pb.n) geo.meta[pb.idx[threadIdx.x]] = pb.val[threadIdx.x];
+    append_body<DT>(geo, sb.ids[bi], bi, h, 1, sb.len[bi] - 1, sp.page[bi], k, v, true, s_blk);
+    return;
+  }
+  score_body<DT, G, CH>(geo, sb, q, scores, blockIdx.x - 1, h, bi);
 }
 
 // ---------------------------------------------------------------------------
@@ -266,9 +313,10 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int seq = sb.ids[bi];
+  const int slot = split * W + wave;
   // given indices: the slot's block index heads the longest dependent chain
   // (index -> page -> K/V), so it is requested before the length and Q
-  const int jg = SEL ? -1 : given_index(geo, idx, bi, h, split * W + wave);
+  const int jg = SEL ? -1 : given_index(geo, idx, bi, h, slot);
   u32x4 qf[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
@@ -291,8 +339,8 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   }
   const int len = uniform(entry_len(geo, sb, bi, seq));
   int j, page;
-  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, jg, &wc, &wgc, s_sel, s_selp, s_ws, j,
-                          page);
+  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, slot, split == 0 && wave == 0, wave, lane, idx, jg, &wc,
+                          &wgc, s_sel, s_selp, s_ws, j, page);
   if (j >= 0) {
     const int valid = min(TB, len - j * TB);
     const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
@@ -527,6 +575,21 @@ static void score_dispatch(const Geometry& g, const SeqBatch& b, int max_nc, con
   }
 }
 
+template <int DT, int CH>
+static void append_score_dispatch(const Geometry& g, const SeqBatch& b, const StepPages& sp,
+                                  const PatchBatch& pb, int chunks, const uint16_t* k,
+                                  const uint16_t* v, const uint16_t* q, float* sc, hipStream_t s,
+                                  Timing* prof) {
+  const dim3 grid(chunks + 1, g.hkv, b.n), blk(256);
+  switch (g.group) {
+    case 1: launch(k_append_score<DT, 1, CH>, grid, blk, 0, s, prof, kProfScore, g, b, sp, pb, k, v, q, sc); break;
+    case 2: launch(k_append_score<DT, 2, CH>, grid, blk, 0, s, prof, kProfScore, g, b, sp, pb, k, v, q, sc); break;
+    case 4: launch(k_append_score<DT, 4, CH>, grid, blk, 0, s, prof, kProfScore, g, b, sp, pb, k, v, q, sc); break;
+    case 8: launch(k_append_score<DT, 8, CH>, grid, blk, 0, s, prof, kProfScore, g, b, sp, pb, k, v, q, sc); break;
+    default: launch(k_append_score<DT, 16, CH>, grid, blk, 0, s, prof, kProfScore, g, b, sp, pb, k, v, q, sc); break;
+  }
+}
+
 int candidates(const Geometry& g, int len) {
   const int nb = len > 0 ? (len + g.tb - 1) / g.tb : 0;
   return nb - g.nr - g.ns;
@@ -621,11 +684,9 @@ int fused_select_limit(int top_k) {
   return top_k <= kSelMaxK ? 64 * std::max(kWaves * kWgKeys, kSelKeysPerLane) : 0;
 }
 
-hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                         int32_t* idx_out, int max_nc, float scale, void* out,
-                         float* partials, hipStream_t s, Timing* prof) {
-  hipError_t e = score_exact(g, b, q, scores, max_nc, s, prof);
-  if (e != hipSuccess) return e;
+hipError_t launch_decode_attend(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                                int32_t* idx_out, int max_nc, float scale, void* out,
+                                float* partials, hipStream_t s, Timing* prof) {
   // every wave of the workgroup takes a share of the candidates (measured
   // faster than one wave selecting, also for 510 candidates: the per-key
   // work of each pass shrinks W-fold for a few workgroup barriers); with
@@ -633,6 +694,35 @@ hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, fl
   if (max_nc <= 64 * kWaves * kWgKeys)
     return attend_impl<2>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
   return attend_impl<1>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
+}
+
+hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
+                         int32_t* idx_out, int max_nc, float scale, void* out,
+                         float* partials, hipStream_t s, Timing* prof) {
+  hipError_t e = score_exact(g, b, q, scores, max_nc, s, prof);
+  if (e != hipSuccess) return e;
+  return launch_decode_attend(g, b, q, scores, idx_out, max_nc, scale, out, partials, s, prof);
+}
+
+hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
+                                const PatchBatch& pb, const void* k, const void* v, const void* q,
+                                float* scores, int32_t* idx_out, int max_nc, float scale,
+                                void* out, float* partials, hipStream_t s, Timing* prof) {
+  // the scoring chunk size follows score_exact
+  const bool small = (int64_t)((max_nc + 63) / 64) * g.hkv * b.n < 1024;
+  const int ch = small ? 32 : 64;
+  const int chunks = ranked_select(g, max_nc) ? (max_nc + ch - 1) / ch : 0;
+  const uint16_t *kk = (const uint16_t*)k, *vv = (const uint16_t*)v, *qq = (const uint16_t*)q;
+  if (g.dtype == 0) {
+    if (small) append_score_dispatch<0, 32>(g, b, sp, pb, chunks, kk, vv, qq, scores, s, prof);
+    else append_score_dispatch<0, 64>(g, b, sp, pb, chunks, kk, vv, qq, scores, s, prof);
+  } else {
+    if (small) append_score_dispatch<1, 32>(g, b, sp, pb, chunks, kk, vv, qq, scores, s, prof);
+    else append_score_dispatch<1, 64>(g, b, sp, pb, chunks, kk, vv, qq, scores, s, prof);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_decode_attend(g, b, q, scores, idx_out, max_nc, scale, out, partials, s, prof);
 }
 
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out, void* v_out,

@@ -315,8 +315,8 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
   }
   const int len = uniform(entry_len(geo, sb, bi, seq));
   int j, page;
-  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split, wave, lane, idx, jg, &wc, &wgc, s_sel, s_selp, s_ws, j,
-                          page);
+  attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split * W + wave, split == 0 && wave == 0, wave, lane,
+                          idx, jg, &wc, &wgc, s_sel, s_selp, s_ws, j, page);
   if (j >= 0) {
     const int valid = min(TB, len - j * TB);
     const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;

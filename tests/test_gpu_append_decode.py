@@ -1,0 +1,92 @@
+"""bsattn_append_decode (the decode step of attentionWithCacheUpdate in one
+call) against bsattn_append followed by bsattn_decode on a deep copy of the
+same cache: outputs and selected blocks bit-identical at every step, across
+block fills (the summary is written in the launch that also scores), new
+pages, ragged lengths with interleaved pages, a reordered subset of the
+sequences, GQA 4 / 8 / 16, and the affine int4 cache (which takes the two
+calls); after the last step also against the oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from common import (Workload, fill, from_dev, log, make_workload, new_cache, oracle_decode,
+                    output_error, to_dev)
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+# dtype, Tb, Hq, Hkv, top_k, sink, recent, kv_bits, starting lengths, steps, seq_ids
+CASES = {
+    "bf16-tb64-g4": ("bf16", 64, 32, 8, 4, 1, 1, 0, [100, 190, 64, 255], 70, None),
+    "f16-tb32-g8-subset": ("f16", 32, 32, 4, 3, 1, 2, 0, [31, 95, 200], 40, [2, 0]),
+    "f16-tb32-g16-recent4": ("f16", 32, 64, 4, 3, 1, 4, 0, [40, 300, 129], 40, None),
+    "int4": ("f16", 64, 32, 8, 2, 1, 1, 4, [100, 130], 30, None),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_append_decode_equals_append_then_decode(gpu, case):
+    import torch
+    dtype, Tb, Hq, Hkv, K, ns, nr, bits, lens0, steps, ids = CASES[case]
+    log(f"[append-decode] {case}")
+    B = len(lens0)
+    ids_l = list(range(B)) if ids is None else ids
+    total = [l + (steps if b in ids_l else 0) for b, l in enumerate(lens0)]
+    w = make_workload(4100, B=B, Hq=Hq, Hkv=Hkv, T=max(total), Tb=Tb, dtype=dtype, top_k=K,
+                      ns=ns, nr=nr, lens=total)
+    a = new_cache(w, kv_bits=bits)
+    w0 = Workload(w.seed, B, Hq, Hkv, w.D, Tb, dtype, lens0, K, ns, nr)
+    w0.keys = [w.keys[b][:, :lens0[b]] for b in range(B)]
+    w0.values = [w.values[b][:, :lens0[b]] for b in range(B)]
+    fill(a, w0, gpu, chunk=40)
+    b_ = a.copy()
+    q = to_dev(w.q[ids_l][:, :, None, :], dtype, gpu)
+    nsel = ns + nr + K
+    cur = list(lens0)
+    for s in range(steps):
+        for b in ids_l:
+            cur[b] += 1
+        k = np.stack([w.keys[b][:, cur[b] - 1:cur[b]] for b in ids_l])
+        v = np.stack([w.values[b][:, cur[b] - 1:cur[b]] for b in ids_l])
+        kd, vd = to_dev(k, dtype, gpu), to_dev(v, dtype, gpu)
+        ia = torch.empty((len(ids_l), Hkv, nsel), dtype=torch.int32, device=gpu)
+        ib = torch.empty_like(ia)
+        out_a = a.appendDecode(kd, vd, q, w.scale, seq_ids=ids, idx_out=ia)
+        b_.append(kd, vd, seq_ids=ids)
+        out_b = b_.decode(q, w.scale, seq_ids=ids, idx_out=ib)
+        torch.cuda.synchronize()
+        assert np.array_equal(ia.cpu().numpy(), ib.cpu().numpy()), f"step {s}: selected blocks differ"
+        assert np.array_equal(from_dev(out_a), from_dev(out_b)), f"step {s}: outputs differ"
+    for b in range(B):
+        assert a.seqLen(b) == b_.seqLen(b) == cur[b]
+    if bits == 0:
+        for b in ids_l:
+            assert np.array_equal(from_dev(a.exportSummaries(b)), from_dev(b_.exportSummaries(b)))
+        wl = Workload(w.seed, len(ids_l), Hq, Hkv, w.D, Tb, dtype, [cur[b] for b in ids_l], K, ns, nr)
+        wl.q = w.q[ids_l]
+        wl.keys = [w.keys[b][:, :cur[b]] for b in ids_l]
+        wl.values = [w.values[b][:, :cur[b]] for b in ids_l]
+        idx_ref, out_ref = oracle_decode(wl)
+        assert np.array_equal(ia.cpu().numpy(), idx_ref), "selected blocks differ from the oracle"
+        got = O.to_f32(from_dev(out_a).reshape(len(ids_l), Hq, w.D), dtype).astype(np.float64)
+        err = output_error(got, out_ref, dtype)
+        assert err <= 2e-3, f"output error {err:.3g}"
+        log(f"[append-decode] {case} err={err:.3g}")
+
+
+def test_append_decode_errors(gpu):
+    """Shape / range errors are reported, and nothing is appended."""
+    import torch
+    w = make_workload(4200, B=2, Hq=32, Hkv=8, T=130, Tb=64, dtype="f16", top_k=1, lens=[130, 130])
+    c = new_cache(w, mbps=3)
+    fill(c, w, gpu)
+    k = torch.zeros((2, 8, 1, 128), dtype=torch.float16, device=gpu)
+    q = torch.zeros((2, 32, 1, 128), dtype=torch.float16, device=gpu)
+    with pytest.raises(ValueError):
+        c.appendDecode(k[:1], k[:1], q, 0.1)
+    c.appendDecode(k, k, q, 0.1)   # 131 tokens: the third block
+    with pytest.raises(Exception):
+        for _ in range(64):        # the 193rd token needs a fourth block
+            c.appendDecode(k, k, q, 0.1)
+    assert c.seqLen(0) == 192 and c.seqLen(1) == 192
