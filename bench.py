@@ -39,6 +39,9 @@ profiling hook); algorithmic bytes per launch = selected K+V bytes (codes and
 scales / biases for quantized caches) + q + out + indices.
 cpu_baseline: the CPU oracle (single thread) doing the same layer-step
 (score given summaries, select, attend) on layer 0's data.
+cpu_dense_reference_path: what the reference's own decode path computes on
+the CPU for that layer (dense attention over every cached token, float32
+numpy with multi-threaded BLAS; the thread count is reported).
 """
 from __future__ import annotations
 
@@ -216,6 +219,51 @@ def cpu_baseline(cfg: Config, cache, q, seconds):
         times.append(time.perf_counter() - t0)
     times.sort()
     return times[len(times) // 2] * 1e6, len(times)
+
+
+def cpu_dense(cfg: Config, cache, q, seconds):
+    """What the reference's decode path computes on the CPU for the same
+    layer: dense attention of each query over every cached token
+    (attentionWithCacheUpdate's SDPA, or quantizedScaledDotProductAttention
+    over the dequantized cache), float32 numpy with its multi-threaded BLAS.
+    Sample: sequence 0 of layer 0 (all kv heads), scaled by the batch;
+    returns (us per layer-step, repetitions, BLAS threads)."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_info
+    G, scale = cfg.G, 1.0 / math.sqrt(D)
+    if cfg.bits:
+        (kw, ks, kb), (vw, vs, vb) = cache.exportQuantized([0])
+
+        def deq(w, sc, bi):
+            words = w[0].cpu().numpy().view(np.uint32)          # [Hkv, T, D*bits/32]
+            per = 32 // cfg.bits
+            sh = (np.arange(per, dtype=np.uint32) * cfg.bits)[None, None, None, :]
+            codes = ((words[..., None] >> sh) & ((1 << cfg.bits) - 1)).astype(np.float32) \
+                .reshape(words.shape[0], words.shape[1], D)
+            sc = sc[0].float().cpu().numpy()                    # [Hkv, T, D/64]
+            bi = bi[0].float().cpu().numpy()
+            return (codes.reshape(*codes.shape[:2], D // 64, 64) * sc[..., None] + bi[..., None]) \
+                .reshape(codes.shape).astype(np.float32)
+        K, V = deq(kw, ks, kb), deq(vw, vs, vb)
+    else:
+        k, v = cache.export([0])
+        K, V = k[0].float().cpu().numpy(), v[0].float().cpu().numpy()   # [Hkv, T, D]
+    qq = q[0, :, 0, :].float().cpu().numpy()                             # [Hq, D]
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        for h in range(cfg.HKV):
+            s_ = (qq[h * G:(h + 1) * G] @ K[h].T) * scale
+            s_ -= s_.max(axis=1, keepdims=True)
+            p_ = np.exp(s_)
+            p_ /= p_.sum(axis=1, keepdims=True)
+            _ = p_ @ V[h]
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    return times[len(times) // 2] * 1e6 * cfg.B, len(times), threads
 
 
 def recall_report(cfg: Config, cache, q, idx, seqs):
@@ -402,6 +450,7 @@ def bench_layers(args, cfg: Config):
         log(f"[bench] recall ({time.time() - t0:.0f}s): {recall}")
 
     cpu = None
+    cpu_dense_path = None
     if not args.no_cpu and args.cpu_seconds > 0:
         cpu_us, n = cpu_baseline(cfg, layers[0][0], layers[0][1], args.cpu_seconds)
         cpu = {"value": round(cpu_us, 1), "unit": "us/layer-step", "cores": 1, "kind": "port",
@@ -409,6 +458,13 @@ def bench_layers(args, cfg: Config):
                          f"tokens), oracle score+select+attend per (seq, kv head) given summaries, "
                          f"median of {n} layer-steps, 1 thread"}
         log(f"[bench] cpu oracle: {cpu_us:.0f} us/layer-step")
+        dense_us, nd, thr = cpu_dense(cfg, layers[0][0], layers[0][1], args.cpu_seconds)
+        cpu_dense_path = {"value": round(dense_us, 1), "unit": "us/layer-step", "cores": thr,
+                          "kind": "reference path (dense)",
+                          "sample": f"the reference's dense decode attention over all {cfg.T} cached tokens "
+                                    f"(float32 numpy + BLAS, {thr} threads) for sequence 0 of layer 0, "
+                                    f"median of {nd} repetitions, x{cfg.B} sequences"}
+        log(f"[bench] cpu dense (reference path): {dense_us:.0f} us/layer-step, {thr} threads")
 
     traffic, traffic_src = recorded_traffic(cfg)
     kv = cfg.dtype if cfg.bits == 0 else f"int{cfg.bits} affine, group 64, fp16 scale/bias"
@@ -444,6 +500,7 @@ def bench_layers(args, cfg: Config):
         "eager_us_per_layer_step": round(eager_ms * 1e3 / L, 3),
         "us_per_layer_step_distribution": dist,
         "cpu_baseline": cpu,
+        "cpu_dense_reference_path": cpu_dense_path,
     }
     if recall is not None:
         result["recall"] = recall

@@ -2,8 +2,8 @@
 reference's KVCache / attentionWithCacheUpdate API over libbsattn.so."""
 from ._lib import BsattnError, EXPORTS, LIB_PATH, lib
 from .attention import attentionWithCacheUpdate
-from .cache import BlockSparseKVCache
+from .cache import BlockSparseKVCache, maybeQuantizeKVCache
 from .prompt_cache import loadPromptCache, savePromptCache
 
 __all__ = ["BlockSparseKVCache", "BsattnError", "attentionWithCacheUpdate", "lib", "LIB_PATH",
-           "EXPORTS", "savePromptCache", "loadPromptCache"]
+           "EXPORTS", "savePromptCache", "loadPromptCache", "maybeQuantizeKVCache"]

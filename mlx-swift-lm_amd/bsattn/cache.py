@@ -445,6 +445,32 @@ class BlockSparseKVCache:
             return "array"
         return "causal"
 
+    def toQuantized(self, groupSize: int = 64, bits: int = 4) -> "BlockSparseKVCache":
+        """KVCacheSimple.toQuantized (KVCache.swift:407-427): a new cache of
+        the same geometry holding every sequence's tokens as MLX-affine
+        `bits`-bit codes with fp16 scales / biases (exported and quantized on
+        append, on the device), with the summaries of the dequantized keys.
+        Quantized caches hold fp16, so a bf16 cache's tokens are rounded to
+        fp16 first."""
+        if self.bits:
+            raise ValueError("toQuantized: the cache is already quantized")
+        d = self.desc
+        qc = BlockSparseKVCache(
+            max_seqs=d.max_seqs, num_q_heads=d.num_q_heads, num_kv_heads=d.num_kv_heads,
+            head_dim=d.head_dim, block_size=d.block_size, dtype=torch.float16, kv_bits=bits,
+            group_size=groupSize, top_k=d.top_k, sink_blocks=d.sink_blocks,
+            recent_blocks=d.recent_blocks, max_blocks_per_seq=d.max_blocks_per_seq,
+            num_pages=d.num_pages, device=self.device.index)
+        for s in range(d.max_seqs):
+            if self.seqLen(s) == 0:
+                continue
+            k, v = self.export([s])
+            if self.dtype != torch.float16:
+                k, v = k.half(), v.half()
+            qc.append(k, v, seq_ids=[s])
+            del k, v
+        return qc
+
     def copy(self) -> "BlockSparseKVCache":
         h = ctypes.c_void_p()
         check(lib().bsattn_copy(self._h, ctypes.byref(h), _stream(self.device)))
@@ -457,4 +483,21 @@ class BlockSparseKVCache:
             num_pages=d.num_pages, device=self.device.index, _handle=h)
 
 
-__all__ = ["BlockSparseKVCache", "BsattnError"]
+def maybeQuantizeKVCache(cache: list, kvBits: Optional[int], kvGroupSize: int = 64,
+                         quantizedKVStart: int = 0) -> None:
+    """maybeQuantizeKVCache (KVCache.swift:1637-1660), in place: once
+    cache[0] holds more than quantizedKVStart tokens, every 16-bit
+    BlockSparseKVCache in the list is replaced by its toQuantized(kvGroupSize,
+    kvBits); nothing happens when kvBits is None, the list is empty or
+    cache[0] is already quantized."""
+    if kvBits is None or not cache:
+        return
+    first = cache[0]
+    if not isinstance(first, BlockSparseKVCache) or first.bits != 0 or first.offset <= quantizedKVStart:
+        return
+    for i, c in enumerate(cache):
+        if isinstance(c, BlockSparseKVCache) and c.bits == 0:
+            cache[i] = c.toQuantized(groupSize=kvGroupSize, bits=kvBits)
+
+
+__all__ = ["BlockSparseKVCache", "BsattnError", "maybeQuantizeKVCache"]

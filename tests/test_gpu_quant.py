@@ -245,3 +245,58 @@ def test_quantized_decode_loop_with_appends(gpu):
             run_and_check_q(cache, w, gpu, 4, kq, vq)
     torch.cuda.synchronize()
     assert [cache.seqLen(b) for b in range(w.B)] == full_lens
+
+
+@pytest.mark.parametrize("bits,Tb,dtype", [(4, 64, "f16"), (8, 32, "f16"), (4, 64, "bf16")])
+def test_to_quantized(gpu, bits, Tb, dtype):
+    """toQuantized (KVCacheSimple.toQuantized): a 16-bit cache (ragged
+    lengths, interleaved pages, one empty sequence) becomes a quantized cache
+    holding the same tokens: codes / scales / biases bit-exact against the
+    codec on the fp16 tokens (bf16 tokens rounded to fp16 first), lengths
+    kept, selection and outputs as the oracle's over the quantized tokens."""
+    import torch
+    lens = [Tb * 40 + 3, Tb * 9, Tb * 23 + 17, 0]
+    log(f"[to-quantized] bits={bits} Tb={Tb} {dtype}")
+    w = make_workload(3600 + bits + Tb, B=len(lens), Hq=32, Hkv=8, T=max(lens), Tb=Tb, dtype=dtype,
+                      top_k=5, ns=1, nr=2, lens=lens, salient_frac=0.01)
+    src = new_cache(w)
+    fill(src, w, gpu, chunk=3 * Tb + 1)
+    qc = src.toQuantized(groupSize=64, bits=bits)
+    assert qc.bits == bits and qc.dtype == torch.float16
+    assert [qc.seqLen(b) for b in range(w.B)] == lens
+    # the fp16 tokens the quantized cache holds
+    w16 = Workload(w.seed, w.B, w.Hq, w.Hkv, w.D, Tb, "f16", lens, w.top_k, w.ns, w.nr)
+    w16.q = w.q if dtype == "f16" else O.from_f32(O.to_f32(w.q, dtype), "f16")
+    conv = (lambda a: a) if dtype == "f16" else (lambda a: O.from_f32(O.to_f32(a, dtype), "f16"))
+    w16.keys = [conv(k) for k in w.keys]
+    w16.values = [conv(v) for v in w.values]
+    kq, vq = quantize_all(w16, bits)
+    check_storage(qc, w16, bits, kq, vq)
+    wd = Workload(w.seed, 3, w.Hq, w.Hkv, w.D, Tb, "f16", lens[:3], w.top_k, w.ns, w.nr)
+    wd.q, wd.keys, wd.values = w16.q[:3], w16.keys[:3], w16.values[:3]
+    err = run_and_check_q(qc, wd, gpu, bits, kq[:3], vq[:3])
+    log(f"[to-quantized] err={err:.3g}")
+
+
+def test_maybe_quantize_kv_cache(gpu):
+    """maybeQuantizeKVCache: nothing for kvBits None or offset <= start;
+    past the start every 16-bit cache of the list is replaced by its
+    quantized form (same tokens); an already quantized list is left alone."""
+    from bsattn import maybeQuantizeKVCache
+    lens = [300, 200]
+    w = make_workload(3700, B=2, Hq=32, Hkv=8, T=max(lens), Tb=64, dtype="f16", top_k=2, lens=lens)
+    caches = [new_cache(w) for _ in range(3)]
+    for c in caches:
+        fill(c, w, gpu)
+    before = list(caches)
+    maybeQuantizeKVCache(caches, None)
+    maybeQuantizeKVCache(caches, 4, quantizedKVStart=300)      # offset 300 is not > 300
+    assert all(a is b for a, b in zip(caches, before))
+    maybeQuantizeKVCache(caches, 4, kvGroupSize=64, quantizedKVStart=299)
+    assert all(c.bits == 4 and c is not b for c, b in zip(caches, before))
+    assert [caches[0].seqLen(b) for b in range(2)] == lens
+    again = list(caches)
+    maybeQuantizeKVCache(caches, 8, quantizedKVStart=0)
+    assert all(a is b for a, b in zip(caches, again))
+    kq, vq = quantize_all(w, 4)
+    check_storage(caches[2], w, 4, kq, vq)

@@ -127,6 +127,30 @@ def test_nonfinite_scores_select_like_oracle(gpu, T_blocks, Hq, Hkv, K):
     assert np.array_equal(idx2.cpu().numpy(), idx_ref)
 
 
+@pytest.mark.parametrize("dtype,Hq,Hkv,Tb,K,lo,hi,mult", [
+    ("f16", 64, 4, 32, 128, 500, 700, 4.0),     # the top blocks in three scoring chunks
+    ("bf16", 64, 4, 32, 128, 1000, 1128, 3.0),  # exactly K boosted blocks, side by side
+    ("f16", 32, 4, 64, 40, 10, 2000, 1.02),     # most blocks slightly boosted: the floor is low
+])
+def test_wide_group_clustered_top_blocks(gpu, dtype, Hq, Hkv, Tb, K, lo, hi, mult):
+    """Wide groups whose best blocks sit side by side: the wave floors of the
+    MFMA scoring then come from waves without any of them, and the candidates
+    kept for the compacted selection (or its fallback to all of them) must
+    still give the canonical selection."""
+    lens = [Tb * 3000 + 7, Tb * 2600]
+    w = make_workload(5600 + lo + K, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype=dtype,
+                      top_k=K, ns=1, nr=4, lens=lens)
+    for b in range(w.B):
+        for h in range(w.Hkv):
+            k = O.to_f32(w.keys[b][h], dtype)
+            k[lo * Tb:hi * Tb] *= mult
+            w.keys[b][h][:] = O.from_f32(k.astype(np.float32), dtype)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    err = check(cache, w, gpu)
+    log(f"[clustered] {dtype} G={Hq // Hkv} [{lo}, {hi}) x{mult} err={err:.3g}")
+
+
 @pytest.mark.parametrize("dtype,Hq,Hkv,Tb,K,scale", [
     ("f16", 64, 4, 32, 128, 1e-3), ("bf16", 32, 4, 64, 40, 1e-2), ("f16", 16, 4, 64, 32, 1e-3),
 ])
