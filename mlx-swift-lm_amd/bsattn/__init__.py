@@ -2,8 +2,9 @@
 reference's KVCache / attentionWithCacheUpdate API over libbsattn.so."""
 from ._lib import BsattnError, EXPORTS, LIB_PATH, lib
 from .attention import attentionWithCacheUpdate
-from .cache import BlockSparseKVCache, maybeQuantizeKVCache
+from .cache import BlockSparseKVCache, GenerateParameters, maybeQuantizeKVCache, newCache
 from .prompt_cache import loadPromptCache, savePromptCache
 
 __all__ = ["BlockSparseKVCache", "BsattnError", "attentionWithCacheUpdate", "lib", "LIB_PATH",
-           "EXPORTS", "savePromptCache", "loadPromptCache", "maybeQuantizeKVCache"]
+           "EXPORTS", "savePromptCache", "loadPromptCache", "maybeQuantizeKVCache", "newCache",
+           "GenerateParameters"]

@@ -15,6 +15,7 @@ computation runs in the HIP kernels of libbsattn.so.
 from __future__ import annotations
 
 import ctypes
+from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
 import torch
@@ -500,4 +501,36 @@ def maybeQuantizeKVCache(cache: list, kvBits: Optional[int], kvGroupSize: int = 
             cache[i] = c.toQuantized(groupSize=kvGroupSize, bits=kvBits)
 
 
-__all__ = ["BlockSparseKVCache", "BsattnError", "maybeQuantizeKVCache"]
+@dataclass
+class GenerateParameters:
+    """The cache fields of GenerateParameters (Evaluate.swift:64-73)."""
+    maxKVSize: Optional[int] = None
+    kvBits: Optional[int] = None
+    kvGroupSize: int = 64
+    quantizedKVStart: int = 0
+
+
+def newCache(kvHeads: Sequence[int], parameters: Optional[GenerateParameters] = None, *,
+             num_q_heads: int, max_seqs: int, max_tokens: int, dtype: torch.dtype = torch.bfloat16,
+             block_size: int = 64, top_k: int = 32, sink_blocks: int = 1, recent_blocks: int = 1,
+             device: int | torch.device = 0) -> List["BlockSparseKVCache"]:
+    """The block-sparse form of LanguageModel.newCache(parameters:)
+    (LanguageModel.swift:215-230): one cache per layer, layer i with
+    kvHeads[i] kv heads (the reference's KVCacheSimple ignores the head
+    count; a paged cache needs it), for up to max_seqs sequences of
+    max_tokens tokens.  As in the reference the caches start 16-bit even when
+    parameters.kvBits is set: maybeQuantizeKVCache converts them once
+    quantizedKVStart is passed.  A maxKVSize asks for the reference's
+    RotatingKVCache (a bounded window), which this cache does not replace."""
+    if parameters is not None and parameters.maxKVSize is not None:
+        raise ValueError("maxKVSize selects RotatingKVCache (KVCache.swift:445-578), which stays on "
+                         "the reference's dense path")
+    mbps = -(-max_tokens // block_size)
+    return [BlockSparseKVCache(max_seqs=max_seqs, num_q_heads=num_q_heads, num_kv_heads=h,
+                               block_size=block_size, dtype=dtype, top_k=top_k,
+                               sink_blocks=sink_blocks, recent_blocks=recent_blocks,
+                               max_blocks_per_seq=mbps, device=device) for h in kvHeads]
+
+
+__all__ = ["BlockSparseKVCache", "BsattnError", "GenerateParameters", "maybeQuantizeKVCache",
+           "newCache"]

@@ -351,3 +351,34 @@ def test_prompt_cache_round_trip(gpu, tmp_path, kv_bits):
     for (w, c), c2 in zip(layers, loaded):
         for a, b in zip(c.state, c2.state):
             assert torch.equal(a, b)
+
+
+def test_new_cache_per_layer_and_quantize_later(gpu):
+    """newCache (LanguageModel.newCache's block-sparse form): one cache per
+    layer with that layer's kv heads; attentionWithCacheUpdate steps every
+    layer (each against the oracle), and maybeQuantizeKVCache with the same
+    parameters converts the layers once quantizedKVStart is passed."""
+    import torch
+    import bsattn
+    params = bsattn.GenerateParameters(kvBits=4, kvGroupSize=64, quantizedKVStart=200)
+    layers = bsattn.newCache([8, 4], params, num_q_heads=32, max_seqs=2, max_tokens=1024,
+                             dtype=torch.float16, top_k=2, device=0)
+    assert [c.desc.num_kv_heads for c in layers] == [8, 4] and all(c.bits == 0 for c in layers)
+    for li, cache in enumerate(layers):
+        Hkv = cache.desc.num_kv_heads
+        w = make_workload(3900 + li, B=2, Hq=32, Hkv=Hkv, T=300, Tb=64, dtype="f16", top_k=2,
+                          lens=[300, 300])
+        prompt = Workload(w.seed, 2, 32, Hkv, w.D, 64, "f16", [299, 299], 2, 1, 1)
+        prompt.keys = [k[:, :299] for k in w.keys]
+        prompt.values = [v[:, :299] for v in w.values]
+        fill(cache, prompt, gpu)
+        k = to_dev(np.stack([kk[:, 299:300] for kk in w.keys]), "f16", gpu)
+        v = to_dev(np.stack([vv[:, 299:300] for vv in w.values]), "f16", gpu)
+        q = to_dev(w.q[:, :, None, :], "f16", gpu)
+        out = bsattn.attentionWithCacheUpdate(q, k, v, cache, w.scale)
+        torch.cuda.synchronize()
+        _, out_ref = oracle_decode(w)
+        got = O.to_f32(from_dev(out).reshape(2, 32, w.D), "f16").astype(np.float64)
+        assert output_error(got, out_ref, "f16") <= TOL
+    bsattn.maybeQuantizeKVCache(layers, params.kvBits, params.kvGroupSize, params.quantizedKVStart)
+    assert all(c.bits == 4 and c.seqLen(0) == 300 for c in layers)
