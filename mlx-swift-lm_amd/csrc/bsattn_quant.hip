@@ -38,17 +38,17 @@ __device__ __forceinline__ float hi_f(uint32_t w) { return h2f(w >> 16); }
 
 // A operand of QK token tile t, k-step s, from the tile's K fragments
 template <int KB>
-__device__ __forceinline__ u32x4 k_operand(const u32x4* kf, int s) {
-  if constexpr (KB == 4) return nib_to_f16(kf[0][s]);
+__device__ __forceinline__ u32x4 k_operand(const u32x4* kf, int s, uint32_t one) {
+  if constexpr (KB == 4) return nib_to_f16(kf[0][s], one);
   else return byte_to_f16(kf[s >> 1][2 * (s & 1)], kf[s >> 1][2 * (s & 1) + 1]);
 }
 
 // B operand of PV dim tile dt, k-step s2, from the V fragments
 template <int KB, int KS2>
-__device__ __forceinline__ u32x4 v_operand(const u32x4* vf, int dt, int s2) {
+__device__ __forceinline__ u32x4 v_operand(const u32x4* vf, int dt, int s2, uint32_t one) {
   constexpr int DPF = QCode<KB>::DPF;
   const u32x4& f = vf[(dt / DPF) * KS2 + s2];
-  if constexpr (KB == 4) return nib_to_f16(f[dt & 3]);
+  if constexpr (KB == 4) return nib_to_f16(f[dt & 3], one);
   else return byte_to_f16(f[2 * (dt & 1)], f[2 * (dt & 1) + 1]);
 }
 
@@ -336,6 +336,7 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
     for (int e = 0; e < EPL; ++e) sbv[e] = Sf[e];
     __builtin_amdgcn_sched_barrier(0);
     const u32x4 ones = u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+    const uint32_t one = f16_one_pair();
     // Q_g = sum of q over dim group g, for head n (every accumulator entry)
     f32x4 qs0 = mfma_f16(ones, qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
     qs0 = mfma_f16(ones, qf[1], qs0);
@@ -348,10 +349,10 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       f32x4 r0 = f32x4{0.f, 0.f, 0.f, 0.f}, r1 = r0;
-      r0 = mfma_f16(k_operand<KB>(kf[t], 0), qf[0], r0);
-      r0 = mfma_f16(k_operand<KB>(kf[t], 1), qf[1], r0);
-      r1 = mfma_f16(k_operand<KB>(kf[t], 2), qf[2], r1);
-      r1 = mfma_f16(k_operand<KB>(kf[t], 3), qf[3], r1);
+      r0 = mfma_f16(k_operand<KB>(kf[t], 0, one), qf[0], r0);
+      r0 = mfma_f16(k_operand<KB>(kf[t], 1, one), qf[1], r0);
+      r1 = mfma_f16(k_operand<KB>(kf[t], 2, one), qf[2], r1);
+      r1 = mfma_f16(k_operand<KB>(kf[t], 3, one), qf[3], r1);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const u32x4& f = sbv[4 * t + i];
@@ -412,7 +413,7 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
     for (int dt = 0; dt < 8; ++dt) {
       f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s2 = 0; s2 < KS2; ++s2) o = mfma_f16(dt < 4 ? pa0[s2] : pa1[s2], v_operand<KB, KS2>(vf, dt, s2), o);
+      for (int s2 = 0; s2 < KS2; ++s2) o = mfma_f16(dt < 4 ? pa0[s2] : pa1[s2], v_operand<KB, KS2>(vf, dt, s2, one), o);
       const f32x4& psg = dt < 4 ? ps0 : ps1;
       const f32x4& vbg = dt < 4 ? vb0 : vb1;
 #pragma unroll
