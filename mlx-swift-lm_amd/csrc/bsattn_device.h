@@ -917,21 +917,32 @@ __device__ __forceinline__ void attend_merge(const Geometry& geo, const SeqBatch
                                              uint16_t* __restrict__ out,
                                              float* __restrict__ partials) {
   const int nsplit = geo.nsplit;
-  for (int e = threadIdx.x; e < G * kHeadDim; e += 64 * W) {
-    const int head = e / kHeadDim, d = e % kHeadDim;
+  // per head: the maximum M over the waves, each wave's weight exp2(m_w - M)
+  // and the merged sum L, once (thread h < G), for all 128 dims
+  __shared__ float s_f[W][16], s_ML[2][16];
+  if (threadIdx.x < G) {
+    const int head = threadIdx.x;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][head]);
-    float L = 0.f, a = 0.f;
-    if (M != -INFINITY) {
+    float L = 0.f;
 #pragma unroll
-      for (int w = 0; w < W; ++w) {
-        const float mw = s_m[w][head];
-        const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-        L += f * s_l[w][head];
-        a += f * s_o[w][head][d];
-      }
+    for (int w = 0; w < W; ++w) {
+      const float mw = s_m[w][head];
+      const float f = (M == -INFINITY || mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+      s_f[w][head] = f;
+      L += f * s_l[w][head];
     }
+    s_ML[0][head] = M;
+    s_ML[1][head] = L;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < G * kHeadDim; e += 64 * W) {
+    const int head = e / kHeadDim, d = e % kHeadDim;
+    const float M = s_ML[0][head], L = s_ML[1][head];
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) a += s_f[w][head] * s_o[w][head][d];
     const size_t row = (size_t)bi * geo.hq + h * G + head;
     if (nsplit == 1) {
       out[q_row(sb, bi, h * G + head) + d] = from_f32<DT>(L > 0.f ? a / L : 0.f);
