@@ -537,7 +537,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
         float sv[8];
         unpack8<DT>(*(const u32x4*)(summary_row(geo, seq, h, j) + 8 * c), sv);
         float best = 0.0f;
-#pragma unroll 1
+#pragma unroll 4
         for (int gq = 0; gq < G; ++gq) {
           float qv[8];
           unpack8<DT>(*(const u32x4*)(qh + gq * kHeadDim + 8 * c), qv);
