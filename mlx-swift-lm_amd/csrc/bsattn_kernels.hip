@@ -603,10 +603,11 @@ static bool wave_selectable(const Geometry& g, int max_nc) {
 static hipError_t score_exact(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                               int max_nc, hipStream_t s, Timing* prof) {
   if (!ranked_select(g, max_nc)) return hipSuccess;
-  // 32-candidate chunks while the 64-candidate grid is under 1024 workgroups
-  // (8 sequences x 8 kv heads at 32k tokens: 512 -> 1024 workgroups, ~0.4 us
-  // faster; grids of thousands of workgroups are issue-bound and keep 64)
-  const bool small = (int64_t)((max_nc + 63) / 64) * g.hkv * b.n < 1024;
+  // 32-candidate chunks while the 64-candidate grid has at most 1024
+  // workgroups (8 sequences x 8 kv heads at 32k tokens: 512 -> 1024
+  // workgroups, ~0.4 us faster; grids of thousands of workgroups are
+  // issue-bound and keep 64)
+  const bool small = (int64_t)((max_nc + 63) / 64) * g.hkv * b.n <= 1024;
   const uint16_t* qq = (const uint16_t*)q;
   if (g.dtype == 0) {
     if (small) score_dispatch<0, 32>(g, b, max_nc, qq, scores, s, prof);
@@ -709,7 +710,7 @@ hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const Step
                                 float* scores, int32_t* idx_out, int max_nc, float scale,
                                 void* out, float* partials, hipStream_t s, Timing* prof) {
   // the scoring chunk size follows score_exact
-  const bool small = (int64_t)((max_nc + 63) / 64) * g.hkv * b.n < 1024;
+  const bool small = (int64_t)((max_nc + 63) / 64) * g.hkv * b.n <= 1024;
   const int ch = small ? 32 : 64;
   const int chunks = ranked_select(g, max_nc) ? (max_nc + ch - 1) / ch : 0;
   const uint16_t *kk = (const uint16_t*)k, *vv = (const uint16_t*)v, *qq = (const uint16_t*)q;
