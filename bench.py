@@ -32,13 +32,16 @@ Other workloads (one JSON line each, not the headline):
   --config mq  speculative verify at the default geometry: decodeMulti of 4
                query tokens per sequence, against 4 single-token decodes.
 
-roofline: the gather + attention kernel (k_attend / k_attend_q via
-bsattn_attend on precomputed indices), timed with HIP start/stop events
-attached to each of its dispatches on the launch stream (the library's
-profiling hook); algorithmic bytes per launch = selected K+V bytes (codes and
-scales / biases for quantized caches) + q + out + indices.
-cpu_baseline: the CPU oracle (single thread) doing the same layer-step
-(score given summaries, select, attend) on layer 0's data.
+roofline: the gather + attention kernel the decode step runs (k_attend /
+k_attend_q, with the top-K selection fused into it where the candidates
+allow), timed with HIP start/stop events attached to each of its dispatches
+on the launch stream (the library's profiling hook) during eager decode
+steps; algorithmic bytes per launch = selected K+V bytes (codes and scales /
+biases for quantized caches) + q + out + indices.  The same kernel on
+precomputed indices (bsattn_attend) is reported as roofline.given_index.
+cpu_baseline: the C oracle doing the same layer-step (score given
+summaries, select, attend) on layer 0's data, its (sequence, kv head) pairs
+over OMP_NUM_THREADS OpenMP threads; the CPU model is reported.
 cpu_dense_reference_path: what the reference's own decode path computes on
 the CPU for that layer (dense attention over every cached token, float32
 numpy with multi-threaded BLAS; the thread count is reported).
@@ -182,43 +185,49 @@ def host16(t, torch, np):
     return t.view(torch.int16).cpu().numpy().view(np.uint16)
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg: Config, cache, q, seconds):
-    """Oracle layer-step on layer 0's data: per (sequence, kv head) score all
-    candidate summaries, select, attend (over dequantized blocks for a
-    quantized cache).  Single thread; repeated for about `seconds`."""
+    """Oracle layer-step on layer 0's data: every (sequence, kv head) scores
+    its candidate summaries, selects, and attends (over dequantized blocks
+    for a quantized cache), the pairs spread over OMP_NUM_THREADS OpenMP
+    threads (the C oracle's orc_layer_step).  Repeated for about `seconds`;
+    returns (median us per layer-step, repetitions, threads, idx, out) with
+    the last repetition's results for the consistency check against the GPU."""
     import numpy as np
     import torch
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     ids = list(range(cfg.B))
+    kw = dict(keys=None, values=None, kq=None, vq=None)
     if cfg.bits:
-        (kw, ks, kb), (vw, vs, vb) = cache.exportQuantized(ids)
+        (k_w, k_s, k_b), (v_w, v_s, v_b) = cache.exportQuantized(ids)
         u32 = lambda t: t.cpu().numpy().view(np.uint32)
-        kq = (u32(kw), host16(ks, torch, np), host16(kb, torch, np))
-        vq = (u32(vw), host16(vs, torch, np), host16(vb, torch, np))
+        kw["kq"] = (u32(k_w), host16(k_s, torch, np), host16(k_b, torch, np))
+        kw["vq"] = (u32(v_w), host16(v_s, torch, np), host16(v_b, torch, np))
     else:
         k, v = cache.export(ids)
-        kh, vh = host16(k, torch, np), host16(v, torch, np)
+        kw["keys"], kw["values"] = host16(k, torch, np), host16(v, torch, np)
     qh = host16(q, torch, np).reshape(cfg.B, cfg.HQ, D)
-    summ = [host16(cache.exportSummaries(b), torch, np) for b in ids]
-    G, scale = cfg.G, 1.0 / math.sqrt(D)
+    summ = np.stack([host16(cache.exportSummaries(b), torch, np) for b in ids])
+    scale = 1.0 / math.sqrt(D)
     times = []
     t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(times) < 2:
         t0 = time.perf_counter()
-        for b in ids:
-            for h in range(cfg.HKV):
-                qq = qh[b, h * G:(h + 1) * G]
-                sc = O.score_blocks(qq, summ[b][h], cfg.dtype)
-                idx, n = O.select(sc, cfg.T, cfg.TB, cfg.ns, cfg.nr, cfg.top_k)
-                if cfg.bits:
-                    O.attend_q(qq, tuple(a[b, h] for a in kq), tuple(a[b, h] for a in vq), cfg.TB,
-                               cfg.bits, 64, idx[:n], scale)
-                else:
-                    O.attend(qq, kh[b, h], vh[b, h], cfg.TB, idx[:n], scale, cfg.dtype)
+        idx, out = O.layer_step(qh, summ, cfg.TB, cfg.ns, cfg.nr, cfg.top_k, scale, cfg.dtype,
+                                bits=cfg.bits, **kw)
         times.append(time.perf_counter() - t0)
     times.sort()
-    return times[len(times) // 2] * 1e6, len(times)
+    return times[len(times) // 2] * 1e6, len(times), O.omp_threads(), idx, out
 
 
 def cpu_dense(cfg: Config, cache, q, seconds):
@@ -413,9 +422,10 @@ def bench_layers(args, cfg: Config):
     for cache, _ in layers:
         cache.profile(False)
 
-    # roofline: the gather + attention kernel alone, on precomputed indices.
-    # Eager bsattn_attend calls with the library's profiling on: each kernel
-    # dispatch carries its own HIP start/stop events on the launch stream.
+    # the given-index gather + attention kernel alone (bsattn_attend on
+    # precomputed indices), for comparison with the decode path's kernel.
+    # Eager calls with the library's profiling on: each kernel dispatch
+    # carries its own HIP start/stop events on the launch stream.
     idx = [cache.selectBlocks(q) for cache, q in layers]
     torch.cuda.synchronize()
     nsel = int((idx[0] >= 0).sum(dim=2).max().item())
@@ -435,13 +445,20 @@ def bench_layers(args, cfg: Config):
         cms, _ = cache.profileRead(bsattn._lib.KERNEL_COMBINE)
         tot_ms, launches, comb_ms = tot_ms + ms, launches + n, comb_ms + cms
         cache.profile(False)
-    attend_us = tot_ms * 1e3 / launches
-    combine_us = comb_ms * 1e3 / launches
+    given_us = tot_ms * 1e3 / launches
+    given_combine_us = comb_ms * 1e3 / launches
     attn_bytes, summ_bytes = algorithmic_bytes(cfg, nsel)
+    given_achieved = attn_bytes / (given_us * 1e-6) / 1e9
+    # roofline: the gather + attention kernel the timed decode step runs
+    # (selection fused into it where the candidates allow), event-timed on
+    # its dispatches during the profiled decode steps above
+    attend_us = decode_kernels["attend"]
+    combine_us = decode_kernels.get("combine", 0.0)
     achieved = attn_bytes / (attend_us * 1e-6) / 1e9
     layer_bytes = attn_bytes + summ_bytes
-    log(f"[bench] attend kernel: {attend_us:.2f} us, {achieved:.0f} GB/s "
-        f"({100 * achieved / HBM_PEAK_GBPS:.1f}% of peak); combine {combine_us:.2f} us")
+    log(f"[bench] decode attend kernel: {attend_us:.2f} us, {achieved:.0f} GB/s "
+        f"({100 * achieved / HBM_PEAK_GBPS:.1f}% of peak); combine {combine_us:.2f} us; "
+        f"given-index attend {given_us:.2f} us ({100 * given_achieved / HBM_PEAK_GBPS:.1f}%)")
 
     recall = None
     if cfg.key == "c5" and not args.no_recall:
@@ -452,12 +469,17 @@ def bench_layers(args, cfg: Config):
     cpu = None
     cpu_dense_path = None
     if not args.no_cpu and args.cpu_seconds > 0:
-        cpu_us, n = cpu_baseline(cfg, layers[0][0], layers[0][1], args.cpu_seconds)
-        cpu = {"value": round(cpu_us, 1), "unit": "us/layer-step", "cores": 1, "kind": "port",
+        cpu_us, n, thr, cidx, _ = cpu_baseline(cfg, layers[0][0], layers[0][1], args.cpu_seconds)
+        same = bool((cidx == idx[0].cpu().numpy()).all())
+        cpu = {"value": round(cpu_us, 1), "unit": "us/layer-step", "cores": thr, "kind": "port",
+               "cpu_model": cpu_model(),
                "sample": f"layer 0 of the same workload ({cfg.B} seq x {cfg.HKV} kv heads x {cfg.T} "
-                         f"tokens), oracle score+select+attend per (seq, kv head) given summaries, "
-                         f"median of {n} layer-steps, 1 thread"}
-        log(f"[bench] cpu oracle: {cpu_us:.0f} us/layer-step")
+                         f"tokens): the C oracle's score + select + attend of every (seq, kv head) "
+                         f"given the block summaries, pairs over {thr} OpenMP threads, median of "
+                         f"{n} layer-steps",
+               "selection_matches_gpu": same}
+        log(f"[bench] cpu oracle: {cpu_us:.0f} us/layer-step ({thr} threads, {cpu_model()}); "
+            f"selection equal to the GPU's: {same}")
         dense_us, nd, thr = cpu_dense(cfg, layers[0][0], layers[0][1], args.cpu_seconds)
         cpu_dense_path = {"value": round(dense_us, 1), "unit": "us/layer-step", "cores": thr,
                           "kind": "reference path (dense)",
@@ -491,10 +513,15 @@ def bench_layers(args, cfg: Config):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "k_attend (gather + attention)" if cfg.bits == 0 else
-                               "k_attend_q (gather + fused dequant + attention)",
+                     "kernel": ("k_attend" if cfg.bits == 0 else "k_attend_q")
+                               + " as the decode step runs it (gather + attention"
+                               + ("" if cfg.bits == 0 else ", dequant fused") + ")",
                      "launch_us": round(attend_us, 3),
-                     "bytes_per_launch": attn_bytes, "combine_us": round(combine_us, 3)},
+                     "bytes_per_launch": attn_bytes, "combine_us": round(combine_us, 3),
+                     "given_index": {"launch_us": round(given_us, 3),
+                                     "achieved": round(given_achieved, 1),
+                                     "frac": round(given_achieved / HBM_PEAK_GBPS, 4),
+                                     "combine_us": round(given_combine_us, 3)}},
         "decode_kernels_us": decode_kernels,
         "layer_step_GBps": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "eager_us_per_layer_step": round(eager_ms * 1e3 / L, 3),
@@ -757,8 +784,9 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the block-sparse decode "
-                                   "path is a single-GPU kernel set (see DESIGN.md for how it "
-                                   "would shard); run with --gpus 1"}))
+                                   "path is a single-GPU kernel set (it would shard by sequence, "
+                                   "then by kv head, with no exchange on this path); run with "
+                                   "--gpus 1"}))
         sys.exit(2)
     if args.config == "c4":
         bench_loop(args)

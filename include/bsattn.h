@@ -38,6 +38,8 @@ extern "C" {
 #define BSATTN_ERR_HIP (-2)      /* a HIP runtime call failed */
 #define BSATTN_ERR_NO_PAGES (-3) /* the page pool is exhausted */
 #define BSATTN_ERR_RANGE (-4)    /* sequence id or length out of range */
+#define BSATTN_ERR_NOMEM (-5)    /* a host allocation failed; the cache is unchanged */
+#define BSATTN_ERR_INTERNAL (-6) /* an unexpected internal failure */
 
 /* element types of q / k / v / output / summaries */
 #define BSATTN_F16 0

@@ -17,6 +17,8 @@ ERR_INVALID = -1
 ERR_HIP = -2
 ERR_NO_PAGES = -3
 ERR_RANGE = -4
+ERR_NOMEM = -5
+ERR_INTERNAL = -6
 
 F16 = 0
 BF16 = 1

@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -25,14 +26,35 @@ namespace {
 
 thread_local std::string g_err;
 
-int fail(int code, const char* fmt, ...) {
+int fail(int code, const char* fmt, ...) noexcept {
   char buf[512];
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
-  g_err = buf;
+  try {
+    g_err = buf;
+  } catch (...) {
+    g_err.clear();  // no memory for the message: the status code still says what failed
+  }
   return code;
+}
+
+// Handler of every entry point's function-try-block: no C++ exception
+// crosses the ABI.  Host state is only changed after the allocations a call
+// needs have succeeded, so a failed call leaves the cache as it was.
+int on_exception() noexcept {
+  try {
+    throw;
+  } catch (const std::bad_alloc&) {
+    return fail(BSATTN_ERR_NOMEM, "host memory allocation failed");
+  } catch (const std::length_error&) {
+    return fail(BSATTN_ERR_NOMEM, "host container size limit exceeded");
+  } catch (const std::exception& e) {
+    return fail(BSATTN_ERR_INTERNAL, "internal error: %s", e.what());
+  } catch (...) {
+    return fail(BSATTN_ERR_INTERNAL, "internal error: unknown exception");
+  }
 }
 
 int hip_fail(hipError_t e, const char* what) {
@@ -167,7 +189,9 @@ int release_pages(bsattn_cache* c, int seq, int keep_blocks,
   return BSATTN_OK;
 }
 
-// Reserve pages for new lengths; on failure nothing changes.
+// Reserve pages for new lengths; on failure nothing changes.  A sequence may
+// already hold more pages than its new length needs (bsattn_reserve took them
+// ahead): it needs none, and its surplus is not counted against the others.
 int reserve_pages(bsattn_cache* c, const std::vector<int32_t>& seqs, int L,
                   std::vector<std::pair<int32_t, int32_t>>& patches) {
   const int tb = c->d.block_size;
@@ -177,11 +201,14 @@ int reserve_pages(bsattn_cache* c, const std::vector<int32_t>& seqs, int L,
     if (newlen > (int64_t)c->d.max_blocks_per_seq * tb)
       return fail(BSATTN_ERR_RANGE, "sequence %d would hold %lld tokens > max_blocks_per_seq * block_size = %d",
                   s, (long long)newlen, c->d.max_blocks_per_seq * tb);
-    need += (newlen + tb - 1) / tb - (int64_t)c->pages[s].size();
+    need += std::max<int64_t>(0, (newlen + tb - 1) / tb - (int64_t)c->pages[s].size());
   }
   if (need > (int64_t)c->free_pages.size())
     return fail(BSATTN_ERR_NO_PAGES, "page pool exhausted: need %lld pages, %zu free", (long long)need,
                 c->free_pages.size());
+  // every allocation first (may throw), then the bookkeeping (cannot)
+  patches.reserve(patches.size() + (size_t)need + seqs.size());
+  for (int s : seqs) c->pages[s].reserve((c->len[s] + L + tb - 1) / tb);
   for (int s : seqs) {
     const int newlen = c->len[s] + L;
     const int nblk = (newlen + tb - 1) / tb;
@@ -269,7 +296,7 @@ int32_t bsattn_version(void) { return BSATTN_VERSION; }
 
 const char* bsattn_last_error(void) { return g_err.c_str(); }
 
-int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
+int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) try {
   if (!desc || !out) return fail(BSATTN_ERR_INVALID, "null argument");
   *out = nullptr;
   int rc = validate_desc(*desc);
@@ -277,7 +304,7 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   DeviceGuard dg(desc->device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", desc->device);
   bsattn_cache* c = new (std::nothrow) bsattn_cache();
-  if (!c) return fail(BSATTN_ERR_INVALID, "host allocation failed");
+  if (!c) return fail(BSATTN_ERR_NOMEM, "host allocation failed");
   c->d = *desc;
   const bsattn_desc& d = c->d;
   c->num_pages = d.num_pages ? d.num_pages : (int64_t)d.max_seqs * d.max_blocks_per_seq;
@@ -307,6 +334,16 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   c->pool_bytes = (size_t)c->num_pages * g.hkv * g.slab_bytes;
   c->summ_bytes = (size_t)d.max_seqs * g.hkv * g.mbps * kHeadDim * 2;
   c->meta_words = (size_t)d.max_seqs * (2 + d.max_blocks_per_seq);
+  // host bookkeeping before any device allocation, so a failure here leaks nothing
+  try {
+    c->len.assign(d.max_seqs, 0);
+    c->pages.assign(d.max_seqs, {});
+    c->free_pages.resize(c->num_pages);
+  } catch (...) {
+    delete c;
+    throw;
+  }
+  for (int64_t i = 0; i < c->num_pages; ++i) c->free_pages[i] = (int32_t)(c->num_pages - 1 - i);
   auto cleanup = [&](int code) {
     (void)hipFree(g.pool);
     (void)hipFree(g.summ);
@@ -337,15 +374,13 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) {
   if ((e = hipMemset(g.summ, 0, c->summ_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(summaries)"));
   if ((e = hipMemset(g.meta, 0, c->meta_words * 4)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(meta)"));
   if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(hip_fail(e, "hipDeviceSynchronize"));
-  c->len.assign(d.max_seqs, 0);
-  c->pages.assign(d.max_seqs, {});
-  c->free_pages.resize(c->num_pages);
-  for (int64_t i = 0; i < c->num_pages; ++i) c->free_pages[i] = (int32_t)(c->num_pages - 1 - i);
   *out = c;
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
-int bsattn_cache_destroy(bsattn_cache* c) {
+int bsattn_cache_destroy(bsattn_cache* c) try {
   if (!c) return BSATTN_OK;
   DeviceGuard dg(c->d.device);
   (void)hipDeviceSynchronize();
@@ -359,9 +394,11 @@ int bsattn_cache_destroy(bsattn_cache* c) {
   (void)hipFree(c->err_ws);
   delete c;
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
-int bsattn_cache_info(const bsattn_cache* c, bsattn_info* out) {
+int bsattn_cache_info(const bsattn_cache* c, bsattn_info* out) try {
   if (!c || !out) return fail(BSATTN_ERR_INVALID, "null argument");
   out->nsel_max = c->geo.nsel_max;
   out->num_splits = c->geo.nsplit;
@@ -369,6 +406,8 @@ int bsattn_cache_info(const bsattn_cache* c, bsattn_info* out) {
   out->pool_bytes = (int64_t)(c->pool_bytes + c->summ_bytes + c->meta_words * 4);
   out->free_pages = (int64_t)c->free_pages.size();
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
 // Calls that need the exact token counts refuse while device-side appends
@@ -380,17 +419,19 @@ static int check_synced(const bsattn_cache* c) {
   return BSATTN_OK;
 }
 
-int bsattn_seq_len(const bsattn_cache* c, int32_t seq, int32_t* out_len) {
+int bsattn_seq_len(const bsattn_cache* c, int32_t seq, int32_t* out_len) try {
   if (!c || !out_len) return fail(BSATTN_ERR_INVALID, "null argument");
   if (seq < 0 || seq >= c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "sequence id %d out of range", seq);
   int rc = check_synced(c);
   if (rc) return rc;
   *out_len = c->len[seq];
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_reserve(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
-                   void* stream) {
+                   void* stream) try {
   if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
   if (n_tokens < 0) return fail(BSATTN_ERR_INVALID, "n_tokens must be >= 0");
   std::vector<int32_t> seqs;
@@ -404,10 +445,12 @@ int bsattn_reserve(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int3
   rc = reserve_pages(c, seqs, n_tokens, patches);
   if (rc) return rc;
   return flush_patches(c, patches, (hipStream_t)stream);
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_append_step(bsattn_cache* c, const void* k, const void* v, const int32_t* seq_ids,
-                       int32_t n_seqs, void* stream) {
+                       int32_t n_seqs, void* stream) try {
   if (!c || !k || !v) return fail(BSATTN_ERR_INVALID, "null argument");
   if (c->d.kv_bits != 0)
     return fail(BSATTN_ERR_INVALID, "device-side appends are provided for 16-bit caches");
@@ -432,9 +475,11 @@ int bsattn_append_step(bsattn_cache* c, const void* k, const void* v, const int3
   }
   c->stale = true;
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
-int bsattn_sync(bsattn_cache* c, void* stream) {
+int bsattn_sync(bsattn_cache* c, void* stream) try {
   if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
@@ -444,6 +489,8 @@ int bsattn_sync(bsattn_cache* c, void* stream) {
   c->len = dev;
   c->stale = false;
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
 // Shared append flow: reserve pages, patch lengths / block tables, then per
@@ -499,7 +546,7 @@ int append_impl(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t
 }
 
 int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* seq_ids,
-                  int32_t n_seqs, int32_t n_tokens, void* stream) {
+                  int32_t n_seqs, int32_t n_tokens, void* stream) try {
   if (!c || !k || !v) return fail(BSATTN_ERR_INVALID, "null argument");
   hipStream_t s = (hipStream_t)stream;
   const size_t row = (size_t)c->geo.hkv * n_tokens * kHeadDim;  // elements per sequence
@@ -511,12 +558,14 @@ int bsattn_append(bsattn_cache* c, const void* k, const void* v, const int32_t* 
     return quant ? launch_append_q16(c->geo, ab, kk, vv, s, prof)
                  : launch_append(c->geo, ab, kk, vv, fused, s, prof);
   });
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_append_quantized(bsattn_cache* c, const uint32_t* k_w, const void* k_s, const void* k_b,
                             const uint32_t* v_w, const void* v_s, const void* v_b,
                             const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
-                            void* stream) {
+                            void* stream) try {
   if (!c || !k_w || !k_s || !k_b || !v_w || !v_s || !v_b) return fail(BSATTN_ERR_INVALID, "null argument");
   if (c->d.kv_bits == 0) return fail(BSATTN_ERR_INVALID, "not a quantized cache (kv_bits 0): use bsattn_append");
   hipStream_t s = (hipStream_t)stream;
@@ -529,6 +578,8 @@ int bsattn_append_quantized(bsattn_cache* c, const uint32_t* k_w, const void* k_
                                    (const uint16_t*)k_b + go, v_w + wo, (const uint16_t*)v_s + go,
                                    (const uint16_t*)v_b + go, s, prof);
   });
+} catch (...) {
+  return on_exception();
 }
 
 // One query of a launch: the sequence, the tokens it sees (-1: all), the
@@ -610,7 +661,7 @@ static int run_entries(bsattn_cache* c, Op op, const void* q, const std::vector<
 }
 
 int bsattn_select(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
-                  int32_t* idx_out, void* stream) {
+                  int32_t* idx_out, void* stream) try {
   if (!c || !q || !idx_out) return fail(BSATTN_ERR_INVALID, "null argument");
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
@@ -619,10 +670,12 @@ int bsattn_select(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   return run_entries(c, Op::Select, q, entries(c, seqs, 1), kHeadDim, nullptr, idx_out, 0.0f, nullptr,
                      (hipStream_t)stream);
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_attend(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
-                  const int32_t* idx, float scale, void* out, void* stream) {
+                  const int32_t* idx, float scale, void* out, void* stream) try {
   if (!c || !q || !idx || !out) return fail(BSATTN_ERR_INVALID, "null argument");
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
@@ -631,10 +684,12 @@ int bsattn_attend(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   return run_entries(c, Op::Attend, q, entries(c, seqs, 1), kHeadDim, idx, nullptr, scale, out,
                      (hipStream_t)stream);
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
-                  float scale, void* out, int32_t* idx_out, void* stream) {
+                  float scale, void* out, int32_t* idx_out, void* stream) try {
   if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
   std::vector<int32_t> seqs;
   int rc = seq_list(c, seq_ids, n_seqs, seqs);
@@ -643,11 +698,13 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   return run_entries(c, Op::Decode, q, entries(c, seqs, 1), kHeadDim, nullptr, idx_out, scale, out,
                      (hipStream_t)stream);
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_append_decode(bsattn_cache* c, const void* k, const void* v, const void* q,
                          const int32_t* seq_ids, int32_t n_seqs, float scale, void* out,
-                         int32_t* idx_out, void* stream) {
+                         int32_t* idx_out, void* stream) try {
   if (!c || !k || !v || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
   if (int rs = check_synced(c)) return rs;
   std::vector<int32_t> seqs;
@@ -704,10 +761,12 @@ int bsattn_append_decode(bsattn_cache* c, const void* k, const void* v, const vo
   if (e != hipSuccess) return hip_fail(e, "append-decode launch");
   for (int sq : seqs) c->len[sq] += 1;
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
-                        int32_t n_query, float scale, void* out, int32_t* idx_out, void* stream) {
+                        int32_t n_query, float scale, void* out, int32_t* idx_out, void* stream) try {
   if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
   if (int rs = check_synced(c)) return rs;
   if (n_query < 1 || n_query > kMaxQueries)
@@ -723,10 +782,12 @@ int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, 
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   return run_entries(c, Op::Decode, q, entries(c, seqs, n_query), n_query * kHeadDim, nullptr, idx_out,
                      scale, out, (hipStream_t)stream);
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_prefill(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
-                   int32_t n_query, float scale, void* out, void* stream) {
+                   int32_t n_query, float scale, void* out, void* stream) try {
   if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
   if (int rs = check_synced(c)) return rs;
   if (n_query < 1) return fail(BSATTN_ERR_INVALID, "n_query must be >= 1");
@@ -761,10 +822,12 @@ int bsattn_prefill(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
   }
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t n_tokens,
-                int32_t* trimmed, void* stream) {
+                int32_t* trimmed, void* stream) try {
   if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
   if (int rs = check_synced(c)) return rs;
   if (n_tokens < 0) return fail(BSATTN_ERR_INVALID, "n_tokens must be >= 0");
@@ -774,6 +837,7 @@ int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   std::vector<std::pair<int32_t, int32_t>> patches;
+  patches.reserve(2 * seqs.size());  // the loop below then cannot throw
   for (int i = 0; i < n_seqs; ++i) {
     const int sq = seqs[i];
     const int t = std::min(c->len[sq], n_tokens);
@@ -783,9 +847,11 @@ int bsattn_trim(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, int32_t
     patches.emplace_back(sq, c->len[sq]);
   }
   return flush_patches(c, patches, (hipStream_t)stream);
+} catch (...) {
+  return on_exception();
 }
 
-int bsattn_reset(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* stream) {
+int bsattn_reset(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* stream) try {
   if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
   if (int rs = check_synced(c)) return rs;
   std::vector<int32_t> seqs;
@@ -794,39 +860,53 @@ int bsattn_reset(bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* 
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   std::vector<std::pair<int32_t, int32_t>> patches;
+  patches.reserve(2 * seqs.size());  // the loop below then cannot throw
   for (int sq : seqs) {
     c->len[sq] = 0;
     release_pages(c, sq, 0, patches);
     patches.emplace_back(sq, 0);
   }
   return flush_patches(c, patches, (hipStream_t)stream);
+} catch (...) {
+  return on_exception();
 }
 
-int bsattn_copy(const bsattn_cache* src, bsattn_cache** out, void* stream) {
+int bsattn_copy(const bsattn_cache* src, bsattn_cache** out, void* stream) try {
   if (!src || !out) return fail(BSATTN_ERR_INVALID, "null argument");
   if (int rs = check_synced(src)) return rs;
   int rc = bsattn_cache_create(&src->d, out);
   if (rc) return rc;
   bsattn_cache* c = *out;
+  *out = nullptr;
+  try {
+    c->len = src->len;
+    c->pages = src->pages;
+    c->free_pages = src->free_pages;
+  } catch (...) {
+    bsattn_cache_destroy(c);
+    throw;
+  }
   DeviceGuard dg(src->d.device);
-  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", src->d.device);
+  if (!dg.ok) {
+    bsattn_cache_destroy(c);
+    return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", src->d.device);
+  }
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if ((e = hipMemcpyAsync(c->geo.pool, src->geo.pool, src->pool_bytes, hipMemcpyDeviceToDevice, s)) != hipSuccess ||
       (e = hipMemcpyAsync(c->geo.summ, src->geo.summ, src->summ_bytes, hipMemcpyDeviceToDevice, s)) != hipSuccess ||
       (e = hipMemcpyAsync(c->geo.meta, src->geo.meta, src->meta_words * 4, hipMemcpyDeviceToDevice, s)) != hipSuccess) {
     bsattn_cache_destroy(c);
-    *out = nullptr;
     return hip_fail(e, "copy");
   }
-  c->len = src->len;
-  c->pages = src->pages;
-  c->free_pages = src->free_pages;
+  *out = c;
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_export(const bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs, void* k_out,
-                  void* v_out, void* stream) {
+                  void* v_out, void* stream) try {
   if (!c || !k_out || !v_out) return fail(BSATTN_ERR_INVALID, "null argument");
   if (int rs = check_synced(c)) return rs;
   if (c->d.kv_bits != 0) return fail(BSATTN_ERR_INVALID, "quantized cache: use bsattn_export_quantized");
@@ -852,11 +932,13 @@ int bsattn_export(const bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs,
             "export launch");
   }
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
 int bsattn_export_quantized(const bsattn_cache* c, const int32_t* seq_ids, int32_t n_seqs,
                             uint32_t* k_w, void* k_s, void* k_b, uint32_t* v_w, void* v_s,
-                            void* v_b, void* stream) {
+                            void* v_b, void* stream) try {
   if (!c || !k_w || !k_s || !k_b || !v_w || !v_s || !v_b) return fail(BSATTN_ERR_INVALID, "null argument");
   if (int rs = check_synced(c)) return rs;
   if (c->d.kv_bits == 0) return fail(BSATTN_ERR_INVALID, "not a quantized cache (kv_bits 0): use bsattn_export");
@@ -885,9 +967,11 @@ int bsattn_export_quantized(const bsattn_cache* c, const int32_t* seq_ids, int32
             "export launch");
   }
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
-int bsattn_export_summaries(const bsattn_cache* c, int32_t seq, void* out, void* stream) {
+int bsattn_export_summaries(const bsattn_cache* c, int32_t seq, void* out, void* stream) try {
   if (!c || !out) return fail(BSATTN_ERR_INVALID, "null argument");
   if (int rs = check_synced(c)) return rs;
   if (seq < 0 || seq >= c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "sequence id %d out of range", seq);
@@ -897,9 +981,11 @@ int bsattn_export_summaries(const bsattn_cache* c, int32_t seq, void* out, void*
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   HIP_TRY(launch_export_summaries(c->geo, seq, nfull, out, (hipStream_t)stream), "export summaries launch");
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
-int bsattn_profile_enable(bsattn_cache* c, int32_t enable) {
+int bsattn_profile_enable(bsattn_cache* c, int32_t enable) try {
   if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
@@ -911,9 +997,11 @@ int bsattn_profile_enable(bsattn_cache* c, int32_t enable) {
   }
   c->profiling = enable != 0;
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
-int bsattn_profile_read(bsattn_cache* c, int32_t kernel, double* total_ms, int64_t* launches) {
+int bsattn_profile_read(bsattn_cache* c, int32_t kernel, double* total_ms, int64_t* launches) try {
   if (!c || !total_ms || !launches) return fail(BSATTN_ERR_INVALID, "null argument");
   if (kernel < 0 || kernel >= kProfKinds) return fail(BSATTN_ERR_INVALID, "unknown kernel id %d", kernel);
   DeviceGuard dg(c->d.device);
@@ -923,6 +1011,8 @@ int bsattn_profile_read(bsattn_cache* c, int32_t kernel, double* total_ms, int64
   *total_ms = c->prof_ms[kernel];
   *launches = c->prof_count[kernel];
   return BSATTN_OK;
+} catch (...) {
+  return on_exception();
 }
 
 }  // extern "C"

@@ -59,10 +59,16 @@ __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
 
 // ---------------------------------------------------------------------------
 // quantize 8 consecutive dims of one row (lane c of the 16 lanes holding the
-// row; lanes c & ~7 .. +7 hold one 64-dim group), exactly as the affine
-// codec: min / max of the group (the first of equal values, as a scan in dim
-// order keeps), scale = fp16((max - min) / (2^b - 1)) (1 if that is 0),
-// bias = fp16(min), code = clamp(rint((x - bias) / scale), 0, 2^b - 1).
+// row; lanes c & ~7 .. +7 hold one 64-dim group) by mlx's affine rule, in
+// fp32 with correctly rounded divisions:
+//   scale = max((max - min) / (2^b - 1), 1e-7), negated unless
+//   |min| > |max|; edge = min if |min| > |max| else max;
+//   q0 = rint(edge / scale); q0 != 0: scale = edge / q0, bias = edge;
+//   q0 == 0 (an all-zero group): bias = 0;
+//   code = clamp(rint((x - bias) / scale), 0, 2^b - 1) from the fp32 scale
+//   and bias, which are stored rounded to fp16.
+// (Signed zeros cannot matter: q0 == 0 only when edge is a zero, and then
+// bias is +0.)
 // ---------------------------------------------------------------------------
 template <int KB>
 __device__ __forceinline__ void quantize8(const uint16_t* __restrict__ src, int c, uint8_t* codes,
@@ -74,35 +80,35 @@ __device__ __forceinline__ void quantize8(const uint16_t* __restrict__ src, int 
   float mn = x[0], mx = x[0];
 #pragma unroll
   for (int e = 1; e < 8; ++e) {
-    if (x[e] < mn) mn = x[e];
-    if (x[e] > mx) mx = x[e];
+    mn = fminf(mn, x[e]);
+    mx = fmaxf(mx, x[e]);
   }
 #pragma unroll
   for (int off = 1; off < 8; off <<= 1) {
-    const float pmn = __shfl_xor(mn, off, 64), pmx = __shfl_xor(mx, off, 64);
-    if (c & off) {  // the partner holds the lower dims and wins ties
-      mn = (mn < pmn) ? mn : pmn;
-      mx = (mx > pmx) ? mx : pmx;
-    } else {
-      mn = (pmn < mn) ? pmn : mn;
-      mx = (pmx > mx) ? pmx : mx;
-    }
+    mn = fminf(mn, __shfl_xor(mn, off, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   }
   constexpr float nbins = (float)((1 << KB) - 1);
-  _Float16 s16 = (_Float16)__fdiv_rn(__fsub_rn(mx, mn), nbins);
-  if ((float)s16 == 0.0f) s16 = (_Float16)1.0f;
-  const _Float16 b16 = (_Float16)mn;
-  const float sf = (float)s16, bf = (float)b16;
+  float scale = fmaxf(__fdiv_rn(__fsub_rn(mx, mn), nbins), (float)1e-7);
+  const bool side = fabsf(mn) > fabsf(mx);
+  scale = side ? scale : -scale;
+  const float edge = side ? mn : mx;
+  const float q0 = __builtin_rintf(__fdiv_rn(edge, scale));
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    scale = __fdiv_rn(edge, q0);
+    bias = edge;
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float qv = __builtin_rintf(__fdiv_rn(__fsub_rn(x[e], bf), sf));
+    float qv = __builtin_rintf(__fdiv_rn(__fsub_rn(x[e], bias), scale));
     qv = qv < 0.0f ? 0.0f : qv;
     qv = qv > nbins ? nbins : qv;
     codes[e] = (uint8_t)qv;
   }
   if ((c & 7) == 0) {
-    *scale_out = __builtin_bit_cast(uint16_t, s16);
-    *bias_out = __builtin_bit_cast(uint16_t, b16);
+    *scale_out = __builtin_bit_cast(uint16_t, (_Float16)scale);
+    *bias_out = __builtin_bit_cast(uint16_t, (_Float16)bias);
   }
 }
 

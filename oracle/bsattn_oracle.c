@@ -24,6 +24,9 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 
 /* ------------------------------------------------------------------ */
 /* numeric formats                                                     */
@@ -209,19 +212,56 @@ int orc_summaries(const uint16_t* keys, int T, int D, int Tb, int dtype,
 }
 
 /* ------------------------------------------------------------------ */
-/* MLX-style affine codec                                              */
-/*   per group of gs elements along D:                                 */
-/*     scale = fp16((max - min) / (2^bits - 1)), bias = fp16(min)      */
-/*     (scale 0 -> 1 so constant groups round-trip exactly)            */
-/*     code  = clamp(rint((x - bias) / scale), 0, 2^bits - 1)          */
-/*   element i of a row lives in word i / (32/bits), bit              */
+/* MLX affine codec                                                    */
+/*   The reference quantizes with mlx-swift's quantized(_:groupSize:   */
+/*   bits:) (KVCache.swift:416-417 in toQuantized, :856-857 in         */
+/*   updateQuantized).  That lives in the un-vendored dependency       */
+/*   mlx-swift 0.31.x (Package.swift:39) -> mlx; restated here is its  */
+/*   published affine rule (mlx ops `affine_quantize`, CPU backend     */
+/*   `quantize`), all in fp32, per group of gs elements along D:       */
+/*     mn, mx  = min / max of the group                                */
+/*     scale   = max((mx - mn) / (2^bits - 1), 1e-7)                   */
+/*     side    = |mn| > |mx|;  scale = side ? scale : -scale           */
+/*     edge    = side ? mn : mx            (the larger-magnitude end)  */
+/*     q0      = rint(edge / scale)                                    */
+/*     q0 != 0: scale = edge / q0, bias = edge;  q0 == 0: bias = 0     */
+/*     code    = clamp(rint((x - bias) / scale), 0, 2^bits - 1)        */
+/*   with the fp32 scale and bias; they are stored rounded (RNE) to    */
+/*   fp16.  rint rounds half to even.  The edge therefore maps to a    */
+/*   code exactly (0 for mx, 2^bits - 1 ... for mn), and a group that  */
+/*   straddles 0 has 0 = bias + scale * (-q0) in exact arithmetic.     */
+/*   Element i of a row lives in word i / (32/bits), bit               */
 /*   bits * (i % (32/bits)), least significant first.                  */
-/*   dequant: w = fmaf(scale, code, bias) in fp32.                     */
+/*   dequant: w = fmaf(scale, code, bias) in fp32 (MLX's w = s*q + b). */
 /* ------------------------------------------------------------------ */
 
 int orc_code_at(const uint32_t* row_codes, int i, int bits) {
   int per = 32 / bits;
   return (int)((row_codes[i / per] >> (bits * (i % per))) & ((1u << bits) - 1u));
+}
+
+void orc_affine_params(const float* x, int gs, int bits, float* scale_out,
+                       float* bias_out) {
+  const float nbins = (float)((1 << bits) - 1);
+  const float eps = (float)1e-7;
+  float mn = INFINITY, mx = -INFINITY;
+  for (int i = 0; i < gs; i++) {
+    mx = mx < x[i] ? x[i] : mx; /* std::max(mx, x) */
+    mn = x[i] < mn ? x[i] : mn; /* std::min(mn, x) */
+  }
+  int side = fabsf(mn) > fabsf(mx);
+  float scale = (mx - mn) / nbins;
+  scale = scale < eps ? eps : scale;
+  scale = side ? scale : -scale;
+  float edge = side ? mn : mx;
+  float q0 = rintf(edge / scale);
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    scale = edge / q0;
+    bias = edge;
+  }
+  *scale_out = scale;
+  *bias_out = bias;
 }
 
 void orc_quantize_affine(const uint16_t* x, int64_t rows, int D, int bits,
@@ -231,29 +271,23 @@ void orc_quantize_affine(const uint16_t* x, int64_t rows, int D, int bits,
   int words = D / per;
   int ng = D / gs;
   float nbins = (float)((1 << bits) - 1);
+  float xf[256];
+  if (gs > 256 || D % gs != 0 || gs % per != 0) abort();
   for (int64_t r = 0; r < rows; r++) {
     const uint16_t* xr = x + r * D;
     uint32_t* cr = codes + r * words;
     memset(cr, 0, sizeof(uint32_t) * (size_t)words);
     for (int g = 0; g < ng; g++) {
-      float mn = orc_f16_to_f32(xr[g * gs]), mx = mn;
-      for (int i = 1; i < gs; i++) {
-        float v = orc_f16_to_f32(xr[g * gs + i]);
-        mn = v < mn ? v : mn;
-        mx = v > mx ? v : mx;
-      }
-      float s = (mx - mn) / nbins;
-      uint16_t s16 = orc_f32_to_f16(s);
-      if (orc_f16_to_f32(s16) == 0.0f) s16 = 0x3C00; /* 1.0 */
-      uint16_t b16 = orc_f32_to_f16(mn);
-      scales[r * ng + g] = s16;
-      biases[r * ng + g] = b16;
-      float sf = orc_f16_to_f32(s16), bf = orc_f16_to_f32(b16);
+      for (int i = 0; i < gs; i++) xf[i] = orc_f16_to_f32(xr[g * gs + i]);
+      float sf, bf;
+      orc_affine_params(xf, gs, bits, &sf, &bf);
+      scales[r * ng + g] = orc_f32_to_f16(sf);
+      biases[r * ng + g] = orc_f32_to_f16(bf);
       for (int i = 0; i < gs; i++) {
         int e = g * gs + i;
-        float q = rintf((orc_f16_to_f32(xr[e]) - bf) / sf);
-        if (q < 0.0f) q = 0.0f;
-        if (q > nbins) q = nbins;
+        float q = rintf((xf[i] - bf) / sf);
+        q = q < 0.0f ? 0.0f : q; /* std::max(q, 0) */
+        q = q > nbins ? nbins : q;
         cr[e / per] |= ((uint32_t)q) << (bits * (e % per));
       }
     }
@@ -558,4 +592,48 @@ int orc_decode_head(const uint16_t* q, int G, const uint16_t* keys,
   free(summ);
   free(sc);
   return n;
+}
+
+/* ------------------------------------------------------------------ */
+/* one decode layer-step of every (sequence, kv head), given the block  */
+/* summaries: score -> select -> attend, the (b, h) pairs spread over   */
+/* OpenMP threads (each pair is independent).  The CPU baseline; the    */
+/* per-pair arithmetic is the functions above.                          */
+/* ------------------------------------------------------------------ */
+
+int orc_omp_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+void orc_layer_step(const uint16_t* q, const uint16_t* summ, const uint16_t* keys,
+                    const uint16_t* values, const uint32_t* kc, const uint16_t* ks,
+                    const uint16_t* kb, const uint32_t* vc, const uint16_t* vs,
+                    const uint16_t* vb, int B, int Hq, int Hkv, int T, int D, int Tb,
+                    int bits, int gs, int ns, int nr, int K, double scale, int dtype,
+                    int32_t* idx_out, double* out) {
+  const int G = Hq / Hkv, nfull = T / Tb, nsel = ns + nr + K;
+  const int words = bits ? D * bits / 32 : 0, ng = bits ? D / gs : 0;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int p = 0; p < B * Hkv; p++) {
+    const int b = p / Hkv, h = p % Hkv;
+    const uint16_t* qq = q + ((int64_t)b * Hq + (int64_t)h * G) * D;
+    float* sc = (float*)malloc(sizeof(float) * (size_t)(nfull + 1));
+    orc_score_blocks(qq, G, summ + (int64_t)p * nfull * D, nfull, D, bits ? ORC_F16 : dtype, sc);
+    int32_t* idx = idx_out + (int64_t)p * nsel;
+    int n = orc_select(sc, T, Tb, ns, nr, K, idx);
+    double* o = out + ((int64_t)b * Hq + (int64_t)h * G) * D;
+    if (bits) {
+      const int64_t t0 = (int64_t)p * T;
+      orc_attend_q(qq, G, kc + t0 * words, ks + t0 * ng, kb + t0 * ng, vc + t0 * words,
+                   vs + t0 * ng, vb + t0 * ng, T, D, Tb, bits, gs, idx, n, scale, o);
+    } else {
+      const int64_t t0 = (int64_t)p * T * D;
+      orc_attend(qq, G, keys + t0, values + t0, T, D, Tb, idx, n, scale, dtype, o);
+    }
+    free(sc);
+  }
 }

@@ -63,7 +63,10 @@ void orc_block_summary(const uint16_t* keys, int64_t ld, int Tb, int D,
 int orc_summaries(const uint16_t* keys, int T, int D, int Tb, int dtype,
                   uint16_t* out /* [T/Tb][D] */);
 
-/* ---- MLX-style affine codec (group along the head dim, LSB-first pack) ---- */
+/* ---- MLX affine codec (group along the head dim, LSB-first pack) ---- */
+/* fp32 scale and bias of one group of gs values (before their fp16 cast) */
+void orc_affine_params(const float* x, int gs, int bits, float* scale_out,
+                       float* bias_out);
 void orc_quantize_affine(const uint16_t* x_f16, int64_t rows, int D, int bits,
                          int gs, uint32_t* codes, uint16_t* scales,
                          uint16_t* biases);
@@ -125,6 +128,20 @@ int orc_decode_head(const uint16_t* q, int G, const uint16_t* keys,
                     const uint16_t* values, int T, int D, int Tb, int ns,
                     int nr, int K, double scale, int dtype, int32_t* idx_out,
                     double* out);
+
+/* ---- one decode layer-step of B sequences x Hkv kv heads, T tokens each,
+ * given the block summaries summ [B][Hkv][T/Tb][D]: score -> select ->
+ * attend per (sequence, kv head), pairs spread over OpenMP threads.  16-bit
+ * caches pass keys / values [B][Hkv][T][D] (dtype); quantized ones (bits 4 /
+ * 8, dtype fp16) pass kc / vc [B][Hkv][T][D*bits/32] and ks / kb / vs / vb
+ * [B][Hkv][T][D/gs] instead.  idx_out [B][Hkv][ns+nr+K], out [B][Hq][D]. */
+int orc_omp_threads(void);
+void orc_layer_step(const uint16_t* q, const uint16_t* summ, const uint16_t* keys,
+                    const uint16_t* values, const uint32_t* kc, const uint16_t* ks,
+                    const uint16_t* kb, const uint32_t* vc, const uint16_t* vs,
+                    const uint16_t* vb, int B, int Hq, int Hkv, int T, int D, int Tb,
+                    int bits, int gs, int ns, int nr, int K, double scale, int dtype,
+                    int32_t* idx_out, double* out);
 
 #ifdef __cplusplus
 }

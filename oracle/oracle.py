@@ -54,6 +54,7 @@ def lib():
             "orc_uniform_int": (i64, [u64, u64, u64, i64, i64]),
             "orc_block_summary": (None, [P, i64, i32, i32, i32, P]),
             "orc_summaries": (i32, [P, i32, i32, i32, i32, P]),
+            "orc_affine_params": (None, [P, i32, i32, P, P]),
             "orc_quantize_affine": (None, [P, i64, i32, i32, i32, P, P, P]),
             "orc_dequantize_affine": (None, [P, P, P, i64, i32, i32, i32, P]),
             "orc_block_summary_q": (None, [P, P, P, i32, i32, i32, i32, P]),
@@ -67,6 +68,8 @@ def lib():
             "orc_dense": (None, [P, i32, P, P, i32, i32, f64, i32, P]),
             "orc_block_mass": (None, [P, P, i32, i32, i32, f64, P]),
             "orc_decode_head": (i32, [P, i32, P, P, i32, i32, i32, i32, i32, i32, f64, i32, P, P]),
+            "orc_omp_threads": (i32, []),
+            "orc_layer_step": (None, [P] * 10 + [i32] * 11 + [f64, i32, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -243,7 +246,16 @@ def decode_head(q, keys, values, Tb, ns, nr, K, scale, dtype):
     return idx, int(n), out
 
 
-# ---- MLX-style affine codec --------------------------------------------------
+# ---- MLX affine codec -------------------------------------------------------
+
+def affine_params(x_f32: np.ndarray, bits: int):
+    """fp32 (scale, bias) of one group, before their fp16 cast."""
+    x = np.ascontiguousarray(x_f32, np.float32)
+    s = np.zeros(1, np.float32)
+    b = np.zeros(1, np.float32)
+    lib().orc_affine_params(_p(x), x.size, bits, _p(s), _p(b))
+    return float(s[0]), float(b[0])
+
 
 def quantize(x_f16: np.ndarray, bits: int, gs: int):
     x = np.ascontiguousarray(x_f16, np.uint16)
@@ -265,3 +277,35 @@ def dequantize(codes, scales, biases, bits: int, gs: int) -> np.ndarray:
     out = np.empty(codes.shape[:-1] + (D,), np.float32)
     lib().orc_dequantize_affine(_p(codes), _p(scales), _p(biases), rows, D, bits, gs, _p(out))
     return out
+
+
+def layer_step(q, summ, Tb, ns, nr, K, scale, dtype, keys=None, values=None, kq=None, vq=None,
+               bits=0, gs=64):
+    """One decode layer-step of every (sequence, kv head) given the block
+    summaries, OpenMP-parallel over the pairs.  q [B, Hq, D]; summ
+    [B, Hkv, T/Tb, D]; 16-bit keys / values [B, Hkv, T, D], or quantized
+    kq / vq = (codes [B, Hkv, T, W], scales, biases [B, Hkv, T, D/gs]).
+    -> (idx [B, Hkv, ns+nr+K] int32, out [B, Hq, D] float64)."""
+    q = np.ascontiguousarray(q, np.uint16)
+    summ = np.ascontiguousarray(summ, np.uint16)
+    B, Hq, D = q.shape
+    Hkv = summ.shape[1]
+    if bits:
+        kq = tuple(np.ascontiguousarray(a) for a in kq)
+        vq = tuple(np.ascontiguousarray(a) for a in vq)
+        T = kq[0].shape[2]
+        ptrs = [None, None, _p(kq[0]), _p(kq[1]), _p(kq[2]), _p(vq[0]), _p(vq[1]), _p(vq[2])]
+    else:
+        keys = np.ascontiguousarray(keys, np.uint16)
+        values = np.ascontiguousarray(values, np.uint16)
+        T = keys.shape[2]
+        ptrs = [_p(keys), _p(values)] + [None] * 6
+    idx = np.empty((B, Hkv, ns + nr + K), np.int32)
+    out = np.empty((B, Hq, D), np.float64)
+    lib().orc_layer_step(_p(q), _p(summ), *ptrs, B, Hq, Hkv, T, D, Tb, bits, gs, ns, nr, K, scale,
+                         dcode(dtype), _p(idx), _p(out))
+    return idx, out
+
+
+def omp_threads() -> int:
+    return int(lib().orc_omp_threads())

@@ -91,3 +91,29 @@ def test_append_step_stops_at_the_reservation(gpu):
     with pytest.raises(BsattnError):
         cq.appendStep(torch.zeros((1, 8, 1, 128), dtype=torch.float16, device=gpu),
                       torch.zeros((1, 8, 1, 128), dtype=torch.float16, device=gpu))
+
+
+def test_reserved_surplus_does_not_hide_a_shortage(gpu):
+    """A sequence holding pages ahead of its length (bsattn_reserve) needs
+    none for its next tokens, and its surplus must not offset what another
+    sequence needs: a pool of 4 pages (Tb 64), 192 tokens reserved for
+    sequence 0 (3 pages), then 128 tokens appended to sequences 0 and 1.
+    Sequence 1 needs 2 pages and 1 is free: BSATTN_ERR_NO_PAGES, with the
+    free pages and every length unchanged."""
+    import torch
+    from bsattn import BsattnError, _lib
+    Tb = 64
+    w = make_workload(8300, B=2, Hq=32, Hkv=8, T=Tb, Tb=Tb, dtype="bf16", top_k=2, lens=[0, 0])
+    c = new_cache(w, mbps=8, num_pages=4)
+    c.reserve(3 * Tb, seq_ids=[0])
+    assert c.freePages == 1
+    k = torch.zeros((2, 8, 2 * Tb, 128), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(BsattnError) as e:
+        c.append(k, k, seq_ids=[0, 1])
+    assert e.value.code == _lib.ERR_NO_PAGES
+    assert c.freePages == 1 and c.seqLen(0) == 0 and c.seqLen(1) == 0
+    # within the pool: sequence 0 uses its reserved pages, sequence 1 takes the free one
+    k1 = k[:, :, :Tb].contiguous()
+    c.append(k1, k1, seq_ids=[0, 1])
+    torch.cuda.synchronize()
+    assert c.freePages == 0 and c.seqLen(0) == Tb and c.seqLen(1) == Tb

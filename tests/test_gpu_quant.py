@@ -8,10 +8,12 @@ Bars:
     bit-exact;
   * attention outputs: max-abs error <= 1e-2 against the fp64 oracle over the
     dequantized keys / values, net of the final rounding to fp16.
-The codec's scale selection and the MLX-internal rounding of the reference's
-quantizedMM / softmax are not available offline (mlx is not vendored): the
-codec here is this library's own MLX-layout-compatible one, and parity is
-against the oracle's statement of it.
+The codec is mlx's published affine rule (signed scale, the larger-magnitude
+extreme as bias, scale = edge / rint(edge / scale)), which the reference reaches
+through quantized() (KVCache.swift:416-417, 856-857); the oracle's statement
+of it is pinned by hand-derived cases in test_oracle.py.  The MLX-internal
+rounding of the reference's quantizedMM / softmax is not available offline
+(mlx is not vendored) and is covered by the 1e-2 bar.
 """
 from __future__ import annotations
 
@@ -90,14 +92,21 @@ def run_and_check_q(cache, w: Workload, device, bits: int, kq, vq):
 
 
 def with_constant_rows(w: Workload):
-    """Some key / value rows constant (scale 0 -> 1) or with repeated extremes."""
+    """Groups that reach the codec's special cases: constant rows (scale
+    1e-7 -> fp16 0x8002 / 0x0002, bias = the value), all-zero groups (q0 = 0,
+    bias 0), |min| == |max| (the max side wins), repeated extremes."""
     for b in range(w.B):
         T = w.lens[b]
         for h in range(w.Hkv):
-            if T > 3:
+            if T > 5:
                 w.keys[b][h, 1, :] = 0x3C00          # all 1.0
                 w.values[b][h, 2, :64] = 0xBC00      # group of -1.0
                 w.keys[b][h, 3, ::7] = 0x4400        # repeated maximum 4.0
+                w.keys[b][h, 4, 64:] = 0x0000        # all-zero group
+                w.values[b][h, 4, :] = 0x8000        # -0.0 row
+                w.keys[b][h, 5, 0] = 0x4200          # 3.0 and -3.0: equal magnitudes
+                w.keys[b][h, 5, 1:64] = np.clip(w.keys[b][h, 5, 1:64], 0, 0x3BFF)
+                w.keys[b][h, 5, 9] = 0xC200
     return w
 
 

@@ -360,33 +360,217 @@ def test_block_mass_sums_to_one():
 
 
 # ------------------------------------------------------------ affine codec --
+# The reference quantizes with mlx's affine rule (KVCache.swift:416-417,
+# 856-857 call quantized(); the rule lives in the un-vendored mlx).  Each case
+# below is derived by hand in fp32 from the published rule: signed scale,
+# the larger-magnitude extreme as bias, scale = edge / rint(edge / scale),
+# codes from the fp32 scale / bias, rint (half to even), fp16 storage.
+
+def _group(vals, n=64):
+    g = np.zeros(n, np.float32)
+    g[:len(vals)] = vals
+    return g
+
+
+def _q1(vals, bits):
+    """quantize one 128-dim row whose two 64-dim groups both hold `vals`."""
+    g = _group(vals)
+    c, s, b = O.quantize(O.from_f32(np.concatenate([g, g]), "f16")[None], bits, 64)
+    return c[0], int(s[0, 0]), int(b[0, 0])
+
+
+def test_codec_min_side_positive_scale():
+    """|min| > |max|: mn -8, mx 4 -> scale 12/15 = 0.8f, edge -8,
+    q0 = rint(-8 / 0.8f) = -10, scale = -8 / -10 = 0.8f, bias -8.
+    codes: -8 -> 0, 4 -> rint(12 / 0.8f) = 15, 0 -> rint(8 / 0.8f) = 10.
+    fp16(0.8) = 0x3A66, fp16(-8) = 0xC800."""
+    c, s, b = _q1([-8, 4], 4)
+    assert (s, b) == (0x3A66, 0xC800)
+    assert c[0] == 0xAAAAAAF0 and all(c[1:8] == 0xAAAAAAAA)
+
+
+def test_codec_max_side_negative_scale():
+    """|max| >= |min|: mn -4, mx 8 -> scale -(12/15), edge 8, q0 = -10,
+    scale = 8 / -10 = -0.8f, bias 8.  codes: 8 -> 0, -4 -> rint(-12 / -0.8f)
+    = 15, 0 -> 10.  (bias = min would give 8 -> 15, -4 -> 0, 0 -> 5.)"""
+    c, s, b = _q1([8, -4], 4)
+    assert (s, b) == (0xBA66, 0x4800)
+    assert c[0] == 0xAAAAAAF0
+
+
+def test_codec_equal_magnitudes_take_max_side():
+    """|min| == |max| (4, -4): side is |mn| > |mx|, false, so edge = 4 and
+    scale = -(8/15) = -0.53333336f; 4 / scale = -7.4999995 -> q0 = -7,
+    scale = 4 / -7 = -0.5714286f (fp16 0xB892), bias 4 (0x4400).
+    codes: 4 -> 0, -4 -> rint(-8 / scale) = 14, 0 -> 7."""
+    c, s, b = _q1([4, -4], 4)
+    assert (s, b) == (0xB892, 0x4400)
+    assert c[0] == 0x777777E0 and c[1] == 0x77777777
+
+
+def test_codec_rounded_q0_and_fp32_scale():
+    """mn -1, mx 2.5: scale -(3.5/15), edge 2.5, 2.5 / scale = -10.71 ->
+    q0 = -11, scale = 2.5 / -11 = -0.22727273f (fp16 0xB346 = -0.2272949),
+    bias 2.5 (0x4100).  codes: -1 -> rint(15.4) = 15, 2.5 -> 0,
+    1 -> rint(6.6) = 7, 0.5 -> rint(8.8) = 9, 1.25 -> -1.25 / scale = 5.5
+    exactly -> 6 (with the fp16 scale it would be 5.4995 -> 5), 0 -> 11
+    (0 = 2.5 + 11 * (2.5 / -11) in exact arithmetic)."""
+    c, s, b = _q1([-1, 2.5, 1, 0.5, 1.25], 4)
+    assert (s, b) == (0xB346, 0x4100)
+    assert c[0] == 0xBBB6970F and c[1] == 0xBBBBBBBB
+
+
+def test_codec_ties_round_half_to_even():
+    """mn -2, mx 5.5: scale -(7.5/15) = -0.5, q0 = -11, scale -0.5 (0xB800),
+    bias 5.5 (0x4580); code = rint(11 - 2x): 0.25 -> 10.5 -> 10,
+    1.25 -> 8.5 -> 8, 0.75 -> 9.5 -> 10 (half away from zero: 11, 9, 10)."""
+    c, s, b = _q1([-2, 5.5, 0.25, 1.25, 0.75], 4)
+    assert (s, b) == (0xB800, 0x4580)
+    assert c[0] == 0xBBBA8A0F
+
+
+def test_codec_int8_word():
+    """int8, mn -1, mx 2.5: scale -(3.5/255), 2.5 / scale = -182.14 -> q0 =
+    -182, scale = 2.5 / -182 = -0.013736264f (fp16 0xA308), bias 2.5;
+    codes: -1 -> rint(254.8) = 255, 2.5 -> 0, 0 -> 182; bytes LSB first."""
+    c, s, b = _q1([-1, 2.5], 8)
+    assert (s, b) == (0xA308, 0x4100)
+    assert c[0] == 0xB6B600FF and c[1] == 0xB6B6B6B6
+
+
+def test_codec_zero_and_constant_groups():
+    """all zero: scale = max(0, 1e-7) -> -1e-7 (max side), q0 = 0 -> bias 0;
+    fp16(-1e-7) = -2 x 2^-24 = 0x8002.  A constant c: q0 = rint(c / -1e-7)
+    != 0, scale = c / q0 ~ -1e-7, bias = c, every code 0, so the group
+    dequantizes to c exactly."""
+    for bits in (4, 8):
+        c, s, b = _q1([], bits)
+        assert (s, b) == (0x8002, 0x0000) and not c.any()
+        for val, bias in ((0.5, 0x3800), (-3.0, 0xC200), (1000.0, 0x63D0)):
+            c, s, b = _q1([val] * 64, bits)
+            assert (s, b) == (0x8002, bias) and not c.any()
+            deq = O.dequantize(c[None], np.array([[s, s]], np.uint16), np.array([[b, b]], np.uint16), bits, 64)
+            assert np.all(deq == np.float32(val))
+
+
+def test_affine_params_fp32():
+    s, b = O.affine_params(_group([-1, 2.5]), 4)
+    assert s == float(np.float32(2.5) / np.float32(-11)) and b == 2.5
+    s, b = O.affine_params(_group([-8, 4]), 4)
+    assert s == float(np.float32(0.8)) and b == -8.0
+
 
 def test_codec_packing_order():
-    x = np.arange(16, dtype=np.float32)
-    x = np.concatenate([x, x, x, x, x, x, x, x])  # 128 values, groups of 64 hold 0..15 x4
+    """Values 0..15: mx side, scale -1, bias 15, code = 15 - x; element i of
+    a row in word i / 8, nibble i % 8 from the least significant end."""
+    x = np.tile(np.arange(16, dtype=np.float32), 8)
     codes, scales, biases = O.quantize(O.from_f32(x, "f16")[None], 4, 64)
-    assert O.to_f32(scales, "f16").tolist() == [[1.0, 1.0]] and O.to_f32(biases, "f16").tolist() == [[0.0, 0.0]]
-    assert codes[0, 0] == 0x76543210 and codes[0, 1] == 0xFEDCBA98  # least significant nibble first
+    assert scales.tolist() == [[0xBC00, 0xBC00]] and biases.tolist() == [[0x4B80, 0x4B80]]
+    assert codes[0, 0] == 0x89ABCDEF and codes[0, 1] == 0x01234567
     g = np.arange(64, dtype=np.float32)
-    g[63] = 255.0  # range 0..255 -> scale 1, bias 0
+    g[63] = 255.0  # range 0..255 -> scale -1, bias 255, code 255 - x
     c8, s8, b8 = O.quantize(O.from_f32(np.concatenate([g, g + 1]), "f16")[None], 8, 64)
-    assert O.to_f32(s8, "f16").tolist() == [[1.0, 1.0]] and O.to_f32(b8, "f16").tolist() == [[0.0, 1.0]]
-    assert c8[0, 0] == 0x03020100 and c8[0, 15] == 0xFF3E3D3C and c8[0, 16] == 0x03020100
+    assert O.to_f32(s8, "f16").tolist() == [[-1.0, -1.0]] and O.to_f32(b8, "f16").tolist() == [[255.0, 256.0]]
+    assert c8[0, 0] == 0xFCFDFEFF and c8[0, 15] == 0x00C1C2C3 and c8[0, 16] == 0xFCFDFEFF
+    assert c8[0, 31] == 0x00C1C2C3
 
 
 @pytest.mark.parametrize("bits", [4, 8])
 def test_codec_round_trip_bound(bits):
+    """codes come from the fp32 scale / bias, dequantization uses their fp16
+    roundings (within 2^-11 relative, 2^-24 absolute below 2^-14):
+    |w - x| <= |s| / 2 + code |s16 - s| + |b16 - b| for values inside the
+    code range.  scale = edge / rint(edge / scale0) can be up to half a code
+    smaller than scale0, so the far end of a group may fall past the last
+    code (by less than one) and is clipped there: error < 1.5 |s|."""
     x = O.fill_normal(71, 1, 0, (300, 128), "f16")
     codes, scales, biases = O.quantize(x, bits, 64)
-    deq = O.dequantize(codes, scales, biases, bits, 64)
-    xf = O.to_f32(x, "f16")
-    sf = np.repeat(O.to_f32(scales, "f16"), 64, axis=1)
-    bf = np.repeat(O.to_f32(biases, "f16"), 64, axis=1)
-    assert np.all(np.abs(deq - xf) <= 0.5 * sf + np.abs(bf) * 2 ** -10 + 1e-6)
+    deq = O.dequantize(codes, scales, biases, bits, 64).astype(np.float64)
+    xf = O.to_f32(x, "f16").astype(np.float64)
+    sf = np.abs(np.repeat(O.to_f32(scales, "f16"), 64, axis=1)).astype(np.float64)
+    bf = np.abs(np.repeat(O.to_f32(biases, "f16"), 64, axis=1)).astype(np.float64)
+    nbins = 2 ** bits - 1
+    per = 32 // bits
+    code = (codes[:, np.arange(128) // per] >> (bits * (np.arange(128) % per))) & nbins
+    rounding = sf * nbins * 2.0 ** -10 + bf * 2.0 ** -10 + 2.0 ** -20
+    err = np.abs(deq - xf)
+    inside = code < nbins
+    assert np.all(err[inside] <= 0.5 * sf[inside] + rounding[inside])
+    assert np.all(err <= 1.5 * sf + rounding)
+    # clipping happens at the far end only, and not for most groups
+    assert np.mean(err > 0.5 * sf + rounding) < 0.01
+    # the larger-magnitude end of every group round-trips to within its fp16 bias rounding
+    g = xf.reshape(300, 2, 64)
+    edge = np.where(np.abs(g.min(-1)) > np.abs(g.max(-1)), g.min(-1), g.max(-1))
+    assert np.array_equal(O.to_f32(biases, "f16"), edge.astype(np.float32))
     # constant rows round-trip exactly
     c = np.repeat(x[:1, :1], 128, axis=1)
     cc, cs, cb = O.quantize(np.ascontiguousarray(c), bits, 64)
     assert np.array_equal(O.dequantize(cc, cs, cb, bits, 64), O.to_f32(c, "f16"))
+
+
+# ------------------------------------------------------- quantized summary --
+
+def _qrow(codes_per_dim, bits):
+    """pack one 128-dim row of codes LSB first"""
+    per = 32 // bits
+    w = np.zeros(128 // per, np.uint32)
+    for i, cv in enumerate(codes_per_dim):
+        w[i // per] |= np.uint32(int(cv) << (bits * (i % per)))
+    return w
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_summary_q_constant_block(bits):
+    """Every token dequantizes to w = fmaf(s, c, b) = -0.5 * 3 + 2.25 = 0.75
+    (group 0) and fmaf(0.125, 1, -1) = -0.875 (group 1): short fp16 values,
+    so the fold of 64 (or 32) equal terms and the 1/Tb scaling are exact and
+    the summary is that value."""
+    for Tb in (32, 64):
+        codes = np.tile(_qrow([3] * 64 + [1] * 64, bits), (Tb, 1))
+        sc = np.tile(O.from_f32(np.array([-0.5, 0.125], np.float32), "f16"), (Tb, 1))
+        bi = np.tile(O.from_f32(np.array([2.25, -1.0], np.float32), "f16"), (Tb, 1))
+        s = O.to_f32(O.summaries_q(codes, sc, bi, Tb, bits, 64)[0], "f16")
+        assert np.all(s[:64] == 0.75) and np.all(s[64:] == -0.875)
+
+
+def test_summary_q_sequential_fold_order():
+    """dim 0 of a 64-token int4 block, from codes and per-token scales /
+    biases: token 0 16 * 2 + 0 = 32, token 1 -16 * 1 + 48 = 32 (negative
+    scale), token 2 2^-6 * 2 + 0 = 2^-5, tokens 3..63 2^-20 * 2 + 0 = 2^-19
+    (fp16 subnormals, exact).  The left fold from token 0 is 64 + 2^-5 (each
+    2^-19 is below half an ulp of 64 and lost), mean 1 + 2^-11, an fp16 tie
+    -> 0x3C00; the exact mean (or any order that adds the small terms first)
+    rounds to 0x3C01."""
+    Tb, bits = 64, 4
+    cd = np.zeros((Tb, 128), np.int64)
+    sc = np.zeros((Tb, 2), np.float32)
+    bi = np.zeros((Tb, 2), np.float32)
+    cd[0, 0], sc[0, 0] = 2, 16.0
+    cd[1, 0], sc[1, 0], bi[1, 0] = 1, -16.0, 48.0
+    cd[2, 0], sc[2, 0] = 2, 2.0 ** -6
+    cd[3:, 0], sc[3:, 0] = 2, 2.0 ** -20
+    codes = np.stack([_qrow(r, bits) for r in cd])
+    s16, b16 = O.from_f32(sc, "f16"), O.from_f32(bi, "f16")
+    assert np.array_equal(O.to_f32(s16, "f16"), sc)
+    s = O.summaries_q(codes, s16, b16, Tb, bits, 64)[0]
+    assert s[0] == 0x3C00
+    exact = (64 + 2.0 ** -5 + 61 * 2.0 ** -19) / 64
+    assert np.float16(exact).view(np.uint16) == 0x3C01
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_summary_q_within_one_ulp_of_exact_mean(bits):
+    Tb = 32
+    k = O.fill_normal(91, 1, 0, (Tb * 100, 128), "f16")
+    kq = O.quantize(k, bits, 64)
+    s = O.to_f32(O.summaries_q(*kq, Tb, bits, 64), "f16").astype(np.float64)
+    deq = O.dequantize(*kq, bits, 64).astype(np.float64)
+    exact = deq.reshape(100, Tb, 128).mean(axis=1)
+    rne = np.vectorize(lambda v: _rne_sig(v, 11))(exact)
+    assert np.mean(s == rne) > 0.999
+    ax = np.maximum(np.abs(exact), 2.0 ** -14)
+    assert np.all(np.abs(s - exact) <= 2.0 ** (np.floor(np.log2(ax)) - 10))
 
 
 def test_quantized_attention_matches_dequantized():
@@ -401,6 +585,37 @@ def test_quantized_attention_matches_dequantized():
     toks = np.concatenate([np.arange(j * Tb, min((j + 1) * Tb, T)) for j in idx])
     ref = numpy_attention(O.to_f32(q, "f16").astype(np.float64), kd[toks], vd[toks], 0.088)
     assert np.max(np.abs(out - ref)) < 1e-12
-    # summaries of dequantized keys: constant-block closed form
-    s = O.summaries_q(*kq, Tb, 8, 64)
-    assert s.shape == (T // Tb, 128)
+
+
+# ---------------------------------------------------- parallel layer-step --
+
+@pytest.mark.parametrize("bits", [0, 4, 8])
+def test_layer_step_equals_per_head_composition(bits):
+    """The OpenMP layer-step (the CPU baseline) is score -> select -> attend
+    of every (sequence, kv head), bit for bit what the per-head functions
+    give, whatever thread runs a pair."""
+    from common import make_workload
+    dt = "bf16" if bits == 0 else "f16"
+    Tb, T, K = 32, 32 * 24 + 7, 6
+    w = make_workload(95 + bits, B=3, Hq=16, Hkv=4, T=T, Tb=Tb, dtype=dt, top_k=K)
+    keys, values = np.stack(w.keys), np.stack(w.values)
+    if bits:
+        kq = [O.quantize(keys[b], bits, 64) for b in range(w.B)]
+        vq = [O.quantize(values[b], bits, 64) for b in range(w.B)]
+        kqs = tuple(np.stack([k[i] for k in kq]) for i in range(3))
+        vqs = tuple(np.stack([v[i] for v in vq]) for i in range(3))
+        summ = np.stack([[O.summaries_q(*(a[h] for a in kq[b]), Tb, bits, 64) for h in range(w.Hkv)]
+                         for b in range(w.B)])
+        idx, out = O.layer_step(w.q, summ, Tb, 1, 1, K, w.scale, dt, kq=kqs, vq=vqs, bits=bits)
+    else:
+        summ = np.stack([[O.summaries(keys[b, h], Tb, dt) for h in range(w.Hkv)] for b in range(w.B)])
+        idx, out = O.layer_step(w.q, summ, Tb, 1, 1, K, w.scale, dt, keys=keys, values=values)
+    for b in range(w.B):
+        for h in range(w.Hkv):
+            q = w.q[b, h * 4:(h + 1) * 4]
+            sel, n = O.select(O.score_blocks(q, summ[b, h], dt), T, Tb, 1, 1, K)
+            assert np.array_equal(idx[b, h], sel)
+            ref = (O.attend_q(q, tuple(a[h] for a in kq[b]), tuple(a[h] for a in vq[b]), Tb, bits, 64,
+                              sel[:n], w.scale) if bits else
+                   O.attend(q, keys[b, h], values[b, h], Tb, sel[:n], w.scale, dt))
+            assert np.array_equal(out[b, h * 4:(h + 1) * 4], ref)
