@@ -623,9 +623,27 @@ static SeqBatch make_batch(const std::vector<Entry>& es, int e0, int n, int qhs)
   return b;
 }
 
-// Selection, attention or both (the selection inside the attention kernel
-// when every entry's candidates fit one wave) for the entries, in launches
-// of at most kMaxBatch entries.  The score, bound, index and partial
+// Whether the fused decode of entries [e0, e0 + n) should read each entry's
+// length before its block summaries: when the rows the entries' held pages
+// cover are well below the block-table width, loading every row at once would
+// fetch mostly unused summaries.
+// (Entries with their own token count carry it in the launch arguments, so
+// knowing it first costs nothing.)
+static bool len_first(const bsattn_cache* c, const std::vector<Entry>& es, int e0, int n) {
+  const int tb = c->d.block_size;
+  int64_t held = 0;
+  bool given = true;
+  for (int i = 0; i < n; ++i) {
+    held += (visible(c, es[e0 + i]) + tb - 1) / tb;
+    given = given && es[e0 + i].len >= 0;
+  }
+  return given || 4 * held < 3 * (int64_t)n * c->d.max_blocks_per_seq;
+}
+
+// Selection, attention or both for the entries, in launches of at most
+// kMaxBatch entries: the fused decode kernel where it applies, else scoring
+// and selection inside the attention kernel when every entry's candidates
+// fit it, else separate selection.  The score, bound, index and partial
 // workspaces are per launch (launches on one stream run in order).
 enum class Op { Select, Attend, Decode };
 static int run_entries(bsattn_cache* c, Op op, const void* q, const std::vector<Entry>& es, int qhs,
@@ -646,7 +664,12 @@ static int run_entries(bsattn_cache* c, Op op, const void* q, const std::vector<
     if (op == Op::Select) {
       e = launch_select(g, b, qq, c->scores, c->err_ws, io, max_nc, s, prof);
     } else if (op == Op::Attend) {
-      e = launch_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, c->partials, s, prof);
+      if (fused_decode_ok(g, b.n, max_nc))
+        e = launch_fused_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, c->partials, s, prof);
+      else
+        e = launch_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, c->partials, s, prof);
+    } else if (fused_decode_ok(g, b.n, max_nc)) {
+      e = launch_fused_decode(g, b, qq, io, len_first(c, es, e0, b.n), scale, oo, c->partials, s, prof);
     } else if (max_nc > fused_select_limit(g.top_k)) {
       int32_t* sel = io ? io : c->idx_ws;
       e = launch_select(g, b, qq, c->scores, c->err_ws, sel, max_nc, s, prof);
@@ -719,7 +742,10 @@ int bsattn_append_decode(bsattn_cache* c, const void* k, const void* v, const vo
     if ((int64_t)c->len[sq] + 1 > (int64_t)c->d.max_blocks_per_seq * tb) one_launch = false;
     else max_nc = std::max(max_nc, candidates(g, c->len[sq] + 1));
   }
-  one_launch = one_launch && max_nc <= fused_select_limit(g.top_k);
+  // fused: the append launch, then the fused decode kernel (scoring inside);
+  // otherwise append + scoring in one launch, then selection + attention
+  const bool fused = one_launch && fused_decode_ok(g, n_seqs, max_nc);
+  one_launch = one_launch && (fused || max_nc <= fused_select_limit(g.top_k));
   if (!one_launch) {
     rc = bsattn_append(c, k, v, seq_ids, n_seqs, 1, stream);
     if (rc) return rc;
@@ -755,8 +781,8 @@ int bsattn_append_decode(bsattn_cache* c, const void* k, const void* v, const vo
   }
   Timing tm[kProfKinds];
   Timing* prof = prof_slots(c, s, tm);
-  hipError_t e = launch_append_decode(g, b, sp, pb, k, v, q, c->scores, idx_out, max_nc, scale, out,
-                                     c->partials, s, prof);
+  hipError_t e = launch_append_decode(g, b, sp, pb, k, v, q, c->scores, idx_out, max_nc, fused, scale,
+                                     out, c->partials, s, prof);
   prof_collect(c, prof);
   if (e != hipSuccess) return hip_fail(e, "append-decode launch");
   for (int sq : seqs) c->len[sq] += 1;

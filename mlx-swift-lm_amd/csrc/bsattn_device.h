@@ -683,7 +683,8 @@ __device__ __forceinline__ void wg_topk(const WgCand& wc, int c0, int nc, int K,
 
 // Block in output slot p of the selection for nb blocks: sinks [0, ns),
 // then the K ranked candidates (sel), then recent [nb - nr, nb); when the
-// candidates do not outnumber K every block is kept.
+// candidates do not outnumber K (ranked false) every block is kept.  sel is
+// read only when ranked and K > 0.
 __device__ __forceinline__ int selected_block(int p, int nb, bool ranked, int ns, int nr, int K,
                                               const int* sel) {
   if (!ranked) return p < nb ? p : -1;
@@ -907,16 +908,15 @@ __device__ __forceinline__ void store_empty(float* s_m, float* s_l, float (*s_o)
 }
 
 // Merges the W waves' (m, l, o) (after a workgroup barrier) and writes the
-// normalised output (one split) or the unnormalised partial (o, m, l) for
-// k_combine.
+// normalised output (nsplit == 1) or the unnormalised partial (o, m, l) of
+// split `split` of nsplit for k_combine.
 template <int DT, int G, int W>
 __device__ __forceinline__ void attend_merge(const Geometry& geo, const SeqBatch& sb, int bi, int h,
-                                             int split,
+                                             int split, int nsplit,
                                              const float (*s_m)[16], const float (*s_l)[16],
                                              const float (*s_o)[G][kHeadDim],
                                              uint16_t* __restrict__ out,
                                              float* __restrict__ partials) {
-  const int nsplit = geo.nsplit;
   // per head: the maximum M over the waves, each wave's weight exp2(m_w - M)
   // and the merged sum L, once (thread h < G), for all 128 dims
   __shared__ float s_f[W][16], s_ML[2][16];

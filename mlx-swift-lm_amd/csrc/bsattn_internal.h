@@ -143,14 +143,38 @@ hipError_t launch_decode_attend(const Geometry& g, const SeqBatch& b, const void
                                 int32_t* idx_out, int max_nc, float scale, void* out,
                                 float* partials, hipStream_t s, Timing* prof);
 // one decode step of a 16-bit cache with one new token per entry (b.len =
-// the lengths after it): the patches pb, the appends (k / v [n, Hkv, 1, D]
-// into the pages sp) and the scoring in one launch, then the selection +
-// attention (+ combine) launches of launch_decode.  Requires max_nc <=
-// fused_select_limit(top_k) (and recent >= 1, which every cache has).
+// the lengths after it): the patches pb and the appends (k / v [n, Hkv, 1, D]
+// into the pages sp) in one launch, then the fused decode kernel (fused:
+// requires fused_decode_ok), or with the scoring in the append launch and
+// then the selection + attention (+ combine) launches of launch_decode
+// (requires max_nc <= fused_select_limit(top_k)).  Every cache has recent
+// >= 1, so the block an append completes is forced, never scored.
 hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
                                 const PatchBatch& pb, const void* k, const void* v, const void* q,
-                                float* scores, int32_t* idx_out, int max_nc, float scale,
+                                float* scores, int32_t* idx_out, int max_nc, bool fused, float scale,
                                 void* out, float* partials, hipStream_t s, Timing* prof);
+// split combine of nsplit partials per (entry, q head) into out
+hipError_t launch_combine(const Geometry& g, const SeqBatch& b, const float* partials, int nsplit,
+                          void* out, hipStream_t s, Timing* prof);
+// fused decode (bsattn_decode.hip): scoring, selection, gather + attention
+// (+ combine) for 16-bit caches with GQA groups up to 4; fused_decode_ok
+// tells whether a launch of n entries with at most max_nc candidate blocks
+// each fits it.  len_first: each workgroup reads its entry's length before
+// the summaries (for ragged batches; otherwise every row of the block-table
+// width is read at once).  idx_out may be null.
+bool fused_decode_ok(const Geometry& g, int n, int max_nc);
+// exact (canonical) block scores of every ranked candidate into `scores`
+hipError_t launch_score(const Geometry& g, const SeqBatch& b, const void* q, float* scores, int max_nc,
+                        hipStream_t s, Timing* prof);
+
+hipError_t launch_fused_decode(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx_out,
+                               bool len_first, float scale, void* out, float* partials,
+                               hipStream_t s, Timing* prof);
+// the same kernel's gather + attention over given indices (used by
+// bsattn_attend exactly where decode takes the fused path, so that
+// decode == select + attend bit for bit)
+hipError_t launch_fused_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
+                               float scale, void* out, float* partials, hipStream_t s, Timing* prof);
 // dense causal attention of the last L tokens of each sequence
 hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
                           void* out, hipStream_t s, Timing* prof);

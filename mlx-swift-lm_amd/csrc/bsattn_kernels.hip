@@ -267,8 +267,9 @@ __global__ __launch_bounds__(64) void k_topk(Geometry geo, SeqBatch sb,
   const bool ranked = ranked_select(geo, nc);
   int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
   if (ranked) wave_topk(wc, c0, nc, geo.top_k, s_sel, nullptr, s_ws);
+  // (top_k 0 with candidates: sinks and recent only, no selection)
   for (int p = lane; p < geo.nsel_max; p += 64)
-    out[p] = selected_block(p, nb, ranked, geo.ns, geo.nr, geo.top_k, s_sel);
+    out[p] = selected_block(p, nb, nc > geo.top_k, geo.ns, geo.nr, geo.top_k, s_sel);
 }
 
 // ---------------------------------------------------------------------------
@@ -434,7 +435,7 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
     store_empty<G>(s_m[wave], s_l[wave], s_o[wave], lane);
   }
   __syncthreads();
-  attend_merge<DT, G, W>(geo, sb, bi, h, split, s_m, s_l, s_o, out, partials);
+  attend_merge<DT, G, W>(geo, sb, bi, h, split, geo.nsplit, s_m, s_l, s_o, out, partials);
 }
 
 // ---------------------------------------------------------------------------
@@ -456,12 +457,12 @@ __device__ __forceinline__ float block_reduce_128(float v, bool is_max, float* s
 template <int DT>
 __global__ __launch_bounds__(128) void k_combine(Geometry geo, SeqBatch sb,
                                                  const float* __restrict__ partials,
-                                                 uint16_t* __restrict__ out) {
+                                                 uint16_t* __restrict__ out, int nsplit) {
   __shared__ float s_w[kMaxSplits];
   __shared__ float s_red[2];
   const int hq = blockIdx.x, bi = blockIdx.y, d = threadIdx.x;
   const size_t row = (size_t)bi * geo.hq + hq;
-  const int ns = geo.nsplit;
+  const int ns = nsplit;
   const float* pp = partials + row * ns * (kHeadDim + 2);
   float M = -INFINITY;
   for (int sp = d; sp < ns; sp += 128) M = fmaxf(M, pp[sp * (kHeadDim + 2) + kHeadDim]);
@@ -600,8 +601,8 @@ static bool wave_selectable(const Geometry& g, int max_nc) {
 }
 
 // exact (canonical) scores of every ranked candidate
-static hipError_t score_exact(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                              int max_nc, hipStream_t s, Timing* prof) {
+hipError_t launch_score(const Geometry& g, const SeqBatch& b, const void* q, float* scores, int max_nc,
+                        hipStream_t s, Timing* prof) {
   if (!ranked_select(g, max_nc)) return hipSuccess;
   // 32-candidate chunks while the 64-candidate grid has at most 1024
   // workgroups (8 sequences x 8 kv heads at 32k tokens: 512 -> 1024
@@ -624,7 +625,7 @@ hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, fl
   const bool small = wave_selectable(g, max_nc);
   if (!small && g.group >= 8)  // MFMA scores + exact rescoring of the band
     return launch_select_large(g, b, q, scores, err, max_nc, idx, s, prof, false);
-  hipError_t e = score_exact(g, b, q, scores, max_nc, s, prof);
+  hipError_t e = launch_score(g, b, q, scores, max_nc, s, prof);
   if (e != hipSuccess) return e;
   if (!small) return launch_select_large(g, b, q, scores, err, max_nc, idx, s, prof, true);
   launch(k_topk, dim3(g.hkv, b.n), dim3(64), 0, s, prof, kProfTopk, g, b, (const float*)scores, idx);
@@ -667,11 +668,16 @@ static hipError_t attend_impl(const Geometry& g, const SeqBatch& b, const void* 
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || g.nsplit == 1) return e;
-  const float* pc = partials;
+  return launch_combine(g, b, partials, g.nsplit, out, s, prof);
+}
+
+hipError_t launch_combine(const Geometry& g, const SeqBatch& b, const float* partials, int nsplit,
+                          void* out, hipStream_t s, Timing* prof) {
+  uint16_t* oo = (uint16_t*)out;
   if (g.dtype == 0)
-    launch(k_combine<0>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, b, pc, oo);
+    launch(k_combine<0>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, b, partials, oo, nsplit);
   else
-    launch(k_combine<1>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, b, pc, oo);
+    launch(k_combine<1>, dim3(g.hq, b.n), dim3(128), 0, s, prof, kProfCombine, g, b, partials, oo, nsplit);
   return hipGetLastError();
 }
 
@@ -700,19 +706,20 @@ hipError_t launch_decode_attend(const Geometry& g, const SeqBatch& b, const void
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                          int32_t* idx_out, int max_nc, float scale, void* out,
                          float* partials, hipStream_t s, Timing* prof) {
-  hipError_t e = score_exact(g, b, q, scores, max_nc, s, prof);
+  hipError_t e = launch_score(g, b, q, scores, max_nc, s, prof);
   if (e != hipSuccess) return e;
   return launch_decode_attend(g, b, q, scores, idx_out, max_nc, scale, out, partials, s, prof);
 }
 
 hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
                                 const PatchBatch& pb, const void* k, const void* v, const void* q,
-                                float* scores, int32_t* idx_out, int max_nc, float scale,
+                                float* scores, int32_t* idx_out, int max_nc, bool fused, float scale,
                                 void* out, float* partials, hipStream_t s, Timing* prof) {
-  // the scoring chunk size follows score_exact
+  // the scoring chunk size follows launch_score; the fused decode scores
+  // itself, so its append launch has no scoring workgroups
   const bool small = (int64_t)((max_nc + 63) / 64) * g.hkv * b.n <= 1024;
   const int ch = small ? 32 : 64;
-  const int chunks = ranked_select(g, max_nc) ? (max_nc + ch - 1) / ch : 0;
+  const int chunks = !fused && ranked_select(g, max_nc) ? (max_nc + ch - 1) / ch : 0;
   const uint16_t *kk = (const uint16_t*)k, *vv = (const uint16_t*)v, *qq = (const uint16_t*)q;
   if (g.dtype == 0) {
     if (small) append_score_dispatch<0, 32>(g, b, sp, pb, chunks, kk, vv, qq, scores, s, prof);
@@ -723,6 +730,7 @@ hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const Step
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (fused) return launch_fused_decode(g, b, q, idx_out, true, scale, out, partials, s, prof);
   return launch_decode_attend(g, b, q, scores, idx_out, max_nc, scale, out, partials, s, prof);
 }
 

@@ -434,7 +434,7 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
     store_empty<G>(s_m[wave], s_l[wave], s_o[wave], lane);
   }
   __syncthreads();
-  attend_merge<0, G, W>(geo, sb, bi, h, split, s_m, s_l, s_o, out, partials);
+  attend_merge<0, G, W>(geo, sb, bi, h, split, geo.nsplit, s_m, s_l, s_o, out, partials);
 }
 
 // ---------------------------------------------------------------------------

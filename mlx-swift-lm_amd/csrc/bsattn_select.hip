@@ -454,8 +454,9 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int nc = nb - geo.nr - c0;
   int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
-  if (!ranked_select(geo, nc)) {  // every block is kept
-    for (int p = tid; p < geo.nsel_max; p += kSelThreads) out[p] = p < nb ? p : -1;
+  if (!ranked_select(geo, nc)) {  // every block kept, or (top_k 0) sinks and recent only
+    for (int p = tid; p < geo.nsel_max; p += kSelThreads)
+      out[p] = selected_block(p, nb, nc > K, geo.ns, geo.nr, K, nullptr);
     return;
   }
   uint32_t kr[PER];
