@@ -137,6 +137,21 @@ int bsattn_decode(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
                   int32_t n_seqs, float scale, void* out, int32_t* idx_out,
                   void* stream);
 
+/* bsattn_decode without any allocation, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * it).  No counterpart in the reference.  The same kernels and results, bit
+ * for bit, as bsattn_decode; its workspaces (block scores, score bounds,
+ * indices, split partials) live in a fixed 16 MiB device scratch that every
+ * call on one GPU shares (each GPU holds its own until the process ends),
+ * and nothing is allocated on the device or the host.  At most 64
+ * sequences per call; a call whose workspaces exceed the scratch fails with
+ * BSATTN_ERR_RANGE.  Calls on one GPU that may overlap (other streams, other
+ * threads, other caches) race on the scratch: serialize them.  Profiling is
+ * not recorded. */
+int bsattn_decode_noalloc(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
+                          int32_t n_seqs, float scale, void* out, int32_t* idx_out,
+                          void* stream);
+
 /* One decode step of attentionWithCacheUpdate (AttentionUtils.swift:37-77
  * with L = 1: cache.update(keys:values:), KVCache.swift:328-371, then the
  * decode attention, AttentionUtils.swift:68-75) in one call: appends one

@@ -36,6 +36,7 @@ EXPORTS = (
     "bsattn_select",
     "bsattn_attend",
     "bsattn_decode",
+    "bsattn_decode_noalloc",
     "bsattn_append_decode",
     "bsattn_decode_multi",
     "bsattn_prefill",
@@ -119,6 +120,7 @@ def lib() -> ctypes.CDLL:
         "bsattn_select": (ctypes.c_int, [P, P, PI32, i32, P, P]),
         "bsattn_attend": (ctypes.c_int, [P, P, PI32, i32, P, ctypes.c_float, P, P]),
         "bsattn_decode": (ctypes.c_int, [P, P, PI32, i32, ctypes.c_float, P, P, P]),
+        "bsattn_decode_noalloc": (ctypes.c_int, [P, P, PI32, i32, ctypes.c_float, P, P, P]),
         "bsattn_append_decode": (ctypes.c_int, [P, P, P, P, PI32, i32, ctypes.c_float, P, P, P]),
         "bsattn_decode_multi": (ctypes.c_int, [P, P, PI32, i32, i32, ctypes.c_float, P, P, P]),
         "bsattn_prefill": (ctypes.c_int, [P, P, PI32, i32, i32, ctypes.c_float, P, P]),

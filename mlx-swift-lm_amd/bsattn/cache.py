@@ -299,6 +299,25 @@ class BlockSparseKVCache:
                                   ctypes.c_float(scale), _ptr(out), idx_p, _stream(self.device)))
         return out
 
+    def decodeNoAlloc(self, queries: torch.Tensor, scale: float, out: torch.Tensor,
+                      seq_ids: Optional[Sequence[int]] = None,
+                      idx_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """decode() through bsattn_decode_noalloc: the same results, with the
+        workspaces in the library's fixed per-GPU scratch and nothing
+        allocated (the caller brings `out`, [B, Hq, 1, D]); at most 64
+        sequences; calls that overlap on one GPU race."""
+        B = self._check_q(queries)
+        if out.shape != queries.shape or out.dtype != queries.dtype or not out.is_contiguous():
+            raise ValueError("out must be a contiguous tensor shaped and typed like queries")
+        idx_p = None
+        if idx_out is not None:
+            if idx_out.dtype != torch.int32 or tuple(idx_out.shape) != (B, self.desc.num_kv_heads, self.nselMax):
+                raise ValueError("idx_out must be int32 [B, Hkv, nselMax]")
+            idx_p = _ptr(idx_out)
+        check(lib().bsattn_decode_noalloc(self._h, _ptr(queries), i32_array(seq_ids), B,
+                                          ctypes.c_float(scale), _ptr(out), idx_p, _stream(self.device)))
+        return out
+
     def appendDecode(self, keys: torch.Tensor, values: torch.Tensor, queries: torch.Tensor,
                      scale: float, seq_ids: Optional[Sequence[int]] = None,
                      idx_out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -611,7 +611,7 @@ static int visible(const bsattn_cache* c, const Entry& e) {
 }
 
 // the launch batch for entries [e0, e0 + n); q / out offsets relative to entry e0
-static SeqBatch make_batch(const std::vector<Entry>& es, int e0, int n, int qhs) {
+static SeqBatch make_batch(const Entry* es, int e0, int n, int qhs) {
   SeqBatch b{};
   b.n = n;
   b.qhs = qhs;
@@ -629,7 +629,7 @@ static SeqBatch make_batch(const std::vector<Entry>& es, int e0, int n, int qhs)
 // fetch mostly unused summaries.
 // (Entries with their own token count carry it in the launch arguments, so
 // knowing it first costs nothing.)
-static bool len_first(const bsattn_cache* c, const std::vector<Entry>& es, int e0, int n) {
+static bool len_first(const bsattn_cache* c, const Entry* es, int e0, int n) {
   const int tb = c->d.block_size;
   int64_t held = 0;
   bool given = true;
@@ -640,15 +640,31 @@ static bool len_first(const bsattn_cache* c, const std::vector<Entry>& es, int e
   return given || 4 * held < 3 * (int64_t)n * c->d.max_blocks_per_seq;
 }
 
+// Device workspaces of one launch (rows = the launch's batch entries):
+// block scores [rows][hkv][sstride] + kScoreSlack, MFMA score bounds
+// [rows][hkv][mfma_err_stride], indices [rows][hkv][nsel_max], split
+// partials [rows][hq][nsplit][D + 2].
+struct Workspace {
+  float* scores;
+  float* err;
+  int32_t* idx;
+  float* partials;
+};
+
+static Workspace cache_workspace(const bsattn_cache* c) {
+  return Workspace{c->scores, c->err_ws, c->idx_ws, c->partials};
+}
+
 // Selection, attention or both for the entries, in launches of at most
 // kMaxBatch entries: the fused decode kernel where it applies, else scoring
 // and selection inside the attention kernel when every entry's candidates
-// fit it, else separate selection.  The score, bound, index and partial
-// workspaces are per launch (launches on one stream run in order).
+// fit it, else separate selection.  The workspaces are per launch (launches
+// on one stream run in order).  profile: time the launches when profiling
+// is on.
 enum class Op { Select, Attend, Decode };
-static int run_entries(bsattn_cache* c, Op op, const void* q, const std::vector<Entry>& es, int qhs,
-                       const int32_t* idx_in, int32_t* idx_out, float scale, void* out, hipStream_t s) {
-  const int n = (int)es.size();
+static int run_entries(bsattn_cache* c, Op op, const void* q, const Entry* es, int n, int qhs,
+                       const int32_t* idx_in, int32_t* idx_out, float scale, void* out, hipStream_t s,
+                       const Workspace& ws, bool profile = true) {
   const Geometry& g = c->geo;
   const size_t idx_row = (size_t)g.hkv * g.nsel_max;
   for (int e0 = 0; e0 < n; e0 += kMaxBatch) {
@@ -659,23 +675,23 @@ static int run_entries(bsattn_cache* c, Op op, const void* q, const std::vector<
     uint16_t* oo = out ? (uint16_t*)out + es[e0].qoff : nullptr;
     int32_t* io = idx_out ? idx_out + e0 * idx_row : nullptr;
     Timing tm[kProfKinds];
-    Timing* prof = prof_slots(c, s, tm);
+    Timing* prof = profile ? prof_slots(c, s, tm) : nullptr;
     hipError_t e = hipSuccess;
     if (op == Op::Select) {
-      e = launch_select(g, b, qq, c->scores, c->err_ws, io, max_nc, s, prof);
+      e = launch_select(g, b, qq, ws.scores, ws.err, io, max_nc, s, prof);
     } else if (op == Op::Attend) {
       if (fused_decode_ok(g, b.n, max_nc))
-        e = launch_fused_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, c->partials, s, prof);
+        e = launch_fused_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, ws.partials, s, prof);
       else
-        e = launch_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, c->partials, s, prof);
+        e = launch_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, ws.partials, s, prof);
     } else if (fused_decode_ok(g, b.n, max_nc)) {
-      e = launch_fused_decode(g, b, qq, io, len_first(c, es, e0, b.n), scale, oo, c->partials, s, prof);
+      e = launch_fused_decode(g, b, qq, io, len_first(c, es, e0, b.n), scale, oo, ws.partials, s, prof);
     } else if (max_nc > fused_select_limit(g.top_k)) {
-      int32_t* sel = io ? io : c->idx_ws;
-      e = launch_select(g, b, qq, c->scores, c->err_ws, sel, max_nc, s, prof);
-      if (e == hipSuccess) e = launch_attend(g, b, qq, sel, scale, oo, c->partials, s, prof);
+      int32_t* sel = io ? io : ws.idx;
+      e = launch_select(g, b, qq, ws.scores, ws.err, sel, max_nc, s, prof);
+      if (e == hipSuccess) e = launch_attend(g, b, qq, sel, scale, oo, ws.partials, s, prof);
     } else {
-      e = launch_decode(g, b, qq, c->scores, io, max_nc, scale, oo, c->partials, s, prof);
+      e = launch_decode(g, b, qq, ws.scores, io, max_nc, scale, oo, ws.partials, s, prof);
     }
     prof_collect(c, prof);
     if (e != hipSuccess) return hip_fail(e, op == Op::Select ? "select launch" : op == Op::Attend ? "attend launch" : "decode launch");
@@ -691,8 +707,9 @@ int bsattn_select(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
-  return run_entries(c, Op::Select, q, entries(c, seqs, 1), kHeadDim, nullptr, idx_out, 0.0f, nullptr,
-                     (hipStream_t)stream);
+  const std::vector<Entry> es = entries(c, seqs, 1);
+  return run_entries(c, Op::Select, q, es.data(), (int)es.size(), kHeadDim, nullptr, idx_out, 0.0f, nullptr,
+                     (hipStream_t)stream, cache_workspace(c));
 } catch (...) {
   return on_exception();
 }
@@ -705,8 +722,9 @@ int bsattn_attend(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
-  return run_entries(c, Op::Attend, q, entries(c, seqs, 1), kHeadDim, idx, nullptr, scale, out,
-                     (hipStream_t)stream);
+  const std::vector<Entry> es = entries(c, seqs, 1);
+  return run_entries(c, Op::Attend, q, es.data(), (int)es.size(), kHeadDim, idx, nullptr, scale, out,
+                     (hipStream_t)stream, cache_workspace(c));
 } catch (...) {
   return on_exception();
 }
@@ -719,8 +737,57 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   if (rc) return rc;
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
-  return run_entries(c, Op::Decode, q, entries(c, seqs, 1), kHeadDim, nullptr, idx_out, scale, out,
-                     (hipStream_t)stream);
+  const std::vector<Entry> es = entries(c, seqs, 1);
+  return run_entries(c, Op::Decode, q, es.data(), (int)es.size(), kHeadDim, nullptr, idx_out, scale, out,
+                     (hipStream_t)stream, cache_workspace(c));
+} catch (...) {
+  return on_exception();
+}
+
+int bsattn_decode_noalloc(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
+                          float scale, void* out, int32_t* idx_out, void* stream) try {
+  // no device or host allocation on the way: the entries live on the stack,
+  // the workspaces in the device's fixed scratch, profiling is not recorded
+  if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (int rs = check_synced(c)) return rs;
+  if (n_seqs < 1 || n_seqs > kMaxBatch || n_seqs > c->d.max_seqs)
+    return fail(BSATTN_ERR_RANGE, "n_seqs %d out of range [1, %d] for the no-allocation decode", n_seqs,
+                std::min(kMaxBatch, c->d.max_seqs));
+  const Geometry& g = c->geo;
+  Entry es[kMaxBatch];
+  for (int i = 0; i < n_seqs; ++i) {
+    const int sq = seq_ids ? seq_ids[i] : i;
+    if (sq < 0 || sq >= c->d.max_seqs)
+      return fail(BSATTN_ERR_RANGE, "sequence id %d out of range [0, %d)", sq, c->d.max_seqs);
+    for (int j = 0; j < i; ++j)
+      if (es[j].seq == sq) return fail(BSATTN_ERR_INVALID, "sequence id %d listed twice", sq);
+    es[i] = Entry{sq, -1, (int64_t)i * g.hq * kHeadDim};
+  }
+  // workspaces of one launch of n_seqs rows, each 256-byte aligned
+  const size_t rows = (size_t)n_seqs;
+  size_t used = 0;
+  auto take = [&used](size_t bytes) {
+    const size_t at = used;
+    used += (bytes + 255) & ~(size_t)255;
+    return at;
+  };
+  const size_t o_sc = take((rows * g.hkv * g.sstride + kScoreSlack) * 4);
+  const size_t o_err = take(rows * g.hkv * mfma_err_stride(g) * 4);
+  const size_t o_idx = take(rows * g.hkv * g.nsel_max * 4);
+  const size_t o_part = take(rows * g.hq * g.nsplit * (kHeadDim + 2) * 4);
+  if (used > kNoAllocScratchBytes)
+    return fail(BSATTN_ERR_RANGE,
+                "the decode of %d sequences needs %zu bytes of workspace; the no-allocation scratch holds %zu "
+                "(decode fewer sequences per call, or use bsattn_decode)",
+                n_seqs, used, kNoAllocScratchBytes);
+  DeviceGuard dg(c->d.device);
+  if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
+  void* base = nullptr;
+  HIP_TRY(noalloc_scratch(c->d.device, &base), "hipGetSymbolAddress(scratch)");
+  char* b = (char*)base;
+  const Workspace ws{(float*)(b + o_sc), (float*)(b + o_err), (int32_t*)(b + o_idx), (float*)(b + o_part)};
+  return run_entries(c, Op::Decode, q, es, n_seqs, kHeadDim, nullptr, idx_out, scale, out, (hipStream_t)stream,
+                     ws, false);
 } catch (...) {
   return on_exception();
 }
@@ -806,8 +873,9 @@ int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, 
                   n_query);
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
-  return run_entries(c, Op::Decode, q, entries(c, seqs, n_query), n_query * kHeadDim, nullptr, idx_out,
-                     scale, out, (hipStream_t)stream);
+  const std::vector<Entry> es = entries(c, seqs, n_query);
+  return run_entries(c, Op::Decode, q, es.data(), (int)es.size(), n_query * kHeadDim, nullptr, idx_out,
+                     scale, out, (hipStream_t)stream, cache_workspace(c));
 } catch (...) {
   return on_exception();
 }

@@ -17,6 +17,8 @@ constexpr int kMaxPatch = 240;  // metadata words patched per launch
 #endif
 constexpr int kWaves = BSATTN_WAVES;  // waves per attention workgroup (one block each)
 constexpr int kMaxSplits = 512;       // attention splits per (sequence, kv head)
+// device scratch of the no-allocation decode (bsattn_noalloc.hip), per GPU
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
 // floats after the last block-score row: the workgroup selection reads a
 // thread's candidates as whole vectors, up to 12 x 1024 entries from a row
 // start, and the entries past the row are never candidates
@@ -91,6 +93,10 @@ struct Timing {
   hipEvent_t start = nullptr, stop = nullptr;
   bool used = false;
 };
+
+// address of the no-allocation scratch on `device`, which must be current
+// (looked up once per device; bsattn_noalloc.hip)
+hipError_t noalloc_scratch(int device, void** out);
 
 // launchers (bsattn_kernels.hip); return hipError_t of the launch
 hipError_t launch_patch(const Geometry& g, const PatchBatch& pb, hipStream_t s);
