@@ -20,8 +20,9 @@ Other workloads (one JSON line each, not the headline):
                tokens, 32-token blocks, top-128 + sink + 4 recent; adds the
                per-head recall of the selection against exact dense
                attention mass on two sequences of layer 0;
-  --config c4  decode loop with appends: B=32, fp16, lengths U[8192, 65536],
-               pages of the sequences interleaved in the pool, 256 steps of
+  --config c4  decode loop with appends: B=32, fp16, lengths U[8192, 65536]
+               (seeded counter stream), pages taken from a seeded
+               permutation of the free list (shuffled physical order), 256 steps of
                (append one token per sequence, score + top-32 + attend) as
                one appendDecode call each (append + scoring in one launch;
                the two-call figure is reported beside it); eager, since
@@ -333,6 +334,29 @@ def replay_distribution(run, reps: int, per: int):
             "reps": reps}
 
 
+def copy_bandwidth(torch, dev, mib: int = 1024, reps: int = 10) -> dict:
+    """Same-run HBM reference point: torch's device copy of `mib` MiB (read +
+    written), median of `reps` event-timed copies."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(src)
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b))
+    del src, dst
+    ms = sorted(ts)[len(ts) // 2]
+    gbps = 2 * (mib << 20) / (ms * 1e-3) / 1e9
+    return {"value": round(gbps, 1), "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "what": f"torch copy_ of {mib} MiB fp32 on the bench's GPU (read + written bytes / "
+                    f"event time), median of {reps}"}
+
+
 def bench_layers(args, cfg: Config):
     import torch
     import bsattn
@@ -488,6 +512,8 @@ def bench_layers(args, cfg: Config):
                                     f"median of {nd} repetitions, x{cfg.B} sequences"}
         log(f"[bench] cpu dense (reference path): {dense_us:.0f} us/layer-step, {thr} threads")
 
+    copy_bw = copy_bandwidth(torch, dev)
+    log(f"[bench] same-run copy bandwidth: {copy_bw['value']} GB/s")
     traffic, traffic_src = recorded_traffic(cfg)
     kv = cfg.dtype if cfg.bits == 0 else f"int{cfg.bits} affine, group 64, fp16 scale/bias"
     result = {
@@ -523,6 +549,8 @@ def bench_layers(args, cfg: Config):
                                      "frac": round(given_achieved / HBM_PEAK_GBPS, 4),
                                      "combine_us": round(given_combine_us, 3)}},
         "decode_kernels_us": decode_kernels,
+        "copy_bandwidth": copy_bw,
+        "attend_frac_of_copy": round(achieved / copy_bw["value"], 4),
         "layer_step_GBps": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "eager_us_per_layer_step": round(eager_ms * 1e3 / L, 3),
         "us_per_layer_step_distribution": dist,
@@ -534,6 +562,16 @@ def bench_layers(args, cfg: Config):
     print(json.dumps(result), flush=True)
 
 
+def _hash3(seed: int, stream: int, index: int) -> int:
+    """splitmix64 finaliser chained over (seed, stream, index)."""
+    def mix(x):
+        z = (x + 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & 0xFFFFFFFFFFFFFFFF
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & 0xFFFFFFFFFFFFFFFF
+        return z ^ (z >> 31)
+    return mix((mix((mix(seed) + stream) & 0xFFFFFFFFFFFFFFFF) + index) & 0xFFFFFFFFFFFFFFFF)
+
+
 def bench_loop(args):
     """Config 4: decode loop with appends, eager (page tables change every step)."""
     import numpy as np
@@ -541,10 +579,10 @@ def bench_loop(args):
     import bsattn
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    B, HQ, HKV, TB, K, STEPS = 32, 32, 8, 64, 32, 256
+    B, HQ, HKV, TB, K, STEPS, SEED = 32, 32, 8, 64, 32, 256, 1004
     steps = args.steps if args.steps != 20 else STEPS
-    rng = np.random.default_rng(4)
-    lens = rng.integers(8192, 65536 + 1, size=B)
+    # lengths U[8192, 65536] from the counter-based stream 4 of seed 1004
+    lens = np.array([8192 + _hash3(SEED, 4, b) % (65536 - 8192 + 1) for b in range(B)], np.int64)
     g = torch.Generator(device=dev)
     g.manual_seed(4004)
     mbps = (int(lens.max()) + steps) // TB + 2
@@ -553,20 +591,20 @@ def bench_loop(args):
                                       block_size=TB, dtype=torch.float16, top_k=K, sink_blocks=1,
                                       recent_blocks=1, max_blocks_per_seq=mbps, num_pages=pages,
                                       device=0)
-    # prefill in random-size chunks, sequences in random order each round, so
-    # every sequence's pages are scattered through the pool
+    # the physical page order is the free list permuted from the seed (stream
+    # 5): every sequence's pages are scattered through the pool
+    cache.shuffleFreePages(SEED)
     t0 = time.time()
-    pos = np.zeros(B, np.int64)
-    while (pos < lens).any():
-        for b in rng.permutation(B):
-            if pos[b] >= lens[b]:
-                continue
-            n = int(min(lens[b] - pos[b], rng.integers(256, 4096)))
-            k = torch.randn(1, HKV, n, D, device=dev, generator=g).half()
-            v = torch.randn(1, HKV, n, D, device=dev, generator=g).half()
-            cache.append(k, v, seq_ids=[int(b)])
-            pos[b] += n
+    for b in range(B):
+        n = int(lens[b])
+        k = torch.randn(1, HKV, n, D, device=dev, generator=g).half()
+        v = torch.randn(1, HKV, n, D, device=dev, generator=g).half()
+        cache.append(k, v, seq_ids=[b])
+        del k, v
     torch.cuda.synchronize()
+    bt = cache.seqPages(0)
+    log(f"[bench] c4: seq 0 pages {bt[:6]}... ({len(bt)} pages, ascending runs: "
+        f"{sum(1 for a, c in zip(bt, bt[1:]) if c == a + 1)} of {len(bt) - 1})")
     log(f"[bench] c4: prefilled {B} sequences ({int(lens.sum())} tokens) in {time.time() - t0:.1f}s")
     kn = torch.randn(steps + args.warmup, B, HKV, 1, D, device=dev, generator=g).half()
     vn = torch.randn(steps + args.warmup, B, HKV, 1, D, device=dev, generator=g).half()
@@ -647,17 +685,19 @@ def bench_loop(args):
         "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": steps,
         "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 5), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "f16",
-        "data": "synthetic: torch RNG on device, K/V/q ~ N(0,1); lengths from numpy seed 4",
+        "data": "synthetic: torch RNG on device, K/V/q ~ N(0,1); lengths from splitmix64 "
+                "(seed 1004, stream 4); physical page order shuffled from seed 1004 (stream 5)",
         "config": {"workload": "decode loop: append 1 token per sequence, score + top-K + attend",
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
                    "lengths": [int(x) for x in lens], "block_size": TB, "top_k": K,
-                   "sink_blocks": 1, "recent_blocks": 1, "pages": pages,
+                   "sink_blocks": 1, "recent_blocks": 1, "pages": pages, "page_order": "shuffled",
                    "timing": "eager wall clock per step (ctypes launches included)",
                    "step_call": "appendDecode (append + scoring in one launch)"},
         "two_calls_us_per_step": round(us_two, 3),
         "kernels_us_per_step": kern, "kernel_us_per_step_total": round(total, 3),
         "graph_us_per_step": round(us_graph, 3),
         "graph_step_us_distribution": dist,
+        "copy_bandwidth": copy_bandwidth(torch, dev),
         "gather_bytes_per_step": gather,
         "gather_GBps_at_kernel_time": round(gather / (total * 1e-6) / 1e9, 1) if total else None,
     }
@@ -685,7 +725,9 @@ def bench_prefill(args, bits=0):
                                       max_blocks_per_seq=T // TB + 2, device=0)
         for b in range(B):
             k = torch.randn(1, HKV, T, D, device=dev, generator=g).to(dt)
-            c.append(k, k, seq_ids=[b])
+            v = torch.randn(1, HKV, T, D, device=dev, generator=g).to(dt)
+            c.append(k, v, seq_ids=[b])
+            del k, v
         caches.append(c)
     q = torch.randn(B, HQ, L, D, device=dev, generator=g).to(dt)
     scale = 1.0 / math.sqrt(D)

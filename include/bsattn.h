@@ -88,6 +88,21 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out);
 int bsattn_cache_destroy(bsattn_cache* cache);
 int bsattn_cache_info(const bsattn_cache* cache, bsattn_info* out);
 
+/* Permutes the pages no sequence holds, from a seed (Fisher-Yates keyed by
+ * splitmix64 over (seed, stream 5, index)), so that later appends take their
+ * pages in a shuffled physical order.  Results never depend on the physical
+ * order; this reproduces the scattered layouts a long-running pool reaches.
+ * No reference counterpart (the reference's caches are contiguous,
+ * KVCache.swift:328-371).  Host only: nothing is enqueued. */
+int bsattn_shuffle_free_pages(bsattn_cache* cache, uint64_t seed);
+
+/* Physical pages of sequence `seq`, in logical order (its block table row,
+ * reserved pages included), into out[0, cap); *n_out = the count, also when
+ * cap is too small (then BSATTN_ERR_RANGE).  Introspection for tests and
+ * integrators; no reference counterpart.  Host only. */
+int bsattn_seq_pages(const bsattn_cache* cache, int32_t seq, int32_t* out, int32_t cap,
+                     int32_t* n_out);
+
 /* Tokens held by sequence `seq` (the reference's `offset`,
  * KVCache.swift:40). */
 int bsattn_seq_len(const bsattn_cache* cache, int32_t seq, int32_t* out_len);

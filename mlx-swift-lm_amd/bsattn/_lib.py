@@ -30,6 +30,8 @@ EXPORTS = (
     "bsattn_cache_create",
     "bsattn_cache_destroy",
     "bsattn_cache_info",
+    "bsattn_shuffle_free_pages",
+    "bsattn_seq_pages",
     "bsattn_seq_len",
     "bsattn_append",
     "bsattn_append_quantized",
@@ -114,6 +116,8 @@ def lib() -> ctypes.CDLL:
         "bsattn_cache_create": (ctypes.c_int, [ctypes.POINTER(Desc), PP]),
         "bsattn_cache_destroy": (ctypes.c_int, [P]),
         "bsattn_cache_info": (ctypes.c_int, [P, ctypes.POINTER(Info)]),
+        "bsattn_shuffle_free_pages": (ctypes.c_int, [P, ctypes.c_uint64]),
+        "bsattn_seq_pages": (ctypes.c_int, [P, i32, PI32, i32, PI32]),
         "bsattn_seq_len": (ctypes.c_int, [P, i32, PI32]),
         "bsattn_append": (ctypes.c_int, [P, P, P, PI32, i32, i32, P]),
         "bsattn_append_quantized": (ctypes.c_int, [P, P, P, P, P, P, P, PI32, i32, i32, P]),

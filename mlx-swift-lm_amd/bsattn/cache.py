@@ -113,6 +113,22 @@ class BlockSparseKVCache:
         check(lib().bsattn_cache_info(self._h, ctypes.byref(info)))
         return int(info.free_pages)
 
+    def shuffleFreePages(self, seed: int) -> None:
+        """Permutes the free pages (seeded): later appends take pages in a
+        shuffled physical order.  Results do not depend on it."""
+        check(lib().bsattn_shuffle_free_pages(self._h, seed))
+
+    def seqPages(self, seq: int) -> List[int]:
+        """Physical page ids of sequence `seq` in logical order."""
+        n = ctypes.c_int32()
+        rc = lib().bsattn_seq_pages(self._h, seq, None, 0, ctypes.byref(n))
+        if n.value == 0:
+            check(rc)
+            return []
+        buf = (ctypes.c_int32 * n.value)()
+        check(lib().bsattn_seq_pages(self._h, seq, buf, n.value, ctypes.byref(n)))
+        return list(buf)
+
     def seqLen(self, seq: int) -> int:
         out = ctypes.c_int32()
         check(lib().bsattn_seq_len(self._h, seq, ctypes.byref(out)))

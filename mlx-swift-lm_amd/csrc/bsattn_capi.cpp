@@ -419,6 +419,40 @@ static int check_synced(const bsattn_cache* c) {
   return BSATTN_OK;
 }
 
+int bsattn_shuffle_free_pages(bsattn_cache* c, uint64_t seed) try {
+  if (!c) return fail(BSATTN_ERR_INVALID, "null argument");
+  // Fisher-Yates over the free list with index hash splitmix64 chained over
+  // (seed, stream 5, i); the stack's back is handed out first
+  auto mix = [](uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  };
+  auto& f = c->free_pages;
+  const size_t n = f.size();
+  for (size_t i = 0; i + 1 < n; ++i) {
+    const uint64_t hsh = mix(mix(mix(seed) + 5u) + (uint64_t)i);
+    std::swap(f[n - 1 - i], f[n - 1 - i - (size_t)(hsh % (uint64_t)(n - i))]);
+  }
+  return BSATTN_OK;
+} catch (...) {
+  return on_exception();
+}
+
+int bsattn_seq_pages(const bsattn_cache* c, int32_t seq, int32_t* out, int32_t cap, int32_t* n_out) try {
+  if (!c || !n_out || (cap > 0 && !out)) return fail(BSATTN_ERR_INVALID, "null argument");
+  if (seq < 0 || seq >= c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "sequence id %d out of range", seq);
+  const auto& pg = c->pages[seq];
+  *n_out = (int32_t)pg.size();
+  if ((int64_t)pg.size() > (int64_t)cap)
+    return fail(BSATTN_ERR_RANGE, "sequence %d holds %zu pages, buffer takes %d", seq, pg.size(), cap);
+  std::copy(pg.begin(), pg.end(), out);
+  return BSATTN_OK;
+} catch (...) {
+  return on_exception();
+}
+
 int bsattn_seq_len(const bsattn_cache* c, int32_t seq, int32_t* out_len) try {
   if (!c || !out_len) return fail(BSATTN_ERR_INVALID, "null argument");
   if (seq < 0 || seq >= c->d.max_seqs) return fail(BSATTN_ERR_RANGE, "sequence id %d out of range", seq);

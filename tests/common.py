@@ -52,12 +52,13 @@ class Workload:
 
 
 def make_workload(seed, B, Hq, Hkv, T, Tb, dtype, top_k, ns=1, nr=1, D=128,
-                  salient_frac=0.0, lens=None) -> Workload:
+                  salient_frac=0.0, lens=None, prefix=None) -> Workload:
     """Keys of sequence b, kv head h, token t, dim d use element index
     ((b*Hkv + h)*Tcap + t)*D + d of stream 1 (values: stream 2); q uses
     (b*Hq + hq)*D + d of stream 0.  salient_frac of each (b, h)'s token
     positions (chosen on stream 3) have their keys scaled by 8 before
-    rounding."""
+    rounding.  With `prefix`, only each sequence's first `prefix` tokens are
+    generated (the same values as in the full workload; `lens` stays full)."""
     lens = list(lens) if lens is not None else [T] * B
     Tcap = max(lens)
     w = Workload(seed, B, Hq, Hkv, D, Tb, dtype, lens, top_k, ns, nr, salient_frac)
@@ -65,6 +66,7 @@ def make_workload(seed, B, Hq, Hkv, T, Tb, dtype, top_k, ns=1, nr=1, D=128,
     w.keys, w.values = [], []
     for b in range(B):
         Tl = lens[b]
+        Tg = Tl if prefix is None else min(Tl, prefix)
         mult = None
         if salient_frac > 0:
             mult = np.ones((Hkv, Tl), np.float64)
@@ -72,16 +74,69 @@ def make_workload(seed, B, Hq, Hkv, T, Tb, dtype, top_k, ns=1, nr=1, D=128,
             for h in range(Hkv):
                 pos = O.choose_positions(seed, S_SALIENT, b * Hkv + h, Tl, cnt)
                 mult[h, pos] = w.salient_mult
-        k = np.empty((Hkv, Tl, D), np.uint16)
-        v = np.empty((Hkv, Tl, D), np.uint16)
+        k = np.empty((Hkv, Tg, D), np.uint16)
+        v = np.empty((Hkv, Tg, D), np.uint16)
         for h in range(Hkv):
             start = ((b * Hkv + h) * Tcap) * D
-            k[h] = O.fill_normal(seed, S_K, start, (Tl, D), dtype,
-                                 row_mult=None if mult is None else mult[h])
-            v[h] = O.fill_normal(seed, S_V, start, (Tl, D), dtype)
+            k[h] = O.fill_normal(seed, S_K, start, (Tg, D), dtype,
+                                 row_mult=None if mult is None else np.ascontiguousarray(mult[h, :Tg]))
+            v[h] = O.fill_normal(seed, S_V, start, (Tg, D), dtype)
         w.keys.append(k)
         w.values.append(v)
     return w
+
+
+# The configurations' inputs (seed 1000 + config number).  C4's lengths are
+# its initial lengths U[8192, 65536] (stream 4) plus its 256 appended tokens.
+def config_args(name: str) -> dict:
+    if name in ("C1_f16", "C1_bf16"):
+        return dict(seed=1001, B=1, Hq=32, Hkv=8, T=4096, Tb=64, dtype=name[3:], top_k=8)
+    if name == "C2":
+        return dict(seed=1002, B=8, Hq=32, Hkv=8, T=32768, Tb=64, dtype="bf16", top_k=32,
+                    salient_frac=0.01)
+    if name == "C3":
+        return dict(seed=1003, B=4, Hq=32, Hkv=8, T=131072, Tb=64, dtype="f16", top_k=64)
+    if name == "C4":
+        lens = [O.uniform_int(1004, S_LEN, b, 8192, 65536) + 256 for b in range(32)]
+        return dict(seed=1004, B=32, Hq=32, Hkv=8, T=max(lens), Tb=64, dtype="f16", top_k=32, lens=lens)
+    if name == "C5":
+        return dict(seed=1005, B=8, Hq=64, Hkv=4, T=262144, Tb=32, dtype="f16", top_k=128, nr=4)
+    raise KeyError(name)
+
+
+CONFIGS = ("C1_f16", "C1_bf16", "C2", "C3", "C4", "C5")
+DIGEST_PREFIX = 256
+
+
+def workload_digest(w: Workload, prefix: Optional[int] = None) -> str:
+    """SHA-256 over the lengths (int32), q, then every (sequence, kv head)'s
+    keys and values (their first `prefix` tokens with `prefix`), as
+    little-endian 16-bit storage words."""
+    import hashlib
+    h = hashlib.sha256()
+    h.update(np.asarray(w.lens, "<i4").tobytes())
+    h.update(np.ascontiguousarray(w.q, "<u2").tobytes())
+    for b in range(w.B):
+        for hh in range(w.Hkv):
+            n = w.keys[b].shape[1] if prefix is None else min(prefix, w.lens[b])
+            h.update(np.ascontiguousarray(w.keys[b][hh, :n], "<u2").tobytes())
+            h.update(np.ascontiguousarray(w.values[b][hh, :n], "<u2").tobytes())
+    return h.hexdigest()
+
+
+def input_digests() -> dict:
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "input_digests.json")) as f:
+        return json.load(f)
+
+
+def check_config_inputs(w: Workload, name: str) -> None:
+    """The generated inputs of configuration `name` hash to the committed
+    digests (full and prefix)."""
+    want = input_digests()[name]
+    assert workload_digest(w, DIGEST_PREFIX) == want["prefix_sha256"], f"{name}: input prefix digest differs"
+    assert workload_digest(w) == want["sha256"], f"{name}: input digest differs"
 
 
 def oracle_decode(w: Workload):

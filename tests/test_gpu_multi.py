@@ -120,3 +120,84 @@ def test_multi_decode_argument_errors(gpu):
     q3 = torch.zeros((1, 32, 3, 128), dtype=torch.bfloat16, device=gpu)
     with pytest.raises(BsattnError):
         c2.decodeMulti(q3, 1.0)  # 2 tokens, 3 queries
+
+
+def _oracle_query(qh, keys, values, T, Tb, ns, nr, K, scale, dtype, bits):
+    """oracle selection and output of one kv head's group of queries qh
+    [G, D] over the first T tokens of keys / values [T_all, D] (16-bit, or
+    quantized on append by the affine codec when bits)."""
+    if bits == 0:
+        idx, _, out = O.decode_head(qh, keys[:T], values[:T], Tb, ns, nr, K, scale, dtype)
+        return idx, out
+    kq = O.quantize(np.ascontiguousarray(keys[:T]), bits, 64)
+    vq = O.quantize(np.ascontiguousarray(values[:T]), bits, 64)
+    summ = O.summaries_q(*kq, Tb, bits, 64)
+    idx, n = O.select(O.score_blocks(qh, summ, "f16"), T, Tb, ns, nr, K)
+    return idx, O.attend_q(qh, kq, vq, Tb, bits, 64, idx[:n], scale)
+
+
+@pytest.mark.parametrize("dtype,Tb,kv_bits", [("bf16", 64, 0), ("f16", 32, 0), ("f16", 64, 4),
+                                               ("f16", 32, 4)])
+def test_trim_rewinds_a_completed_block(gpu, dtype, Tb, kv_bits):
+    """A speculative round that is mostly rejected (Evaluate.swift:909-911 ->
+    trimPromptCache, KVCache.swift:1520-1524, 396-402): 5 draft tokens
+    complete a block (its summary is written) and start the next; trimming 4
+    of them makes the completed block partial again; 3 different tokens then
+    refill it, so its summary must be recomputed from the new token.  After
+    each pass the summaries are bit-exact and every query of decodeMulti
+    matches the oracle on its own prefix of the accepted sequence."""
+    import torch
+    L1, REJ, L2 = 5, 4, 3
+    T0 = [7 * Tb - 2, 9 * Tb - 1]
+    log(f"[trim-rewind] {dtype} Tb={Tb} bits={kv_bits}")
+    w = make_workload(6400 + Tb + kv_bits, B=2, Hq=32, Hkv=8, T=max(T0) + L1, Tb=Tb, dtype=dtype, top_k=4,
+                      ns=1, nr=1, lens=[t + L1 for t in T0])
+    refill_k = O.fill_normal(6450 + Tb, 1, 0, (w.B, w.Hkv, L2, w.D), dtype)
+    refill_v = O.fill_normal(6450 + Tb, 2, 0, (w.B, w.Hkv, L2, w.D), dtype)
+    c = new_cache(w, kv_bits=kv_bits)
+    for b in range(w.B):
+        c.append(to_dev(np.ascontiguousarray(w.keys[b][None, :, :T0[b]]), dtype, gpu),
+                 to_dev(np.ascontiguousarray(w.values[b][None, :, :T0[b]]), dtype, gpu), seq_ids=[b])
+
+    def check(keys, values, T_end, L, q, out, idx):
+        got = from_dev(out)
+        for b in range(w.B):
+            for i in range(L):
+                T_i = T_end[b] - L + 1 + i
+                for h in range(w.Hkv):
+                    ri, ro = _oracle_query(q[b, h * w.G:(h + 1) * w.G, i], keys[b][h], values[b][h], T_i, Tb,
+                                           w.ns, w.nr, w.top_k, w.scale, dtype, kv_bits)
+                    assert np.array_equal(idx[b, i, h].cpu().numpy(), ri), f"seq {b} query {i} head {h}"
+                    err = output_error(O.to_f32(got[b, h * w.G:(h + 1) * w.G, i], dtype).astype(np.float64),
+                                       ro, dtype)
+                    assert err <= (1e-2 if kv_bits else TOL), f"seq {b} query {i} head {h}: {err:.3g}"
+        for b in range(w.B):
+            s = from_dev(c.exportSummaries(b))
+            for h in range(w.Hkv):
+                if kv_bits:
+                    ref = O.summaries_q(*O.quantize(np.ascontiguousarray(keys[b][h][:T_end[b]]), kv_bits, 64),
+                                       Tb, kv_bits, 64)
+                else:
+                    ref = O.summaries(np.ascontiguousarray(keys[b][h][:T_end[b]]), Tb, dtype)
+                assert np.array_equal(s[h], ref), f"seq {b} head {h}: summaries"
+
+    # the draft pass: 5 tokens, completing a block
+    dk = np.stack([k[:, T0[b]:T0[b] + L1] for b, k in enumerate(w.keys)])
+    dv = np.stack([v[:, T0[b]:T0[b] + L1] for b, v in enumerate(w.values)])
+    c.append(to_dev(dk, dtype, gpu), to_dev(dv, dtype, gpu))
+    q1 = O.fill_normal(6460, 0, 0, (w.B, w.Hq, L1, w.D), dtype)
+    idx1 = torch.empty((w.B, L1, w.Hkv, c.nselMax), dtype=torch.int32, device=gpu)
+    o1 = c.decodeMulti(to_dev(q1, dtype, gpu), w.scale, idx_out=idx1)
+    torch.cuda.synchronize()
+    check(w.keys, w.values, [t + L1 for t in T0], L1, q1, o1, idx1)
+    # reject 4: the completed block is partial again
+    assert c.trim(REJ) == REJ and [c.seqLen(b) for b in range(w.B)] == [t + 1 for t in T0]
+    # 3 different tokens refill it
+    c.append(to_dev(refill_k, dtype, gpu), to_dev(refill_v, dtype, gpu))
+    keys = [np.concatenate([w.keys[b][:, :T0[b] + 1], refill_k[b]], axis=1) for b in range(w.B)]
+    values = [np.concatenate([w.values[b][:, :T0[b] + 1], refill_v[b]], axis=1) for b in range(w.B)]
+    q2 = O.fill_normal(6470, 0, 0, (w.B, w.Hq, L2, w.D), dtype)
+    idx2 = torch.empty((w.B, L2, w.Hkv, c.nselMax), dtype=torch.int32, device=gpu)
+    o2 = c.decodeMulti(to_dev(q2, dtype, gpu), w.scale, idx_out=idx2)
+    torch.cuda.synchronize()
+    check(keys, values, [t + 1 + L2 for t in T0], L2, q2, o2, idx2)

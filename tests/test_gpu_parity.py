@@ -13,8 +13,8 @@ import sys
 import numpy as np
 import pytest
 
-from common import (Workload, fill, from_dev, log, make_workload, new_cache, oracle_decode,
-                    oracle_summaries, output_error, to_dev, torch_dtype)
+from common import (S_LEN, Workload, check_config_inputs, config_args, fill, from_dev, log, make_workload,
+                    new_cache, oracle_decode, oracle_summaries, output_error, to_dev, torch_dtype)
 import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -48,7 +48,8 @@ def run_and_check(cache, w: Workload, device, check_summaries=True):
 def test_config1_single_decode(gpu, dtype):
     """B=1, Hq=32, Hkv=8, D=128, 4096 tokens in 64-token blocks, top-8 + sink + newest."""
     log(f"[config1] dtype={dtype}")
-    w = make_workload(1000, B=1, Hq=32, Hkv=8, T=4096, Tb=64, dtype=dtype, top_k=8)
+    w = make_workload(**config_args(f"C1_{dtype}"))
+    check_config_inputs(w, f"C1_{dtype}")
     cache = new_cache(w)
     fill(cache, w, gpu)
     err = run_and_check(cache, w, gpu)
@@ -58,8 +59,8 @@ def test_config1_single_decode(gpu, dtype):
 def test_config2_batched_salient(gpu):
     """B=8, 32k context, bf16, 1% of keys scaled x8, top-32 + sink + recent."""
     log("[config2] generating")
-    w = make_workload(1001, B=8, Hq=32, Hkv=8, T=32768, Tb=64, dtype="bf16", top_k=32,
-                      salient_frac=0.01)
+    w = make_workload(**config_args("C2"))
+    check_config_inputs(w, "C2")
     cache = new_cache(w)
     fill(cache, w, gpu)
     err = run_and_check(cache, w, gpu)
@@ -147,17 +148,20 @@ def test_decode_loop_with_appends(gpu):
 
 
 def test_config4_decode_loop_full(gpu):
-    """B=32 sequences of U[8192, 65536] tokens (stream 4), their pages
-    interleaved in the pool, Hq=32, Hkv=8, fp16, top-32 + sink + recent; 256
-    decode steps, each appending one token per sequence: selected blocks and
-    outputs against the oracle after steps 1, 128 and 256 (every head), block
-    summaries after the last."""
+    """B=32 sequences of U[8192, 65536] tokens (stream 4), their pages taken
+    in shuffled physical order (the free list permuted from the seed, stream
+    5), Hq=32, Hkv=8, fp16, top-32 + sink + recent; 256 decode steps, each
+    appending one token per sequence: selected blocks and outputs against the
+    oracle after steps 1, 128 and 256 (every head), block summaries after the
+    last."""
     import torch
     seed, steps, Tb = 1004, 256, 64
-    lens0 = [O.uniform_int(seed, 4, b, 8192, 65536) for b in range(32)]
+    lens0 = [O.uniform_int(seed, S_LEN, b, 8192, 65536) for b in range(32)]
     total = [l + steps for l in lens0]
     log("[config4] generating")
-    w = make_workload(seed, B=32, Hq=32, Hkv=8, T=max(total), Tb=Tb, dtype="f16", top_k=32, lens=total)
+    w = make_workload(**config_args("C4"))
+    assert w.lens == total and w.seed == seed and w.Tb == Tb
+    check_config_inputs(w, "C4")
 
     def view(cur):
         ws = Workload(w.seed, w.B, w.Hq, w.Hkv, w.D, Tb, "f16", list(cur), w.top_k, w.ns, w.nr)
@@ -167,7 +171,11 @@ def test_config4_decode_loop_full(gpu):
         return ws
 
     cache = new_cache(w)
-    fill(cache, view(lens0), gpu, chunk=4096)
+    cache.shuffleFreePages(seed)
+    fill(cache, view(lens0), gpu)
+    # the pages of a sequence are scattered through the pool, not ascending
+    bt = cache.seqPages(0)
+    assert bt != sorted(bt) and len(set(bt)) == len(bt)
     worst = 0.0
     for s in range(steps):
         cur = [l + s + 1 for l in lens0]

@@ -177,3 +177,61 @@ def test_prefill_quantized_cache(gpu, bits, Hq, Hkv, Tb, lens, L):
                 assert err <= 1e-2, f"seq {b} query {i} head {h}: error {err:.3g}"
                 worst = max(worst, err)
     log(f"[prefill-q] err={worst:.3g}")
+
+
+def _threads():
+    import os
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+@pytest.mark.parametrize("bits", [0, 4])
+def test_prefill_timed_shape(gpu, bits):
+    """The benchmarked prefill shape: a 512-token chunk appended at the end of
+    32768 tokens, B=8, Hq=32, Hkv=8, 64-token blocks (bf16, or an int4 affine
+    cache over fp16 inputs).  Every head of every sequence at the first and
+    last 8 query tokens and at two middle ones, against the oracle's attention
+    over the query's prefix (dense, or over the quantized keys / values);
+    the oracle calls run on a thread pool (ctypes releases the GIL)."""
+    import torch
+    from concurrent.futures import ThreadPoolExecutor
+    B, Hq, Hkv, Tb, T, L, GS = 8, 32, 8, 64, 32768, 512, 64
+    dtype = "bf16" if bits == 0 else "f16"
+    log(f"[prefill-timed] {'bf16' if bits == 0 else 'int4'}: generating")
+    w = make_workload(7800 + bits, B=B, Hq=Hq, Hkv=Hkv, T=T, Tb=Tb, dtype=dtype, top_k=32, salient_frac=0.01)
+    c = new_cache(w, kv_bits=bits)
+    for b in range(B):
+        c.append(to_dev(np.ascontiguousarray(w.keys[b][None, :, :T - L]), dtype, gpu),
+                 to_dev(np.ascontiguousarray(w.values[b][None, :, :T - L]), dtype, gpu), seq_ids=[b])
+    c.append(to_dev(np.stack([w.keys[b][:, T - L:] for b in range(B)]), dtype, gpu),
+             to_dev(np.stack([w.values[b][:, T - L:] for b in range(B)]), dtype, gpu))
+    qm = O.fill_normal(7850 + bits, 0, 0, (B, Hq, L, w.D), dtype)
+    got = from_dev(c.prefill(to_dev(qm, dtype, gpu), w.scale))
+    torch.cuda.synchronize()
+    queries = list(range(8)) + [L // 3, 2 * L // 3] + list(range(L - 8, L))
+    log(f"[prefill-timed] checking {B * Hkv * len(queries)} (sequence, kv head, query) triples")
+
+    def job(item):
+        b, h, i = item
+        pos = T - L + i
+        qh = np.ascontiguousarray(qm[b, h * w.G:(h + 1) * w.G, i])
+        if bits == 0:
+            ref = O.dense(qh, w.keys[b][h][:pos + 1], w.values[b][h][:pos + 1], w.scale, dtype)
+        else:
+            kq, vq = qcache[(b, h)]
+            ref = O.attend_q(qh, [a[:pos + 1] for a in kq], [a[:pos + 1] for a in vq], Tb, bits, GS,
+                             np.arange(pos // Tb + 1, dtype=np.int32), w.scale)
+        a = O.to_f32(got[b, h * w.G:(h + 1) * w.G, i], dtype).astype(np.float64)
+        return output_error(a, ref, dtype)
+
+    qcache = {}
+    if bits:
+        with ThreadPoolExecutor(_threads()) as ex:
+            pairs = [(b, h) for b in range(B) for h in range(Hkv)]
+            codes = ex.map(lambda p: (O.quantize(w.keys[p[0]][p[1]], bits, GS),
+                                      O.quantize(w.values[p[0]][p[1]], bits, GS)), pairs)
+            qcache = dict(zip(pairs, codes))
+    with ThreadPoolExecutor(_threads()) as ex:
+        errs = list(ex.map(job, [(b, h, i) for b in range(B) for h in range(Hkv) for i in queries]))
+    worst = max(errs)
+    log(f"[prefill-timed] max error {worst:.3g}")
+    assert worst <= (TOL if bits == 0 else 1e-2), f"max error {worst:.3g}"

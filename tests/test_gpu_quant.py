@@ -20,7 +20,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from common import (Workload, fill, from_dev, log, make_workload, new_cache, output_error, to_dev)
+from common import (Workload, check_config_inputs, config_args, fill, from_dev, log, make_workload, new_cache,
+                    output_error, to_dev)
 import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -203,7 +204,8 @@ def test_config3_int4_full(gpu):
     """B=4, Hq=32, Hkv=8, 131072 tokens in 64-token blocks, int4 group 64,
     top-64 + sink + recent: every head against the oracle."""
     log("[config3] generating")
-    w = make_workload(3400, B=4, Hq=32, Hkv=8, T=131072, Tb=64, dtype="f16", top_k=64)
+    w = make_workload(**config_args("C3"))
+    check_config_inputs(w, "C3")
     cache = new_cache(w, kv_bits=4)
     fill(cache, w, gpu)
     log("[config3] oracle")
@@ -218,7 +220,8 @@ def test_config5_int8_wide_group_full(gpu):
     against the oracle (the MFMA-band scoring and the workgroup selection at
     full size)."""
     log("[config5] generating")
-    w = make_workload(1005, B=8, Hq=64, Hkv=4, T=262144, Tb=32, dtype="f16", top_k=128, nr=4)
+    w = make_workload(**config_args("C5"))
+    check_config_inputs(w, "C5")
     cache = new_cache(w, kv_bits=8)
     fill(cache, w, gpu)
     log("[config5] oracle")
