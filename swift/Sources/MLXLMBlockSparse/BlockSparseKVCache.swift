@@ -443,3 +443,25 @@ public func maybeQuantizeBlockSparseKVCache(
         }
     }
 }
+
+/// The block-sparse form of LanguageModel.newCache(parameters:)
+/// (LanguageModel.swift:215-230): one cache per layer, layer i with
+/// kvHeads[i] KV heads, for up to `maxSeqs` sequences of `maxTokens` tokens.
+/// The caches start 16-bit even when parameters.kvBits is set, as in the
+/// reference; maybeQuantizeBlockSparseKVCache converts them once
+/// quantizedKVStart is passed.  A maxKVSize asks for the reference's
+/// RotatingKVCache (a bounded window), which stays on the dense path.
+public func newBlockSparseCache(
+    kvHeads: [Int], qHeads: Int, parameters: GenerateParameters? = nil, maxSeqs: Int, maxTokens: Int,
+    dtype: DType = .bfloat16, blockSize: Int = 64, topK: Int = 32, sinkBlocks: Int = 1,
+    recentBlocks: Int = 1, device: BlockSparseDevice? = nil
+) -> [KVCache] {
+    precondition(parameters?.maxKVSize == nil,
+                 "maxKVSize selects RotatingKVCache (KVCache.swift:445-578), which stays on the dense path")
+    let blocks = (maxTokens + blockSize - 1) / blockSize
+    return kvHeads.map { h in
+        BlockSparseKVCache(
+            maxSeqs: maxSeqs, qHeads: qHeads, kvHeads: h, blockSize: blockSize, dtype: dtype, topK: topK,
+            sinkBlocks: sinkBlocks, recentBlocks: recentBlocks, maxBlocksPerSeq: blocks, device: device)
+    }
+}
