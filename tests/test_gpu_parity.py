@@ -13,8 +13,8 @@ import sys
 import numpy as np
 import pytest
 
-from common import (S_LEN, Workload, check_config_inputs, config_args, fill, from_dev, log, make_workload,
-                    new_cache, oracle_decode, oracle_summaries, output_error, to_dev, torch_dtype)
+from common import (S_LEN, Workload, check_config_inputs, check_literal_bar, config_args, fill, from_dev, log,
+                    make_workload, new_cache, oracle_decode, oracle_summaries, output_error, to_dev, torch_dtype)
 import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -37,6 +37,7 @@ def run_and_check(cache, w: Workload, device, check_summaries=True):
     assert np.array_equal(from_dev(out).reshape(w.B, w.Hq, w.D), got2), "decode != select + attend"
     err = output_error(got, out_ref, w.dtype)
     assert err <= TOL, f"output error {err:.3g} > {TOL}"
+    check_literal_bar(got, out_ref, w.dtype, TOL, f"B{w.B} Hq{w.Hq} T{max(w.lens)} {w.dtype}")
     if check_summaries:
         for b in range(w.B):
             s = from_dev(cache.exportSummaries(b))

@@ -20,8 +20,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from common import (Workload, check_config_inputs, config_args, fill, from_dev, log, make_workload, new_cache,
-                    output_error, to_dev)
+from common import (Workload, check_config_inputs, check_literal_bar, config_args, fill, from_dev, log,
+                    make_workload, new_cache, output_error, to_dev)
 import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -87,8 +87,10 @@ def run_and_check_q(cache, w: Workload, device, bits: int, kq, vq):
     assert np.array_equal(idx, idx_ref), f"selected blocks differ: {np.argwhere(idx != idx_ref)[:5]}"
     a, a2 = from_dev(out).reshape(w.B, w.Hq, w.D), from_dev(out2).reshape(w.B, w.Hq, w.D)
     assert np.array_equal(a, a2), "decode != select + attend"
-    err = output_error(O.to_f32(a, "f16").astype(np.float64), out_ref, "f16")
+    got = O.to_f32(a, "f16").astype(np.float64)
+    err = output_error(got, out_ref, "f16")
     assert err <= TOL, f"output error {err:.3g} > {TOL}"
+    check_literal_bar(got, out_ref, "f16", TOL, f"int{bits} B{w.B} Hq{w.Hq} T{max(w.lens)}")
     return err
 
 
