@@ -78,7 +78,7 @@ struct bsattn_cache {
   float* scores = nullptr;    // [rows][hkv][sstride] + kScoreSlack
   int32_t* idx_ws = nullptr;  // [rows][hkv][nsel_max]
   float* partials = nullptr;  // [rows][hq][nsplit][D + 2]
-  float* err_ws = nullptr;    // [rows][hkv][mfma_err_stride]: MFMA score bounds
+  float* err_ws = nullptr;    // [rows][hkv][2][mfma_err_stride]: MFMA score bounds, chunk floors
   std::vector<int32_t> len;
   // set by bsattn_append_step: the device-side lengths may be ahead of `len`
   // until bsattn_sync
@@ -367,7 +367,7 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) try {
     return cleanup(hip_fail(e, "hipMalloc(indices)"));
   if ((e = hipMalloc((void**)&c->partials, rows * g.hq * g.nsplit * (kHeadDim + 2) * 4)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMalloc(partials)"));
-  if ((e = hipMalloc((void**)&c->err_ws, rows * g.hkv * mfma_err_stride(g) * 4)) != hipSuccess)
+  if ((e = hipMalloc((void**)&c->err_ws, rows * g.hkv * 2 * mfma_err_stride(g) * 4)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMalloc(bounds)"));
   // zeroed pages: never-written token slots hold finite values
   if ((e = hipMemset(g.pool, 0, c->pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(pool)"));
@@ -676,7 +676,7 @@ static bool len_first(const bsattn_cache* c, const Entry* es, int e0, int n) {
 
 // Device workspaces of one launch (rows = the launch's batch entries):
 // block scores [rows][hkv][sstride] + kScoreSlack, MFMA score bounds
-// [rows][hkv][mfma_err_stride], indices [rows][hkv][nsel_max], split
+// and floors [rows][hkv][2][mfma_err_stride], indices [rows][hkv][nsel_max], split
 // partials [rows][hq][nsplit][D + 2].
 struct Workspace {
   float* scores;
@@ -806,7 +806,7 @@ int bsattn_decode_noalloc(bsattn_cache* c, const void* q, const int32_t* seq_ids
     return at;
   };
   const size_t o_sc = take((rows * g.hkv * g.sstride + kScoreSlack) * 4);
-  const size_t o_err = take(rows * g.hkv * mfma_err_stride(g) * 4);
+  const size_t o_err = take(rows * g.hkv * 2 * mfma_err_stride(g) * 4);
   const size_t o_idx = take(rows * g.hkv * g.nsel_max * 4);
   const size_t o_part = take(rows * g.hq * g.nsplit * (kHeadDim + 2) * 4);
   if (used > kNoAllocScratchBytes)

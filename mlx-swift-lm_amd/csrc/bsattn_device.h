@@ -208,6 +208,9 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
   return wave_allreduce_u32(x, [](uint32_t a, uint32_t b) { return max(a, b); });
 }
+__device__ __forceinline__ int wave_sum_i32(int x) {
+  return (int)wave_allreduce_u32((uint32_t)x, [](uint32_t a, uint32_t b) { return a + b; });
+}
 // inclusive prefix sum over the wave's lanes
 __device__ __forceinline__ int wave_scan_incl(int v) {
   uint32_t x = (uint32_t)v;

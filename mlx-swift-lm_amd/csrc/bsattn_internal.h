@@ -126,7 +126,8 @@ hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_cou
 // candidate blocks (neither sink nor recent) of a sequence of `len` tokens
 int candidates(const Geometry& g, int len);
 // scoring + top-K for a batch whose largest candidate count is max_nc;
-// err: bound workspace of mfma_err_stride(g) floats per (sequence, kv head)
+// err: bound and floor workspace of 2 * mfma_err_stride(g) floats per
+// (sequence, kv head)
 hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                          float* err, int32_t* idx, int max_nc, hipStream_t s, Timing* prof);
 int mfma_err_stride(const Geometry& g);

@@ -72,8 +72,11 @@ template <int DT, int G>
 __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
                                                     const uint16_t* __restrict__ q,
                                                     float* __restrict__ scores,
-                                                    float* __restrict__ err, int err_stride) {
+                                                    float* __restrict__ err, int err_stride,
+                                                    int floor_rank) {
   __shared__ float s_e[4];
+  __shared__ float s_sc[kMfmaChunk];  // the chunk's approximate scores (-inf: no candidate)
+  s_sc[threadIdx.x] = -INFINITY;  // (entries wave*64 .. +63 are written below by the same wave)
   const int chunk = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
@@ -105,9 +108,12 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
   const int len = entry_len(geo, sb, bi, seq);
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int c1 = nb - geo.nr;
-  float* erow = err + ((size_t)bi * geo.hkv + h) * err_stride;
+  float* erow = err + ((size_t)bi * geo.hkv + h) * 2 * err_stride;
   if (!ranked_select(geo, c1 - c0)) {
-    if (threadIdx.x == 0) erow[chunk] = 0.0f;
+    if (threadIdx.x == 0) {
+      erow[chunk] = 0.0f;
+      erow[err_stride + chunk] = INFINITY;
+    }
     return;
   }
   constexpr uint32_t one2 = DT == 0 ? 0x3C003C00u : 0x3F803F80u;
@@ -152,15 +158,55 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
     const bool any_bad = (((bm | (bm >> 16) | (bm >> 32) | (bm >> 48)) >> n) & 1ull) != 0ull;
     const int j = j0 + n;
     if (j < c1) {
-      if (g == 0) srow[j] = any_bad ? __builtin_nanf("") : sc;
+      const float v = any_bad ? __builtin_nanf("") : sc;
+      if (g == 0) {
+        srow[j] = v;
+        s_sc[wave * 16 * kMfmaTiles + 16 * t + n] = v;
+      }
       if (!any_bad) emax = fmaxf(emax, am + k1[0]);  // k1[i] = ||summary row||_1 for every i
     }
   }
   emax = wave_max_f32(emax);
   if (lane == 0) s_e[wave] = emax;
   __syncthreads();
-  if (threadIdx.x == 0)
-    erow[chunk] = 0x1p-14f * (fmaxf(fmaxf(s_e[0], s_e[1]), fmaxf(s_e[2], s_e[3])) + q1max);
+  if (wave == 0) {
+    // the chunk's floor: its floor_rank-th largest approximate score (with
+    // repeats), -inf if a score is not finite (no certificate), +inf if the
+    // chunk has fewer candidates
+    float v[4];
+    bool nonfinite = false;
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = s_sc[lane + 64 * i];
+      nonfinite = nonfinite || __builtin_isnan(v[i]) || v[i] == INFINITY;
+      cnt += v[i] != -INFINITY;
+    }
+    const bool any_nonfinite = __ballot(nonfinite) != 0ull;
+    const int total = wave_sum_i32(cnt);
+    float fl = INFINITY;
+    if (any_nonfinite) {
+      fl = -INFINITY;
+    } else if (total >= floor_rank) {
+      for (int r = 0; r < floor_rank; ++r) {
+        float lm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        const float m = wave_max_f32(lm);
+        fl = m;
+        // remove one occurrence: the lowest lane holding it, its first slot
+        const int src = __ffsll((unsigned long long)__ballot(lm == m)) - 1;
+        if (lane == src) {
+          if (v[0] == m) v[0] = -INFINITY;
+          else if (v[1] == m) v[1] = -INFINITY;
+          else if (v[2] == m) v[2] = -INFINITY;
+          else v[3] = -INFINITY;
+        }
+      }
+    }
+    if (lane == 0) {
+      erow[chunk] = 0x1p-14f * (fmaxf(fmaxf(s_e[0], s_e[1]), fmaxf(s_e[2], s_e[3])) + q1max);
+      erow[err_stride + chunk] = fl;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -422,67 +468,27 @@ __device__ __forceinline__ void load_scores(const float* __restrict__ src, float
 }
 
 // ---------------------------------------------------------------------------
-// block-wide selection; grid (Hkv, n), 1024 threads.  Thread t owns blocks
-// j = t*PER + p, p < PER, of its score row (the candidates are ns <= j <
-// ns + nc), so thread order then p is block order.
-// BAND: scores are the approximate MFMA scores with bounds in err (see the
-// top of this file); dynamic LDS then holds the band (u32 per candidate).
+// The selection over the keys the workgroup's threads hold (kr[p] of slot p
+// valid where vmask has bit p; jr[p] its block index; thread order then p
+// is block order; nvalid valid keys in all): the K largest by (exact key,
+// index), as a mask over the thread's slots.  BAND: the keys are
+// approximate MFMA scores with bound e (see the top of this file), and the
+// band around the K-th is rescored in the canonical order (the query rows
+// in s_q); the argument needs only that the keys held include the row's
+// top K.
 // ---------------------------------------------------------------------------
 template <int DT, int G, bool BAND, int PER>
-__global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch sb,
-                                                        const uint16_t* __restrict__ q,
-                                                        const float* __restrict__ scores,
-                                                        const float* __restrict__ err,
-                                                        int err_stride, int err_count,
-                                                        int32_t* __restrict__ idx_out) {
-  extern __shared__ uint32_t s_band[];
-  __shared__ SelScratch ss;
-  __shared__ __align__(16) uint32_t s_q[BAND ? G * kHeadDim / 2 : 4];
+__device__ uint32_t select_core(const Geometry& geo, int seq, int h, const uint32_t (&kr)[PER],
+                                const int (&jr)[PER], uint32_t vmask, int nvalid, int K, float e,
+                                SelScratch& ss, int& ph, uint32_t* s_band, const uint32_t* s_q) {
   const int tid = threadIdx.x, lane = tid & 63;
-  const int h = blockIdx.x, bi = blockIdx.y;
-  const int seq = sb.ids[bi];
-  const int c0 = geo.ns, K = geo.top_k;
-  // scores (and the chunk bounds) are loaded before the sequence length is
-  // known: the row reads stay inside the score buffer (its slack covers
-  // the last row), and entries that are not candidates are never used
-  const int i0 = tid * PER;
-  float sc[PER];
-  load_scores<PER>(score_row(geo, scores, bi, h) + i0, sc);
-  float ev = 0.0f;
-  if (BAND && tid < 64 && lane < err_count) ev = err[((size_t)bi * geo.hkv + h) * err_stride + lane];
-  const int len = entry_len(geo, sb, bi, seq);
-  const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
-  const int nc = nb - geo.nr - c0;
-  int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
-  if (!ranked_select(geo, nc)) {  // every block kept, or (top_k 0) sinks and recent only
-    for (int p = tid; p < geo.nsel_max; p += kSelThreads)
-      out[p] = selected_block(p, nb, nc > K, geo.ns, geo.nr, K, nullptr);
-    return;
-  }
-  uint32_t kr[PER];
-  uint32_t vmask = 0u;
-#pragma unroll
-  for (int p = 0; p < PER; ++p) {
-    const bool v = i0 + p >= c0 && i0 + p < c0 + nc;
-    kr[p] = v ? score_key(sc[p]) : 0u;
-    vmask |= (uint32_t)v << p;
-  }
-  int ph = 0;
-  uint32_t take;
+  if (nvalid <= K) return vmask;
   if constexpr (!BAND) {
-    take = wg_topk_mask(kr, vmask, nc, K, ss, ph);
+    return wg_topk_mask(kr, vmask, nvalid, K, ss, ph);
   } else {
-    for (int e = tid; e < G * kHeadDim / 2; e += kSelThreads)
-      s_q[e] = ((const uint32_t*)(q + q_row(sb, bi, h * G + e / (kHeadDim / 2))))[e % (kHeadDim / 2)];
-    // the bound: maximum over the chunks' bounds (NaN bounds are skipped)
-    if (tid < 64) {
-      ev = wave_max_f32(ev);
-      if (tid == 0) ss.misc[7] = __float_as_int(ev);
-    }
-    // K-th largest approximate key (wg_kth's barriers publish misc[7] and s_q)
+    // K-th largest approximate key
     int gt, eq;
-    const uint32_t t1 = wg_kth(kr, vmask, nc, K, ss, ph, &gt, &eq);
-    const float e = __int_as_float(ss.misc[7]) * (1.0f + 0x1p-8f) + 0x1p-120f;
+    const uint32_t t1 = wg_kth(kr, vmask, nvalid, K, ss, ph, &gt, &eq);
     // one exchange: the largest key below t1 and whether every approximate
     // score is finite
     uint32_t fin = 1u, below = 0u;
@@ -500,8 +506,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
     // nothing: then every candidate is rescored
     const bool bounds_ok = fin != 0u && __builtin_isfinite(lb) && __builtin_isfinite(ub);
     // classify: certainly in (take), band (rescored), certainly out
-    uint32_t band = 0u;
-    take = 0u;
+    uint32_t band = 0u, take = 0u;
     int nin = 0, nband = 0;
 #pragma unroll
     for (int p = 0; p < PER; ++p)
@@ -522,62 +527,179 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
     const int nin_total = packed_total >> 16, nband_total = packed_total & 0xFFFF;
     const int bpos = packed_pos & 0xFFFF;
     const int krem = K - nin_total;
-    if (nband_total <= krem) {
-      take |= band;
-    } else {
-      // band list, then the canonical score of every band block
-      int w = bpos;
+    if (nband_total <= krem) return take | band;
+    // band list, then the canonical score of every band block
+    int w = bpos;
+#pragma unroll
+    for (int p = 0; p < PER; ++p)
+      if (band & (1u << p)) s_band[w++] = (uint32_t)jr[p];
+    __syncthreads();
+    const int c = tid & 15;
+    const uint16_t* qh = (const uint16_t*)s_q;
+    for (int bk = tid >> 4; bk < nband_total; bk += kSelThreads / 16) {
+      const int j = (int)s_band[bk];
+      float sv[8];
+      unpack8<DT>(*(const u32x4*)(summary_row(geo, seq, h, j) + 8 * c), sv);
+      float best = 0.0f;
+#pragma unroll 4
+      for (int gq = 0; gq < G; ++gq) {
+        float qv[8];
+        unpack8<DT>(*(const u32x4*)(qh + gq * kHeadDim + 8 * c), qv);
+        const float acc = canonical_dot16(qv, sv);
+        if (gq == 0 || acc > best) best = acc;
+      }
+      if (c == 0) s_band[bk] = score_key(best);  // the slot's index is no longer needed
+    }
+    __syncthreads();
+    if (nband_total <= 64) {
+      // one wave picks the krem best of the band (band slots are in block
+      // order) and leaves a 0/1 flag in each slot
+      if (tid < 64) {
+        const bool valid = lane < nband_total;
+        const uint32_t x = valid ? s_band[lane] : 0u;
+        const bool t = wave_take_best(x, valid, krem);
+        if (valid) s_band[lane] = t ? 1u : 0u;
+      }
+      __syncthreads();
+      w = bpos;
 #pragma unroll
       for (int p = 0; p < PER; ++p)
-        if (band & (1u << p)) s_band[w++] = (uint32_t)(i0 + p);
-      __syncthreads();
-      const int c = tid & 15;
-      const uint16_t* qh = (const uint16_t*)s_q;
-      for (int bk = tid >> 4; bk < nband_total; bk += kSelThreads / 16) {
-        const int j = (int)s_band[bk];
-        float sv[8];
-        unpack8<DT>(*(const u32x4*)(summary_row(geo, seq, h, j) + 8 * c), sv);
-        float best = 0.0f;
-#pragma unroll 4
-        for (int gq = 0; gq < G; ++gq) {
-          float qv[8];
-          unpack8<DT>(*(const u32x4*)(qh + gq * kHeadDim + 8 * c), qv);
-          const float acc = canonical_dot16(qv, sv);
-          if (gq == 0 || acc > best) best = acc;
-        }
-        if (c == 0) s_band[bk] = score_key(best);  // the slot's index is no longer needed
-      }
-      __syncthreads();
-      if (nband_total <= 64) {
-        // one wave picks the krem best of the band (band slots are in block
-        // order) and leaves a 0/1 flag in each slot
-        if (tid < 64) {
-          const bool valid = lane < nband_total;
-          const uint32_t x = valid ? s_band[lane] : 0u;
-          const bool t = wave_take_best(x, valid, krem);
-          if (valid) s_band[lane] = t ? 1u : 0u;
-        }
-        __syncthreads();
-        w = bpos;
+        if (band & (1u << p)) take |= (s_band[w++] != 0u ? 1u : 0u) << p;
+      return take;
+    }
+    uint32_t br[PER];
+    w = bpos;
 #pragma unroll
-        for (int p = 0; p < PER; ++p)
-          if (band & (1u << p)) take |= (s_band[w++] != 0u ? 1u : 0u) << p;
-      } else {
-        uint32_t br[PER];
-        w = bpos;
+    for (int p = 0; p < PER; ++p) br[p] = (band & (1u << p)) ? s_band[w++] : 0u;
+    return take | wg_topk_mask(br, band, nband_total, krem, ss, ph);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// block-wide selection; grid (Hkv, n), 1024 threads.  Thread t owns blocks
+// j = t*PER + p, p < PER, of its score row (the candidates are ns <= j <
+// ns + nc), so thread order then p is block order.
+// BAND: scores are the approximate MFMA scores with bounds in err (see the
+// top of this file); dynamic LDS then holds the band (u32 per candidate).
+// The scoring also left each chunk's floor (its floor_rank-th largest
+// approximate score): every chunk with a finite floor holds floor_rank
+// candidates at or above it, so when those chunks hold at least K of them,
+// the row's K-th largest exact score is at least tau - e (tau = the least
+// floor), and a candidate with s~ < tau - 2e is certainly out.  The
+// remaining candidates (a few percent of a row of iid scores) are compacted
+// into LDS, one per thread, and the selection runs over them.
+// ---------------------------------------------------------------------------
+template <int DT, int G, bool BAND, int PER>
+__global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch sb,
+                                                        const uint16_t* __restrict__ q,
+                                                        const float* __restrict__ scores,
+                                                        const float* __restrict__ err,
+                                                        int err_stride, int err_count, int floor_rank,
+                                                        int32_t* __restrict__ idx_out) {
+  extern __shared__ uint32_t s_band[];
+  __shared__ SelScratch ss;
+  __shared__ __align__(16) uint32_t s_q[BAND ? G * kHeadDim / 2 : 4];
+  __shared__ float s_lim[2];  // e, tau - 2e
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int h = blockIdx.x, bi = blockIdx.y;
+  const int seq = sb.ids[bi];
+  const int c0 = geo.ns, K = geo.top_k;
+  // scores (and the chunk bounds and floors) are loaded before the sequence
+  // length is known: the row reads stay inside the score buffer (its slack
+  // covers the last row), and entries that are not candidates are never used
+  const int i0 = tid * PER;
+  float sc[PER];
+  load_scores<PER>(score_row(geo, scores, bi, h) + i0, sc);
+  float ev = 0.0f, fl = INFINITY;
+  if (BAND && tid < 64 && lane < err_count) {
+    const float* erow = err + ((size_t)bi * geo.hkv + h) * 2 * err_stride;
+    ev = erow[lane];
+    fl = erow[err_stride + lane];
+  }
+  const int len = entry_len(geo, sb, bi, seq);
+  const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
+  const int nc = nb - geo.nr - c0;
+  int32_t* out = idx_out + ((size_t)bi * geo.hkv + h) * geo.nsel_max;
+  if (!ranked_select(geo, nc)) {  // every block kept, or (top_k 0) sinks and recent only
+    for (int p = tid; p < geo.nsel_max; p += kSelThreads)
+      out[p] = selected_block(p, nb, nc > K, geo.ns, geo.nr, K, nullptr);
+    return;
+  }
+  uint32_t kr[PER];
+  int jr[PER];
+  uint32_t vmask = 0u;
 #pragma unroll
-        for (int p = 0; p < PER; ++p) br[p] = (band & (1u << p)) ? s_band[w++] : 0u;
-        take |= wg_topk_mask(br, band, nband_total, krem, ss, ph);
+  for (int p = 0; p < PER; ++p) {
+    const bool v = i0 + p >= c0 && i0 + p < c0 + nc;
+    kr[p] = v ? score_key(sc[p]) : 0u;
+    jr[p] = i0 + p;
+    vmask |= (uint32_t)v << p;
+  }
+  int ph = 0;
+  uint32_t take;
+  int total;
+  if constexpr (!BAND) {
+    take = select_core<DT, G, BAND, PER>(geo, seq, h, kr, jr, vmask, nc, K, 0.0f, ss, ph, s_band, s_q);
+    const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
+    int w = geo.ns + pos;
+#pragma unroll
+    for (int p = 0; p < PER; ++p)
+      if (take & (1u << p)) out[w++] = jr[p];
+  } else {
+    for (int e = tid; e < G * kHeadDim / 2; e += kSelThreads)
+      s_q[e] = ((const uint32_t*)(q + q_row(sb, bi, h * G + e / (kHeadDim / 2))))[e % (kHeadDim / 2)];
+    if (tid < 64) {
+      // the bound: maximum over the chunks' bounds (NaN bounds are skipped);
+      // the floor: least chunk floor, if the chunks with one hold K
+      const float e = wave_max_f32(ev) * (1.0f + 0x1p-8f) + 0x1p-120f;
+      const float tau = __uint_as_float(wave_allreduce_u32(__float_as_uint(fl), [](uint32_t a, uint32_t b) {
+        return __float_as_uint(fminf(__uint_as_float(a), __uint_as_float(b)));
+      }));
+      const int nfl = __popcll(__ballot(fl < INFINITY));
+      if (tid == 0) {
+        s_lim[0] = e;
+        s_lim[1] = (int64_t)nfl * floor_rank >= K ? tau - 2.0f * e : -INFINITY;
       }
     }
-  }
-  // output: sinks, the chosen candidates in block order, recent blocks
-  int total;
-  const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
-  int w = geo.ns + pos;
+    __syncthreads();
+    const float e = s_lim[0], lim = s_lim[1];
+    // certainly out: below lim (-inf: no floor; a NaN candidate's chunk has
+    // floor -inf, so nothing is dropped then)
+    if (lim > -INFINITY) {
 #pragma unroll
-  for (int p = 0; p < PER; ++p)
-    if (take & (1u << p)) out[w++] = i0 + p;
+      for (int p = 0; p < PER; ++p)
+        if (((vmask >> p) & 1u) && key_value(kr[p]) < lim) vmask &= ~(1u << p);
+    }
+    int nv;
+    const int cpos = wg_scan_excl(__popc(vmask), ss, ph, &nv);
+    if (nv <= kSelThreads) {
+      // one candidate per thread, in block order: keys through the band
+      // buffer (mbps >= nc >= nv words), blocks through the histogram
+      // (2048 words), both free until the selection
+      int w = cpos;
+#pragma unroll
+      for (int p = 0; p < PER; ++p)
+        if ((vmask >> p) & 1u) {
+          s_band[w] = kr[p];
+          ss.hist[w++] = (uint32_t)jr[p];
+        }
+      __syncthreads();
+      const uint32_t k1[1] = {tid < nv ? s_band[tid] : 0u};
+      const int j1[1] = {tid < nv ? (int)ss.hist[tid] : -1};
+      __syncthreads();  // read before the selection reuses both
+      take = select_core<DT, G, BAND, 1>(geo, seq, h, k1, j1, tid < nv ? 1u : 0u, nv, K, e, ss, ph, s_band, s_q);
+      const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
+      if (take) out[geo.ns + pos] = j1[0];
+    } else {
+      take = select_core<DT, G, BAND, PER>(geo, seq, h, kr, jr, vmask, nv, K, e, ss, ph, s_band, s_q);
+      const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
+      int w = geo.ns + pos;
+#pragma unroll
+      for (int p = 0; p < PER; ++p)
+        if (take & (1u << p)) out[w++] = jr[p];
+    }
+  }
+  // sinks, the chosen candidates in block order (above), recent blocks
   for (int p = tid; p < geo.ns; p += kSelThreads) out[p] = p;
   for (int r = tid; r < geo.nr; r += kSelThreads) out[geo.ns + total + r] = nb - geo.nr + r;
   for (int p = geo.ns + total + geo.nr + tid; p < geo.nsel_max; p += kSelThreads) out[p] = -1;
@@ -591,22 +713,22 @@ int mfma_err_stride(const Geometry& g) { return (g.mbps + kMfmaChunk - 1) / kMfm
 
 template <int DT, int G, bool BAND>
 static void select_per(const Geometry& g, const SeqBatch& b, const uint16_t* q, const float* scores,
-                       const float* err, int stride, int chunks, int max_nc, int32_t* idx,
+                       const float* err, int stride, int chunks, int floor_rank, int max_nc, int32_t* idx,
                        hipStream_t s, Timing* prof) {
   const int per = (g.ns + max_nc + kSelThreads - 1) / kSelThreads;  // blocks 0 .. ns + max_nc - 1
   const dim3 grid(g.hkv, b.n), blk(kSelThreads);
   const size_t lds = BAND ? (size_t)g.mbps * 4 : 0;
   if (per <= 1)
-    launch(k_select<DT, G, BAND, 1>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, idx);
+    launch(k_select<DT, G, BAND, 1>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, floor_rank, idx);
   else if (per <= 2)
-    launch(k_select<DT, G, BAND, 2>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, idx);
+    launch(k_select<DT, G, BAND, 2>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, floor_rank, idx);
   else if (per <= 4)
-    launch(k_select<DT, G, BAND, 4>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, idx);
+    launch(k_select<DT, G, BAND, 4>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, floor_rank, idx);
   else if (per <= 8)
-    launch(k_select<DT, G, BAND, 8>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, idx);
+    launch(k_select<DT, G, BAND, 8>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride, chunks, floor_rank, idx);
   else
     launch(k_select<DT, G, BAND, kSelPerMax>, grid, blk, lds, s, prof, kProfTopk, g, b, q, scores, err, stride,
-           chunks, idx);
+           chunks, floor_rank, idx);
 }
 
 template <int DT, int G>
@@ -614,9 +736,11 @@ static void select_wide(const Geometry& g, const SeqBatch& b, const uint16_t* q,
                         float* err, int max_nc, int32_t* idx, hipStream_t s, Timing* prof) {
   const int chunks = (max_nc + kMfmaChunk - 1) / kMfmaChunk;
   const int stride = mfma_err_stride(g);
+  // each chunk's floor_rank-th largest score, so that the chunks hold K
+  const int floor_rank = std::min(8, std::max(1, (g.top_k + chunks - 1) / chunks));
   launch(k_score_mfma<DT, G>, dim3(chunks, g.hkv, b.n), dim3(256), 0, s, prof, kProfScore, g, b, q,
-         scores, err, stride);
-  select_per<DT, G, true>(g, b, q, scores, err, stride, chunks, max_nc, idx, s, prof);
+         scores, err, stride, floor_rank);
+  select_per<DT, G, true>(g, b, q, scores, err, stride, chunks, floor_rank, max_nc, idx, s, prof);
 }
 
 hipError_t launch_select_large(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
@@ -634,8 +758,8 @@ hipError_t launch_select_large(const Geometry& g, const SeqBatch& b, const void*
     return hipGetLastError();
   }
   // exact scores already in `scores`
-  if (g.dtype == 0) select_per<0, 1, false>(g, b, qq, scores, nullptr, 0, 0, max_nc, idx, s, prof);
-  else select_per<1, 1, false>(g, b, qq, scores, nullptr, 0, 0, max_nc, idx, s, prof);
+  if (g.dtype == 0) select_per<0, 1, false>(g, b, qq, scores, nullptr, 0, 0, 1, max_nc, idx, s, prof);
+  else select_per<1, 1, false>(g, b, qq, scores, nullptr, 0, 0, 1, max_nc, idx, s, prof);
   return hipGetLastError();
 }
 
