@@ -57,6 +57,31 @@ __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// DPP inside each 16-lane row (bank b = lanes 4b .. 4b+3 of the row); r and
+// t are constants once the calling loops are unrolled.
+// row_ror: lane n reads lane (n - r) mod 16 of its row (r in {4, 8, 12}).
+__device__ __forceinline__ uint32_t row_ror(uint32_t x, int r) {
+  switch (r) {
+    case 4: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x124, 0xF, 0xF, false);
+    case 8: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, false);
+    case 12: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x12C, 0xF, 0xF, false);
+    default: return x;
+  }
+}
+__device__ __forceinline__ float row_ror(float x, int r) {
+  return __uint_as_float(row_ror(__float_as_uint(x), r));
+}
+// old with bank t (1..3) replaced by src's bank 0
+__device__ __forceinline__ float bank_from0(float old, float src, int t) {
+  const int o = __float_as_int(old), s = __float_as_int(src);
+  switch (t) {
+    case 1: return __int_as_float(__builtin_amdgcn_update_dpp(o, s, 0x124, 0xF, 0x2, false));
+    case 2: return __int_as_float(__builtin_amdgcn_update_dpp(o, s, 0x128, 0xF, 0x4, false));
+    case 3: return __int_as_float(__builtin_amdgcn_update_dpp(o, s, 0x12C, 0xF, 0x8, false));
+    default: return src;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // quantize 8 consecutive dims of one row (lane c of the 16 lanes holding the
 // row; lanes c & ~7 .. +7 hold one 64-dim group) by mlx's affine rule, in
@@ -337,9 +362,21 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
     u32x4 vf[NVF];
 #pragma unroll
     for (int i = 0; i < NVF; ++i) vf[i] = __builtin_nontemporal_load(Vf + i * 64);
-    u32x4 sbv[EPL];
+    // CMP (groups of at most 4 heads): the real heads of a QK tile's scores
+    // are the lanes of bank 0 (n < 4) of each row, so tile t is rotated into
+    // bank t and the per-score work runs on 4 registers instead of EPL;
+    // lane (n, g) then holds head n & 3, tile n >> 2, entries 4 (n >> 2) + i
+    constexpr bool CMP = G <= 4;
+    constexpr int NSB = CMP ? 4 : EPL;  // scale / bias entries per lane
+    const int tcp = n >> 2;
+    u32x4 sbv[NSB];
+    if constexpr (CMP) {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) sbv[e] = Sf[e];
+      for (int i = 0; i < 4; ++i) sbv[i] = tcp < NT ? Sf[4 * tcp + i] : u32x4{0u, 0u, 0u, 0u};
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) sbv[e] = Sf[e];
+    }
     __builtin_amdgcn_sched_barrier(0);
     const u32x4 ones = u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
     const uint32_t one = f16_one_pair();
@@ -348,63 +385,153 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
     qs0 = mfma_f16(ones, qf[1], qs0);
     f32x4 qs1 = mfma_f16(ones, qf[2], f32x4{0.f, 0.f, 0.f, 0.f});
     qs1 = mfma_f16(ones, qf[3], qs1);
-    const float q0 = qs0[0], q1 = qs1[0];
-    const float q0c = q0 * (QC::OFF * QC::INV_UNIT), q1c = q1 * (QC::OFF * QC::INV_UNIT);
-    // raw_g = K-codes-as-fp16 . Q^T per dim group
-    float pv[EPL];
+    // A operands: P_g = p * v_scale_g and p * v_bias_g per dim group
+    u32x4 pa0[KS2], pa1[KS2], pb0[KS2], pb1[KS2];
+    float mx, ps;
+    if constexpr (CMP) {
+      // raw_g = K-codes-as-fp16 . Q^T per dim group, every tile
+      f32x4 r0[NT], r1[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      f32x4 r0 = f32x4{0.f, 0.f, 0.f, 0.f}, r1 = r0;
-      r0 = mfma_f16(k_operand<KB>(kf[t], 0, one), qf[0], r0);
-      r0 = mfma_f16(k_operand<KB>(kf[t], 1, one), qf[1], r0);
-      r1 = mfma_f16(k_operand<KB>(kf[t], 2, one), qf[2], r1);
-      r1 = mfma_f16(k_operand<KB>(kf[t], 3, one), qf[3], r1);
+      for (int t = 0; t < NT; ++t) {
+        r0[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        r1[t] = r0[t];
+        r0[t] = mfma_f16(k_operand<KB>(kf[t], 0, one), qf[0], r0[t]);
+        r0[t] = mfma_f16(k_operand<KB>(kf[t], 1, one), qf[1], r0[t]);
+        r1[t] = mfma_f16(k_operand<KB>(kf[t], 2, one), qf[2], r1[t]);
+        r1[t] = mfma_f16(k_operand<KB>(kf[t], 3, one), qf[3], r1[t]);
+      }
+      f32x4 c0 = r0[0], c1 = r1[0];
+#pragma unroll
+      for (int t = 1; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          c0[i] = bank_from0(c0[i], r0[t][i], t);
+          c1[i] = bank_from0(c1[i], r1[t][i], t);
+        }
+      float q0 = qs0[0], q1 = qs1[0];  // of head n & 3 after the rotations
+#pragma unroll
+      for (int t = 1; t < 4; ++t) {
+        q0 = bank_from0(q0, qs0[0], t);
+        q1 = bank_from0(q1, qs1[0], t);
+      }
+      const float q0c = q0 * (QC::OFF * QC::INV_UNIT), q1c = q1 * (QC::OFF * QC::INV_UNIT);
+      float pv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const u32x4& f = sbv[4 * t + i];
-        const float d0 = __builtin_fmaf(r0[i], QC::INV_UNIT, -q0c);  // sum_d q_d c_d, group 0
-        const float d1 = __builtin_fmaf(r1[i], QC::INV_UNIT, -q1c);
+        const u32x4& f = sbv[i];
+        const float d0 = __builtin_fmaf(c0[i], QC::INV_UNIT, -q0c);
+        const float d1 = __builtin_fmaf(c1[i], QC::INV_UNIT, -q1c);
         float sc = lo_f(f[0]) * d0;
         sc = __builtin_fmaf(lo_f(f[1]), q0, sc);
         sc = __builtin_fmaf(hi_f(f[0]), d1, sc);
         sc = __builtin_fmaf(hi_f(f[1]), q1, sc);
-        pv[4 * t + i] = sc * sl2;
+        pv[i] = sc * sl2;
       }
-    }
-    if (valid < TB) {
-      // tokens past the end: no score, and no stale scale / bias reaches PV
+      // tokens past the end (and, for 32-token blocks, the banks past the
+      // block's two tiles): no score, and no stale scale / bias reaches PV
+      if (NT < 4 || valid < TB) {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e)
-        if (tok_of(g, e) >= valid) {
-          pv[e] = -INFINITY;
-          sbv[e] = u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < 4; ++i)
+          if (tok_of(g, 4 * tcp + i) >= valid) {
+            pv[i] = -INFINITY;
+            sbv[i] = u32x4{0u, 0u, 0u, 0u};
+          }
+      }
+      // per head: over the lane's entries, the row's 4 banks, the 4 rows
+      float m = fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3]));
+      m = fmaxf(m, row_ror(m, 4));
+      m = fmaxf(m, row_ror(m, 8));
+      mx = max_over_groups(m);
+      ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pv[i] = __builtin_amdgcn_exp2f(pv[i] - mx);
+        ps += pv[i];
+      }
+      ps += row_ror(ps, 4);
+      ps += row_ror(ps, 8);
+      ps = sum_over_groups(ps);
+      // compact pairs (entries 2 pp, 2 pp + 1), then each A operand pair jj
+      // of k-step s2 (tokens of tile 2 s2 + jj / 2, entries 2 (jj % 2) ..)
+      // is rotated from its tile's bank into bank 0 (rows of the other banks
+      // are heads past the group, never stored)
+      uint32_t ca0[2], ca1[2], cb0[2], cb1[2];
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const float p0 = pv[2 * pp], p1 = pv[2 * pp + 1];
+        const u32x4 &f0 = sbv[2 * pp], &f1 = sbv[2 * pp + 1];
+        ca0[pp] = cvt_pk<0>(p0 * lo_f(f0[2]), p1 * lo_f(f1[2]));
+        ca1[pp] = cvt_pk<0>(p0 * hi_f(f0[2]), p1 * hi_f(f1[2]));
+        cb0[pp] = cvt_pk<0>(p0 * lo_f(f0[3]), p1 * lo_f(f1[3]));
+        cb1[pp] = cvt_pk<0>(p0 * hi_f(f0[3]), p1 * hi_f(f1[3]));
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < KS2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int r = (16 - 4 * (2 * s2 + (jj >> 1))) & 15, pp = jj & 1;
+          pa0[s2][jj] = row_ror(ca0[pp], r);
+          pa1[s2][jj] = row_ror(ca1[pp], r);
+          pb0[s2][jj] = row_ror(cb0[pp], r);
+          pb1[s2][jj] = row_ror(cb1[pp], r);
+        }
+    } else {
+      const float q0 = qs0[0], q1 = qs1[0];
+      const float q0c = q0 * (QC::OFF * QC::INV_UNIT), q1c = q1 * (QC::OFF * QC::INV_UNIT);
+      // raw_g = K-codes-as-fp16 . Q^T per dim group
+      float pv[EPL];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        f32x4 r0 = f32x4{0.f, 0.f, 0.f, 0.f}, r1 = r0;
+        r0 = mfma_f16(k_operand<KB>(kf[t], 0, one), qf[0], r0);
+        r0 = mfma_f16(k_operand<KB>(kf[t], 1, one), qf[1], r0);
+        r1 = mfma_f16(k_operand<KB>(kf[t], 2, one), qf[2], r1);
+        r1 = mfma_f16(k_operand<KB>(kf[t], 3, one), qf[3], r1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const u32x4& f = sbv[4 * t + i];
+          const float d0 = __builtin_fmaf(r0[i], QC::INV_UNIT, -q0c);  // sum_d q_d c_d, group 0
+          const float d1 = __builtin_fmaf(r1[i], QC::INV_UNIT, -q1c);
+          float sc = lo_f(f[0]) * d0;
+          sc = __builtin_fmaf(lo_f(f[1]), q0, sc);
+          sc = __builtin_fmaf(hi_f(f[0]), d1, sc);
+          sc = __builtin_fmaf(hi_f(f[1]), q1, sc);
+          pv[4 * t + i] = sc * sl2;
+        }
+      }
+      if (valid < TB) {
+        // tokens past the end: no score, and no stale scale / bias reaches PV
+#pragma unroll
+        for (int e = 0; e < EPL; ++e)
+          if (tok_of(g, e) >= valid) {
+            pv[e] = -INFINITY;
+            sbv[e] = u32x4{0u, 0u, 0u, 0u};
+          }
+      }
+      mx = pv[0];
+#pragma unroll
+      for (int e = 1; e < EPL; ++e) mx = fmaxf(mx, pv[e]);
+      mx = max_over_groups(mx);
+      ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        pv[e] = __builtin_amdgcn_exp2f(pv[e] - mx);
+        ps += pv[e];
+      }
+      ps = sum_over_groups(ps);
+#pragma unroll
+      for (int s2 = 0; s2 < KS2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int e0 = 8 * s2 + 2 * jj, e1 = e0 + 1;
+          const float p0 = pv[e0], p1 = pv[e1];
+          const u32x4 &f0 = sbv[e0], &f1 = sbv[e1];
+          pa0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[2]), p1 * lo_f(f1[2]));
+          pa1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[2]), p1 * hi_f(f1[2]));
+          pb0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[3]), p1 * lo_f(f1[3]));
+          pb1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[3]), p1 * hi_f(f1[3]));
         }
     }
-    float mx = pv[0];
-#pragma unroll
-    for (int e = 1; e < EPL; ++e) mx = fmaxf(mx, pv[e]);
-    mx = max_over_groups(mx);
-    float ps = 0.f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      pv[e] = __builtin_amdgcn_exp2f(pv[e] - mx);
-      ps += pv[e];
-    }
-    ps = sum_over_groups(ps);
-    // A operands: P_g = p * v_scale_g and p * v_bias_g per dim group
-    u32x4 pa0[KS2], pa1[KS2], pb0[KS2], pb1[KS2];
-#pragma unroll
-    for (int s2 = 0; s2 < KS2; ++s2)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int e0 = 8 * s2 + 2 * jj, e1 = e0 + 1;
-        const float p0 = pv[e0], p1 = pv[e1];
-        const u32x4 &f0 = sbv[e0], &f1 = sbv[e1];
-        pa0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[2]), p1 * lo_f(f1[2]));
-        pa1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[2]), p1 * hi_f(f1[2]));
-        pb0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[3]), p1 * lo_f(f1[3]));
-        pb1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[3]), p1 * hi_f(f1[3]));
-      }
     // sum_t P_g and sum_t p v_bias_g, in O's accumulator layout
     f32x4 ps0 = f32x4{0.f, 0.f, 0.f, 0.f}, ps1 = ps0, vb0 = ps0, vb1 = ps0;
 #pragma unroll
