@@ -229,6 +229,33 @@ __device__ __forceinline__ void wave_lds_order() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// The bin of a kWaveBins-bin LDS histogram (bins filled, read-only here)
+// that holds the need-th largest key: lane l owns bins kWaveBins-1 - 16l - j,
+// j < 16 (descending), so a scan of the lanes' sums counts the keys in
+// higher bins; the owning lane's 16 bins are then scanned by 16 lanes.
+// b_star: the bin; abv: keys in higher bins; cnt: keys in b_star.
+__device__ __forceinline__ void find_kth_bin(const uint32_t* hist, int need, int& b_star, int& abv, int& cnt) {
+  constexpr int BPL = kWaveBins / 64;
+  const int lane = threadIdx.x & 63;
+  const u32x4* r4 = (const u32x4*)(hist + kWaveBins - BPL * (lane + 1));
+  int lsum = 0;
+#pragma unroll
+  for (int i = 0; i < BPL / 4; ++i) {
+    const u32x4 v = r4[i];
+    lsum += (int)(v[0] + v[1] + v[2] + v[3]);
+  }
+  const int incl = wave_scan_incl(lsum);
+  const int excl = incl - lsum;
+  const int src = __ffsll((unsigned long long)__ballot(excl < need && need <= incl)) - 1;
+  const int base = __builtin_amdgcn_readlane(excl, src);
+  const int ct = lane < BPL ? (int)hist[kWaveBins - 1 - BPL * src - lane] : 0;
+  const int ci = wave_scan_incl(ct);
+  const int js = __ffsll((unsigned long long)__ballot(lane < BPL && base + ci - ct < need && need <= base + ci)) - 1;
+  b_star = kWaveBins - 1 - BPL * src - js;
+  abv = base + __builtin_amdgcn_readlane(ci - ct, js);
+  cnt = __builtin_amdgcn_readlane(ct, js);
+}
+
 template <int S>
 __device__ __forceinline__ uint32_t wave_kth_key(const uint32_t (&key)[S], int nc, int K, uint32_t* ws) {
   const int lane = threadIdx.x & 63;
@@ -253,7 +280,8 @@ __device__ __forceinline__ uint32_t wave_kth_key(const uint32_t (&key)[S], int n
     // exponents), later passes by key bits
     const float vlo = key_value(lo), span = key_value(hi) - vlo;
     const bool use_v = by_value && __builtin_isfinite(vlo) && __builtin_isfinite(span) && span > 0.0f;
-    const float scale = use_v ? (float)(kWaveBins - 1) / span : 0.0f;
+    // bins need only be monotone in the key: an approximate reciprocal will do
+    const float scale = use_v ? (float)(kWaveBins - 1) * __builtin_amdgcn_rcpf(span) : 0.0f;
     const int sh = use_v ? 0 : max(0, 32 - __clz(hi - lo) - 10);  // (hi - lo) >> sh < 1024
     auto bin = [&](uint32_t k) -> int {
       return use_v ? min(kWaveBins - 1, (int)((key_value(k) - vlo) * scale)) : (int)((k - lo) >> sh);
@@ -262,44 +290,15 @@ __device__ __forceinline__ uint32_t wave_kth_key(const uint32_t (&key)[S], int n
 #pragma unroll
     for (int i = 0; i < kWaveBins / 256; ++i) h4[i] = u32x4{0u, 0u, 0u, 0u};
     wave_lds_order();
+    int bk[S];  // each key's bin in this pass, -1 outside the range
 #pragma unroll
-    for (int k = 0; k < S; ++k)
-      if (lane + 64 * k < nc && key[k] >= lo && key[k] <= hi) atomicAdd(&hist[bin(key[k])], 1u);
+    for (int k = 0; k < S; ++k) {
+      bk[k] = lane + 64 * k < nc && key[k] >= lo && key[k] <= hi ? bin(key[k]) : -1;
+      if (bk[k] >= 0) atomicAdd(&hist[bk[k]], 1u);
+    }
     wave_lds_order();
-    // lane l owns bins 1023 - 16l - j, j < 16 (descending), so a scan over
-    // lanes counts the keys in higher bins
-    constexpr int BPL = kWaveBins / 64;
-    const u32x4* r4 = (const u32x4*)(hist + kWaveBins - BPL * (lane + 1));
-    uint32_t c[BPL];  // c[j] = bin 1023 - 16 * lane - j
-#pragma unroll
-    for (int i = 0; i < BPL / 4; ++i) {
-      const u32x4 v = r4[i];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) c[BPL - 1 - (4 * i + e)] = v[e];
-    }
-    int lsum = 0;
-#pragma unroll
-    for (int j = 0; j < BPL; ++j) lsum += (int)c[j];
-    const int incl = wave_scan_incl(lsum);
-    const int excl = incl - lsum;
-    const bool mine = excl < need && need <= incl;
-    int b_star = 0, abv = 0, cnt = 0;
-    if (mine) {
-      int cum = excl;
-#pragma unroll
-      for (int j = 0; j < BPL; ++j) {
-        if (cum < need && need <= cum + (int)c[j]) {
-          b_star = kWaveBins - 1 - BPL * lane - j;
-          abv = cum;
-          cnt = (int)c[j];
-        }
-        cum += (int)c[j];
-      }
-    }
-    const int src = __ffsll((unsigned long long)__ballot(mine)) - 1;
-    b_star = __builtin_amdgcn_readlane(b_star, src);
-    abv = __builtin_amdgcn_readlane(abv, src);
-    cnt = __builtin_amdgcn_readlane(cnt, src);
+    int b_star, abv, cnt;
+    find_kth_bin(hist, need, b_star, abv, cnt);
     need -= abv;
     if (!use_v && sh == 0) return lo + (uint32_t)b_star;  // one-value bin
     if (cnt <= 64) {
@@ -307,7 +306,7 @@ __device__ __forceinline__ uint32_t wave_kth_key(const uint32_t (&key)[S], int n
       int base = 0;
 #pragma unroll
       for (int k = 0; k < S; ++k) {
-        const bool in = lane + 64 * k < nc && key[k] >= lo && key[k] <= hi && bin(key[k]) == b_star;
+        const bool in = bk[k] == b_star;
         const uint64_t m = __ballot(in);
         if (in) small[base + __popcll(m & below)] = key[k];
         base += __popcll(m);
@@ -342,7 +341,7 @@ __device__ __forceinline__ uint32_t wave_kth_key(const uint32_t (&key)[S], int n
       uint32_t nlo = 0xFFFFFFFFu, nhi = 0u;
 #pragma unroll
       for (int k = 0; k < S; ++k)
-        if (lane + 64 * k < nc && key[k] >= lo && key[k] <= hi && bin(key[k]) == b_star) {
+        if (bk[k] == b_star) {
           nlo = min(nlo, key[k]);
           nhi = max(nhi, key[k]);
         }
@@ -498,7 +497,8 @@ __device__ __forceinline__ uint32_t wg_kth_key(const uint32_t (&key)[S], const b
     if (lo == hi) return lo;
     const float vlo = key_value(lo), span = key_value(hi) - vlo;
     const bool use_v = by_value && __builtin_isfinite(vlo) && __builtin_isfinite(span) && span > 0.0f;
-    const float scale = use_v ? (float)(kWaveBins - 1) / span : 0.0f;
+    // bins need only be monotone in the key: an approximate reciprocal will do
+    const float scale = use_v ? (float)(kWaveBins - 1) * __builtin_amdgcn_rcpf(span) : 0.0f;
     const int sh = use_v ? 0 : max(0, 32 - __clz(hi - lo) - 10);
     auto bin = [&](uint32_t k) -> int {
       return use_v ? min(kWaveBins - 1, (int)((key_value(k) - vlo) * scale)) : (int)((k - lo) >> sh);
@@ -508,42 +508,15 @@ __device__ __forceinline__ uint32_t wg_kth_key(const uint32_t (&key)[S], const b
     for (int i = threadIdx.x; i < kWaveBins / 4; i += 64 * W) ((u32x4*)hist)[i] = u32x4{0u, 0u, 0u, 0u};
     if (threadIdx.x == 0) *small_n = 0u;
     __syncthreads();
+    int bk[S];  // each key's bin in this pass, -1 outside the range
 #pragma unroll
-    for (int k = 0; k < S; ++k)
-      if (real[k] && key[k] >= lo && key[k] <= hi) atomicAdd(&hist[bin(key[k])], 1u);
+    for (int k = 0; k < S; ++k) {
+      bk[k] = real[k] && key[k] >= lo && key[k] <= hi ? bin(key[k]) : -1;
+      if (bk[k] >= 0) atomicAdd(&hist[bk[k]], 1u);
+    }
     __syncthreads();
-    constexpr int BPL = kWaveBins / 64;
-    const u32x4* r4 = (const u32x4*)(hist + kWaveBins - BPL * (lane + 1));
-    uint32_t c[BPL];
-#pragma unroll
-    for (int i = 0; i < BPL / 4; ++i) {
-      const u32x4 v = r4[i];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) c[BPL - 1 - (4 * i + e)] = v[e];
-    }
-    int lsum = 0;
-#pragma unroll
-    for (int j = 0; j < BPL; ++j) lsum += (int)c[j];
-    const int incl = wave_scan_incl(lsum);
-    const int excl = incl - lsum;
-    const bool mine = excl < need && need <= incl;
-    int b_star = 0, abv = 0, cnt = 0;
-    if (mine) {
-      int cum = excl;
-#pragma unroll
-      for (int j = 0; j < BPL; ++j) {
-        if (cum < need && need <= cum + (int)c[j]) {
-          b_star = kWaveBins - 1 - BPL * lane - j;
-          abv = cum;
-          cnt = (int)c[j];
-        }
-        cum += (int)c[j];
-      }
-    }
-    const int src = __ffsll((unsigned long long)__ballot(mine)) - 1;
-    b_star = __builtin_amdgcn_readlane(b_star, src);
-    abv = __builtin_amdgcn_readlane(abv, src);
-    cnt = __builtin_amdgcn_readlane(cnt, src);
+    int b_star, abv, cnt;
+    find_kth_bin(hist, need, b_star, abv, cnt);
     need -= abv;
     if (!use_v && sh == 0) return lo + (uint32_t)b_star;  // one-value bin
     if (cnt <= 64) {
@@ -552,7 +525,7 @@ __device__ __forceinline__ uint32_t wg_kth_key(const uint32_t (&key)[S], const b
       uint64_t m[S];
 #pragma unroll
       for (int k = 0; k < S; ++k) {
-        m[k] = __ballot(real[k] && key[k] >= lo && key[k] <= hi && bin(key[k]) == b_star);
+        m[k] = __ballot(bk[k] == b_star);
         mine_n += __popcll(m[k]);
       }
       uint32_t base = 0u;
@@ -593,7 +566,7 @@ __device__ __forceinline__ uint32_t wg_kth_key(const uint32_t (&key)[S], const b
       uint32_t nlo = 0xFFFFFFFFu, nhi = 0u;
 #pragma unroll
       for (int k = 0; k < S; ++k)
-        if (real[k] && key[k] >= lo && key[k] <= hi && bin(key[k]) == b_star) {
+        if (bk[k] == b_star) {
           nlo = min(nlo, key[k]);
           nhi = max(nhi, key[k]);
         }
