@@ -36,20 +36,52 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 __device__ __forceinline__ float lo_f(uint32_t w) { return h2f(w & 0xFFFFu); }
 __device__ __forceinline__ float hi_f(uint32_t w) { return h2f(w >> 16); }
 
+// Codes as the decode kernel's MFMA operands: int8 code c is the fp16
+// 1024 + c (byte_to_f16); an int4 word (element e in nibble q_nib(e)) gives
+// pairs 0 and 2 (elements 0, 1, 4, 5) as 1024 + c and pairs 1 and 3
+// (elements 2, 3, 6, 7) as 1024 + 16 c: pair k's nibbles k and k + 4 sit at
+// bits 4 (k & 1) and 16 + 4 (k & 1) once the word is shifted by 8 (k >> 1),
+// inside the fp16 mantissa under the exponent of 1024, so a word costs one
+// shift and four v_and_or_b32 (base: 0x64006400 in a VGPR).  The other
+// operand of each unit-16 element is scaled by 1/16 (kUnit16), so every
+// product is q c (or p c) plus 1024 times the other operand, and
+// sum (1024 + u c) x = sum x c u + 1024 sum x removes the offset with the sum
+// of the same scaled operand.
+__device__ __forceinline__ u32x4 nib_to_f16_dec(uint32_t w, uint32_t base) {
+  const uint32_t w8 = w >> 8;
+  return u32x4{(w & 0x000F000Fu) | base, (w & 0x00F000F0u) | base, (w8 & 0x000F000Fu) | base,
+               (w8 & 0x00F000F0u) | base};
+}
+constexpr float kDecOff = 1024.0f;  // value of code 0 in the decode operands
+constexpr float kUnit16 = 0.0625f;  // scale of the other operand at unit-16 int4 elements
+
+// 0x64006400 (two fp16 1024.0) in a VGPR the compiler cannot fold
+__device__ __forceinline__ uint32_t f16_pair_1024() {
+  uint32_t v;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(v));
+  return v;
+}
+
 // A operand of QK token tile t, k-step s, from the tile's K fragments
 template <int KB>
-__device__ __forceinline__ u32x4 k_operand(const u32x4* kf, int s, uint32_t one) {
-  if constexpr (KB == 4) return nib_to_f16(kf[0][s], one);
+__device__ __forceinline__ u32x4 k_operand(const u32x4* kf, int s, uint32_t base) {
+  if constexpr (KB == 4) return nib_to_f16_dec(kf[0][s], base);
   else return byte_to_f16(kf[s >> 1][2 * (s & 1)], kf[s >> 1][2 * (s & 1) + 1]);
 }
 
 // B operand of PV dim tile dt, k-step s2, from the V fragments
 template <int KB, int KS2>
-__device__ __forceinline__ u32x4 v_operand(const u32x4* vf, int dt, int s2, uint32_t one) {
+__device__ __forceinline__ u32x4 v_operand(const u32x4* vf, int dt, int s2, uint32_t base) {
   constexpr int DPF = QCode<KB>::DPF;
   const u32x4& f = vf[(dt / DPF) * KS2 + s2];
-  if constexpr (KB == 4) return nib_to_f16(f[dt & 3], one);
+  if constexpr (KB == 4) return nib_to_f16_dec(f[dt & 3], base);
   else return byte_to_f16(f[2 * (dt & 1)], f[2 * (dt & 1) + 1]);
+}
+
+// x * 1/16 on both fp16 halves (exact unless the result is below fp16's
+// normal range)
+__device__ __forceinline__ uint32_t f16x2_unit16(uint32_t x) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, x) * f16x2{(_Float16)kUnit16, (_Float16)kUnit16});
 }
 
 __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
@@ -379,12 +411,31 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
     }
     __builtin_amdgcn_sched_barrier(0);
     const u32x4 ones = u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
-    const uint32_t one = f16_one_pair();
-    // Q_g = sum of q over dim group g, for head n (every accumulator entry)
-    f32x4 qs0 = mfma_f16(ones, qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
-    qs0 = mfma_f16(ones, qf[1], qs0);
-    f32x4 qs1 = mfma_f16(ones, qf[2], f32x4{0.f, 0.f, 0.f, 0.f});
-    qs1 = mfma_f16(ones, qf[3], qs1);
+    const uint32_t base = f16_pair_1024();
+    // the QK operand: q, with int4's unit-16 elements (2, 3, 6, 7 of every
+    // k-step) scaled by 1/16
+    u32x4 qk[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      qk[s] = qf[s];
+      if constexpr (KB == 4) {
+        qk[s][1] = f16x2_unit16(qf[s][1]);
+        qk[s][3] = f16x2_unit16(qf[s][3]);
+      }
+    }
+    // per dim group g, for head n (every accumulator entry): the sum of the
+    // QK operand (qs, for the code offset) and of q (qb, for the biases)
+    f32x4 qs0 = mfma_f16(ones, qk[0], f32x4{0.f, 0.f, 0.f, 0.f});
+    qs0 = mfma_f16(ones, qk[1], qs0);
+    f32x4 qs1 = mfma_f16(ones, qk[2], f32x4{0.f, 0.f, 0.f, 0.f});
+    qs1 = mfma_f16(ones, qk[3], qs1);
+    f32x4 qb0 = qs0, qb1 = qs1;
+    if constexpr (KB == 4) {
+      qb0 = mfma_f16(ones, qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      qb0 = mfma_f16(ones, qf[1], qb0);
+      qb1 = mfma_f16(ones, qf[2], f32x4{0.f, 0.f, 0.f, 0.f});
+      qb1 = mfma_f16(ones, qf[3], qb1);
+    }
     // A operands: P_g = p * v_scale_g and p * v_bias_g per dim group
     u32x4 pa0[KS2], pa1[KS2], pb0[KS2], pb1[KS2];
     float mx, ps;
@@ -395,10 +446,10 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
       for (int t = 0; t < NT; ++t) {
         r0[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         r1[t] = r0[t];
-        r0[t] = mfma_f16(k_operand<KB>(kf[t], 0, one), qf[0], r0[t]);
-        r0[t] = mfma_f16(k_operand<KB>(kf[t], 1, one), qf[1], r0[t]);
-        r1[t] = mfma_f16(k_operand<KB>(kf[t], 2, one), qf[2], r1[t]);
-        r1[t] = mfma_f16(k_operand<KB>(kf[t], 3, one), qf[3], r1[t]);
+        r0[t] = mfma_f16(k_operand<KB>(kf[t], 0, base), qk[0], r0[t]);
+        r0[t] = mfma_f16(k_operand<KB>(kf[t], 1, base), qk[1], r0[t]);
+        r1[t] = mfma_f16(k_operand<KB>(kf[t], 2, base), qk[2], r1[t]);
+        r1[t] = mfma_f16(k_operand<KB>(kf[t], 3, base), qk[3], r1[t]);
       }
       f32x4 c0 = r0[0], c1 = r1[0];
 #pragma unroll
@@ -408,19 +459,29 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
           c0[i] = bank_from0(c0[i], r0[t][i], t);
           c1[i] = bank_from0(c1[i], r1[t][i], t);
         }
-      float q0 = qs0[0], q1 = qs1[0];  // of head n & 3 after the rotations
+      // of head n & 3 after the rotations
+      float q0c = qs0[0], q1c = qs1[0], q0 = qb0[0], q1 = qb1[0];
 #pragma unroll
       for (int t = 1; t < 4; ++t) {
-        q0 = bank_from0(q0, qs0[0], t);
-        q1 = bank_from0(q1, qs1[0], t);
+        q0c = bank_from0(q0c, qs0[0], t);
+        q1c = bank_from0(q1c, qs1[0], t);
+        if constexpr (KB == 4) {
+          q0 = bank_from0(q0, qb0[0], t);
+          q1 = bank_from0(q1, qb1[0], t);
+        }
       }
-      const float q0c = q0 * (QC::OFF * QC::INV_UNIT), q1c = q1 * (QC::OFF * QC::INV_UNIT);
+      if constexpr (KB != 4) {
+        q0 = q0c;
+        q1 = q1c;
+      }
+      q0c *= kDecOff;
+      q1c *= kDecOff;
       float pv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const u32x4& f = sbv[i];
-        const float d0 = __builtin_fmaf(c0[i], QC::INV_UNIT, -q0c);
-        const float d1 = __builtin_fmaf(c1[i], QC::INV_UNIT, -q1c);
+        const float d0 = c0[i] - q0c;  // sum_d q_d c_d, group 0
+        const float d1 = c1[i] - q1c;
         float sc = lo_f(f[0]) * d0;
         sc = __builtin_fmaf(lo_f(f[1]), q0, sc);
         sc = __builtin_fmaf(hi_f(f[0]), d1, sc);
@@ -455,13 +516,15 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
       // of k-step s2 (tokens of tile 2 s2 + jj / 2, entries 2 (jj % 2) ..)
       // is rotated from its tile's bank into bank 0 (rows of the other banks
       // are heads past the group, never stored)
+      // (pair 1's tokens meet int4's unit-16 V elements: P_g takes 1/16)
       uint32_t ca0[2], ca1[2], cb0[2], cb1[2];
 #pragma unroll
       for (int pp = 0; pp < 2; ++pp) {
         const float p0 = pv[2 * pp], p1 = pv[2 * pp + 1];
+        const float u = KB == 4 && pp == 1 ? kUnit16 : 1.0f;
         const u32x4 &f0 = sbv[2 * pp], &f1 = sbv[2 * pp + 1];
-        ca0[pp] = cvt_pk<0>(p0 * lo_f(f0[2]), p1 * lo_f(f1[2]));
-        ca1[pp] = cvt_pk<0>(p0 * hi_f(f0[2]), p1 * hi_f(f1[2]));
+        ca0[pp] = cvt_pk<0>(p0 * u * lo_f(f0[2]), p1 * u * lo_f(f1[2]));
+        ca1[pp] = cvt_pk<0>(p0 * u * hi_f(f0[2]), p1 * u * hi_f(f1[2]));
         cb0[pp] = cvt_pk<0>(p0 * lo_f(f0[3]), p1 * lo_f(f1[3]));
         cb1[pp] = cvt_pk<0>(p0 * hi_f(f0[3]), p1 * hi_f(f1[3]));
       }
@@ -476,22 +539,22 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
           pb1[s2][jj] = row_ror(cb1[pp], r);
         }
     } else {
-      const float q0 = qs0[0], q1 = qs1[0];
-      const float q0c = q0 * (QC::OFF * QC::INV_UNIT), q1c = q1 * (QC::OFF * QC::INV_UNIT);
+      const float q0 = qb0[0], q1 = qb1[0];
+      const float q0c = qs0[0] * kDecOff, q1c = qs1[0] * kDecOff;
       // raw_g = K-codes-as-fp16 . Q^T per dim group
       float pv[EPL];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         f32x4 r0 = f32x4{0.f, 0.f, 0.f, 0.f}, r1 = r0;
-        r0 = mfma_f16(k_operand<KB>(kf[t], 0, one), qf[0], r0);
-        r0 = mfma_f16(k_operand<KB>(kf[t], 1, one), qf[1], r0);
-        r1 = mfma_f16(k_operand<KB>(kf[t], 2, one), qf[2], r1);
-        r1 = mfma_f16(k_operand<KB>(kf[t], 3, one), qf[3], r1);
+        r0 = mfma_f16(k_operand<KB>(kf[t], 0, base), qk[0], r0);
+        r0 = mfma_f16(k_operand<KB>(kf[t], 1, base), qk[1], r0);
+        r1 = mfma_f16(k_operand<KB>(kf[t], 2, base), qk[2], r1);
+        r1 = mfma_f16(k_operand<KB>(kf[t], 3, base), qk[3], r1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const u32x4& f = sbv[4 * t + i];
-          const float d0 = __builtin_fmaf(r0[i], QC::INV_UNIT, -q0c);  // sum_d q_d c_d, group 0
-          const float d1 = __builtin_fmaf(r1[i], QC::INV_UNIT, -q1c);
+          const float d0 = r0[i] - q0c;  // sum_d q_d c_d, group 0
+          const float d1 = r1[i] - q1c;
           float sc = lo_f(f[0]) * d0;
           sc = __builtin_fmaf(lo_f(f[1]), q0, sc);
           sc = __builtin_fmaf(hi_f(f[0]), d1, sc);
@@ -525,9 +588,10 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
         for (int jj = 0; jj < 4; ++jj) {
           const int e0 = 8 * s2 + 2 * jj, e1 = e0 + 1;
           const float p0 = pv[e0], p1 = pv[e1];
+          const float u = KB == 4 && (jj & 1) ? kUnit16 : 1.0f;  // int4's unit-16 V elements
           const u32x4 &f0 = sbv[e0], &f1 = sbv[e1];
-          pa0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[2]), p1 * lo_f(f1[2]));
-          pa1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[2]), p1 * hi_f(f1[2]));
+          pa0[s2][jj] = cvt_pk<0>(p0 * u * lo_f(f0[2]), p1 * u * lo_f(f1[2]));
+          pa1[s2][jj] = cvt_pk<0>(p0 * u * hi_f(f0[2]), p1 * u * hi_f(f1[2]));
           pb0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[3]), p1 * lo_f(f1[3]));
           pb1[s2][jj] = cvt_pk<0>(p0 * hi_f(f0[3]), p1 * hi_f(f1[3]));
         }
@@ -546,11 +610,11 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
     for (int dt = 0; dt < 8; ++dt) {
       f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s2 = 0; s2 < KS2; ++s2) o = mfma_f16(dt < 4 ? pa0[s2] : pa1[s2], v_operand<KB, KS2>(vf, dt, s2, one), o);
+      for (int s2 = 0; s2 < KS2; ++s2) o = mfma_f16(dt < 4 ? pa0[s2] : pa1[s2], v_operand<KB, KS2>(vf, dt, s2, base), o);
       const f32x4& psg = dt < 4 ? ps0 : ps1;
       const f32x4& vbg = dt < 4 ? vb0 : vb1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(o[i] - QC::OFF * psg[i], QC::INV_UNIT, vbg[i]);
+      for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(-kDecOff, psg[i], o[i]) + vbg[i];
       store_o_tile<G>(s_o[wave], dt, n, g, o);
     }
     if (g == 0 && n < G) {
