@@ -6,16 +6,19 @@
 // attention kernel's MFMA operands need them, so every gather load is a
 // contiguous 1 KiB fragment, and the scales / biases of a lane group's
 // tokens as one contiguous run.  Dequantisation is fused into the MFMAs:
-//   - a code c becomes the exact fp16 value OFF + UNIT * c (int4: 1 + c/16,
-//     int8: 1024 + c) with two bit operations per pair, no conversion;
-//   - QK per group g of 64 dims: raw_g = sum_d q_d (OFF + UNIT c_d), so
-//     sum_d q_d c_d = (raw_g - OFF * Q_g) / UNIT with Q_g = sum_d q_d (one
-//     MFMA against an all-ones operand), and
-//     s = sum_g k_scale_g * sum_d q_d c_d + k_bias_g * Q_g;
-//   - PV per group: P_g = p * v_scale_g (fp16) is the A operand against the
-//     codes; the same P_g and p * v_bias_g against an all-ones operand give
-//     sum_t P_g and sum_t p v_bias_g in the accumulator layout of O, so
-//     o = (raw - OFF * sum P_g) / UNIT + sum p v_bias_g needs no shuffles.
+//   - a code c becomes the exact fp16 value 1024 + u c with bit operations
+//     only (int8: u = 1; int4: u = 1 or 16 by the element's place in its
+//     word, the other operand of a unit-16 element taking 1/16, so that
+//     every product is the other operand times c plus 1024 times it);
+//   - QK per group g of 64 dims: raw_g = sum_d q'_d (1024 + u_d c_d), so
+//     sum_d q_d c_d = raw_g - 1024 Q'_g with Q'_g = sum_d q'_d (one MFMA
+//     against an all-ones operand; q' = q with the 1/16 applied), and
+//     s = sum_g k_scale_g * sum_d q_d c_d + k_bias_g * Q_g (Q_g = sum_d q_d);
+//   - PV per group: P_g = p * v_scale_g (fp16, times 1/16 at unit-16
+//     tokens) is the A operand against the codes; the same P_g and
+//     p * v_bias_g against an all-ones operand give sum_t P_g and
+//     sum_t p v_bias_g in the accumulator layout of O, so
+//     o = raw - 1024 sum P_g + sum p v_bias_g needs no shuffles.
 // Summaries of a quantized cache are fp16 means of the dequantized keys
 // (fmaf(scale, code, bias), sequential fold), so scoring and selection are
 // the 16-bit kernels' own.
