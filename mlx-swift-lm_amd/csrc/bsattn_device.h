@@ -751,23 +751,14 @@ __host__ __device__ inline int sb_entry(int tb, int tok) {
 }
 
 // int4 word (element e in nibble q_nib(e)) -> 8 fp16 values 1 + c/16, in
-// element order: pair k = elements 2k, 2k+1 = nibbles k, k+4
-// one: 0x3C003C00 held in a VGPR (f16_one_pair()), so that each pair is a
-// shift and one v_and_or_b32 (a VOP3 takes the mask from an SGPR and the
-// constant from the VGPR; with both constant the compiler emits and + or)
-__device__ __forceinline__ u32x4 nib_to_f16(uint32_t w, uint32_t one) {
-  constexpr uint32_t M = 0x03C003C0u;
-  return u32x4{((w << 6) & M) | one, ((w << 2) & M) | one, ((w >> 2) & M) | one,
-               ((w >> 6) & M) | one};
+// element order: pair k = elements 2k, 2k+1 = nibbles k, k+4 (the prefill
+// kernel's per-workgroup dequantisation)
+__device__ __forceinline__ u32x4 nib_to_f16(uint32_t w) {
+  constexpr uint32_t M = 0x03C003C0u, ONE = 0x3C003C00u;
+  return u32x4{((w << 6) & M) | ONE, ((w << 2) & M) | ONE, ((w >> 2) & M) | ONE,
+               ((w >> 6) & M) | ONE};
 }
-__device__ __forceinline__ u32x4 nib_to_f16(uint32_t w) { return nib_to_f16(w, 0x3C003C00u); }
 
-// 0x3C003C00 (two fp16 ones) in a VGPR the compiler cannot fold
-__device__ __forceinline__ uint32_t f16_one_pair() {
-  uint32_t one;
-  asm("v_mov_b32 %0, 0x3c003c00" : "=v"(one));
-  return one;
-}
 
 // two int8 words (element e in byte e) -> 8 fp16 values 1024 + c: each
 // byte becomes the low byte of an fp16 whose high byte is 0x64

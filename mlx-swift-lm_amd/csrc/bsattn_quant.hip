@@ -58,11 +58,12 @@ __device__ __forceinline__ u32x4 nib_to_f16_dec(uint32_t w, uint32_t base) {
 constexpr float kDecOff = 1024.0f;  // value of code 0 in the decode operands
 constexpr float kUnit16 = 0.0625f;  // scale of the other operand at unit-16 int4 elements
 
-// 0x64006400 (two fp16 1024.0) in a VGPR the compiler cannot fold
+// 0x64006400 (two fp16 1024.0) in a VGPR the compiler cannot fold into the
+// v_and_or_b32 (a DPP identity move: unlike an inline-asm move, the
+// compiler sees its register write, so the MFMA hazard wait states around
+// it are inserted)
 __device__ __forceinline__ uint32_t f16_pair_1024() {
-  uint32_t v;
-  asm("v_mov_b32 %0, 0x64006400" : "=v"(v));
-  return v;
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)0x64006400, 0xE4, 0xF, 0xF, false);
 }
 
 // A operand of QK token tile t, k-step s, from the tile's K fragments

@@ -188,6 +188,27 @@ def test_quantized_decode_ragged(gpu, bits, Tb, Hq, Hkv):
     log(f"[q-decode] bits={bits} Tb={Tb} err={err:.3g}")
 
 
+@pytest.mark.parametrize("bits,Hq,Hkv,qscale", [
+    (4, 32, 8, 1e-4), (4, 32, 8, 300.0), (4, 64, 4, 1e-4), (8, 32, 8, 1e-4), (8, 64, 4, 300.0),
+])
+def test_quantized_decode_query_magnitudes(gpu, bits, Hq, Hkv, qscale):
+    """Queries scaled by 1e-4 (the int4 kernel's query operand, scaled by 1/16
+    at half of the dims, then falls below fp16's normal range) and by 300 (a
+    softmax that one token dominates): selection bit-exact, outputs within
+    1e-2 of the oracle over the same fp16 queries."""
+    Tb = 64
+    lens = [30 * Tb + 5, 12 * Tb, 45 * Tb + 63]
+    log(f"[q-mag] bits={bits} Hq={Hq} Hkv={Hkv} q x {qscale:g}")
+    w = make_workload(3250 + bits + Hq, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype="f16",
+                      top_k=8, ns=1, nr=1, lens=lens, salient_frac=0.01)
+    w.q = (O.to_f32(w.q, "f16").astype(np.float64) * qscale).astype(np.float16).view(np.uint16)
+    cache = new_cache(w, kv_bits=bits)
+    fill(cache, w, gpu)
+    kq, vq = quantize_all(w, bits)
+    err = run_and_check_q(cache, w, gpu, bits, kq, vq)
+    log(f"[q-mag] err={err:.3g}")
+
+
 def test_quantized_many_candidates(gpu):
     """int8, 32-token blocks, GQA 16, 1500+ candidate blocks (radix
     selection path), top-128 + sink + 4 recent."""
