@@ -26,11 +26,15 @@
 // Bound: products of fp16 / bf16 pairs are exact or within one rounding in
 // fp32; the canonical order adds 11 roundings and any fp32 accumulation of
 // 128 products at most 128 more, so |s~ - s| <= 2^-14 * A with
-// A = max over the group of sum |q_d| |k_d| (computed by an MFMA on the
-// magnitudes).  Inputs below fp16's normal range that an MFMA might flush
-// change a dot by at most 2^-14 * (||q||_1 + ||k||_1), which is added.  The
-// bound used per (sequence, kv head) is the maximum over its blocks, widened
-// by 2^-8 of itself to cover the roundings of the comparisons.
+// A = max over the group of sum |q_d| |k_d|.  Inputs below fp16's normal
+// range that an MFMA might flush change a dot by at most
+// 2^-14 * (||q||_1 + ||k||_1), which is added.  A + ||k||_1 is one MFMA on
+// the magnitudes: max over the group of sum (|q_d| + 1) |k_d|, with |q_d| + 1
+// rounded to nearest in the cache's type (>= 1, so within 2^-11 of itself in
+// fp16, 2^-8 in bf16) and the product widened by 2^-10 (fp16) or 2^-7 (bf16)
+// of itself to cover that rounding.  The bound used per (sequence, kv head)
+// is the maximum over its blocks, widened by 2^-8 of itself to cover the
+// roundings of the comparisons.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -50,6 +54,16 @@ __device__ __forceinline__ u32x4 abs16x8(u32x4 v) {
   return u32x4{v[0] & 0x7FFF7FFFu, v[1] & 0x7FFF7FFFu, v[2] & 0x7FFF7FFFu, v[3] & 0x7FFF7FFFu};
 }
 
+// a pair of non-negative fp16 / bf16 values x -> x + 1, rounded to nearest
+template <int DT>
+__device__ __forceinline__ uint32_t abs_plus_one(uint32_t x) {
+  if constexpr (DT == 0) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, x) + f16x2{(_Float16)1.0f, (_Float16)1.0f});
+  } else {
+    return cvt_pk<1>(__uint_as_float(x << 16) + 1.0f, __uint_as_float(x & 0xFFFF0000u) + 1.0f);
+  }
+}
+
 // fmaxf over the whole wave
 __device__ __forceinline__ float wave_max_f32(float x) {
   return __uint_as_float(wave_allreduce_u32(__float_as_uint(x), [](uint32_t a, uint32_t b) {
@@ -64,9 +78,12 @@ __device__ __forceinline__ float wave_max_f32(float x) {
 //   S[head][block] = Q[head][:] . Summ[block][:]   (A = Q, B = summary rows^T)
 // so that lane (block n, group g) holds heads 4g .. 4g+3 of block n and the
 // maximum over the group is taken in-lane and across the four lane groups;
-// plus the same product on magnitudes and 1 . |Summ| for the bound.  Writes
-// the approximate score (max over the group) of every candidate and the
-// chunk's bound to err[seq row][chunk].  grid (chunks, Hkv, n)
+// plus (|Q| + 1) . |Summ|^T for the bound.  Writes the approximate score
+// (max over the group) of every candidate and the chunk's bound to
+// err[seq row][chunk].  The query loads are issued before the rows: loads
+// complete in issue order, so each tile's MFMAs wait only for that tile's
+// rows, and the tiles are computed while the later rows arrive.
+// grid (chunks, Hkv, n)
 // ---------------------------------------------------------------------------
 template <int DT, int G>
 __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
@@ -82,6 +99,14 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
   const int n = lane & 15, g = lane >> 4;
   const int seq = sb.ids[bi];
   const int c0 = geo.ns;
+  u32x4 qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
+  if (n < G) {
+    const uint16_t* src = q + q_row(sb, bi, h * G + n) + 8 * g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = *(const u32x4*)(src + 32 * s);
+  }
   // this wave's kMfmaTiles consecutive 16-block tiles; every summary load is
   // issued before the sequence length is known (rows are clamped into the
   // table; rows past the candidates are read and not used)
@@ -93,17 +118,6 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
     const uint16_t* row = summary_row(geo, seq, h, jr) + 8 * g;
 #pragma unroll
     for (int s = 0; s < 4; ++s) af[t][s] = *(const u32x4*)(row + 32 * s);
-  }
-  u32x4 qf[4], qa[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) qf[s] = qa[s] = u32x4{0u, 0u, 0u, 0u};
-  if (n < G) {
-    const uint16_t* src = q + q_row(sb, bi, h * G + n) + 8 * g;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      qf[s] = *(const u32x4*)(src + 32 * s);
-      qa[s] = abs16x8(qf[s]);
-    }
   }
   const int len = entry_len(geo, sb, bi, seq);
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
@@ -118,6 +132,14 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
   }
   constexpr uint32_t one2 = DT == 0 ? 0x3C003C00u : 0x3F803F80u;
   const u32x4 ones = u32x4{one2, one2, one2, one2};
+  // |q| and |q| + 1 (zero past the group)
+  u32x4 qa[4], qm[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    qa[s] = abs16x8(qf[s]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qm[s][i] = n < G ? abs_plus_one<DT>(qa[s][i]) : 0u;
+  }
   // ||q_head||_1 (|Q| . 1), maximum over the group
   f32x4 q1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -133,13 +155,11 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
   for (int t = 0; t < kMfmaTiles; ++t) {
     const int j0 = jw + 16 * t;
     if (j0 >= c1) break;
-    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f}, a = d, k1 = d;
+    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f}, a = d;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4 ab = abs16x8(af[t][s]);
       d = mfma16x16x32<DT>(qf[s], af[t][s], d);
-      a = mfma16x16x32<DT>(qa[s], ab, a);
-      k1 = mfma16x16x32<DT>(ones, ab, k1);
+      a = mfma16x16x32<DT>(qm[s], abs16x8(af[t][s]), a);
     }
     // lane (block j0 + n, group g), entry i: head 4g + i
     float sc = -INFINITY, am = 0.0f;
@@ -163,7 +183,7 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
         srow[j] = v;
         s_sc[wave * 16 * kMfmaTiles + 16 * t + n] = v;
       }
-      if (!any_bad) emax = fmaxf(emax, am + k1[0]);  // k1[i] = ||summary row||_1 for every i
+      if (!any_bad) emax = fmaxf(emax, am);
     }
   }
   emax = wave_max_f32(emax);
@@ -203,7 +223,8 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
       }
     }
     if (lane == 0) {
-      erow[chunk] = 0x1p-14f * (fmaxf(fmaxf(s_e[0], s_e[1]), fmaxf(s_e[2], s_e[3])) + q1max);
+      constexpr float slack = DT == 0 ? 1.0f + 0x1p-10f : 1.0f + 0x1p-7f;  // |q| + 1 rounded
+      erow[chunk] = 0x1p-14f * (fmaxf(fmaxf(s_e[0], s_e[1]), fmaxf(s_e[2], s_e[3])) * slack + q1max);
       erow[err_stride + chunk] = fl;
     }
   }
