@@ -64,6 +64,14 @@ __device__ __forceinline__ uint32_t abs_plus_one(uint32_t x) {
   }
 }
 
+// fmaxf over each 16-lane row (every lane of the row gets it)
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x121, 0xF, 0xF, false)));  // row_ror:1
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x122, 0xF, 0xF, false)));  // row_ror:2
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x124, 0xF, 0xF, false)));  // row_ror:4
+  return fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xF, 0xF, false)));  // row_ror:8
+}
+
 // fmaxf over the whole wave
 __device__ __forceinline__ float wave_max_f32(float x) {
   return __uint_as_float(wave_allreduce_u32(__float_as_uint(x), [](uint32_t a, uint32_t b) {
@@ -86,16 +94,20 @@ __device__ __forceinline__ float wave_max_f32(float x) {
 // grid (chunks, Hkv, n)
 // ---------------------------------------------------------------------------
 template <int DT, int G>
-__global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_score_mfma(Geometry geo, SeqBatch sb,
                                                     const uint16_t* __restrict__ q,
                                                     float* __restrict__ scores,
                                                     float* __restrict__ err, int err_stride,
                                                     int floor_rank) {
   __shared__ float s_e[4];
-  __shared__ float s_sc[kMfmaChunk];  // the chunk's approximate scores (-inf: no candidate)
-  s_sc[threadIdx.x] = -INFINITY;  // (entries wave*64 .. +63 are written below by the same wave)
+  __shared__ int s_bad[4];
+  __shared__ float s_tm[4 * kMfmaTiles];  // each tile's largest approximate score (-inf: no candidate)
+  __shared__ float s_sc[kMfmaChunk];      // the chunk's approximate scores (-inf: no candidate)
   const int chunk = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // (the entries of wave w are written below by the same wave)
+  s_sc[threadIdx.x] = -INFINITY;
+  if (lane < kMfmaTiles) s_tm[wave * kMfmaTiles + lane] = -INFINITY;
   const int n = lane & 15, g = lane >> 4;
   const int seq = sb.ids[bi];
   const int c0 = geo.ns;
@@ -150,11 +162,13 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
     if (4 * g + i < G) q1h = fmaxf(q1h, q1[i]);
   const float q1max = max_over_groups(q1h);
   float emax = 0.0f;
+  bool wbad = false;
   float* srow = score_row(geo, scores, bi, h);
 #pragma unroll
   for (int t = 0; t < kMfmaTiles; ++t) {
+    // every tile, also past the candidates (masked below): each row load is
+    // then waited for here, and nothing after the loop waits for memory
     const int j0 = jw + 16 * t;
-    if (j0 >= c1) break;
     f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f}, a = d;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -177,37 +191,55 @@ __global__ __launch_bounds__(256) void k_score_mfma(Geometry geo, SeqBatch sb,
     const uint64_t bm = __ballot(bad);
     const bool any_bad = (((bm | (bm >> 16) | (bm >> 32) | (bm >> 48)) >> n) & 1ull) != 0ull;
     const int j = j0 + n;
+    float tv = -INFINITY;
     if (j < c1) {
       const float v = any_bad ? __builtin_nanf("") : sc;
       if (g == 0) {
         srow[j] = v;
         s_sc[wave * 16 * kMfmaTiles + 16 * t + n] = v;
       }
-      if (!any_bad) emax = fmaxf(emax, am);
+      if (!any_bad) {
+        emax = fmaxf(emax, am);
+        tv = sc;
+      }
     }
+    wbad = wbad || __ballot(j < c1 && any_bad) != 0ull;
+    tv = row_max16(tv);
+    if (lane == 0) s_tm[wave * kMfmaTiles + t] = tv;
   }
   emax = wave_max_f32(emax);
-  if (lane == 0) s_e[wave] = emax;
+  if (lane == 0) {
+    s_e[wave] = emax;
+    s_bad[wave] = wbad;
+  }
   __syncthreads();
   if (wave == 0) {
-    // the chunk's floor: its floor_rank-th largest approximate score (with
-    // repeats), -inf if a score is not finite (no certificate), +inf if the
+    // the chunk's floor, a score that floor_rank of its candidates reach:
+    // the floor_rank-th largest of its tile maxima (distinct blocks), or,
+    // when fewer tiles hold candidates, its floor_rank-th largest score (with
+    // repeats).  -inf if a score is not finite (no certificate), +inf if the
     // chunk has fewer candidates
-    float v[4];
-    bool nonfinite = false;
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = s_sc[lane + 64 * i];
-      nonfinite = nonfinite || __builtin_isnan(v[i]) || v[i] == INFINITY;
-      cnt += v[i] != -INFINITY;
-    }
-    const bool any_nonfinite = __ballot(nonfinite) != 0ull;
-    const int total = wave_sum_i32(cnt);
+    const int total = min(max(c1 - (c0 + chunk * kMfmaChunk), 0), kMfmaChunk);
     float fl = INFINITY;
-    if (any_nonfinite) {
+    if (s_bad[0] | s_bad[1] | s_bad[2] | s_bad[3]) {
       fl = -INFINITY;
+    } else if ((total + 15) / 16 >= floor_rank) {
+      // rank of each tile maximum in descending order, ties by tile index;
+      // the ranks of the 16 maxima are 0 .. 15, each once
+      const int me = lane & 15;
+      const float mine = s_tm[me];
+      int rank = 0;
+#pragma unroll
+      for (int i = 0; i < 4 * kMfmaTiles; ++i) {
+        const float o = s_tm[i];
+        rank += (o > mine || (o == mine && i < me)) ? 1 : 0;
+      }
+      const uint64_t at = __ballot(lane < 16 && rank == floor_rank - 1);
+      fl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), (int)__ffsll((unsigned long long)at) - 1));
     } else if (total >= floor_rank) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = s_sc[lane + 64 * i];
       for (int r = 0; r < floor_rank; ++r) {
         float lm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
         const float m = wave_max_f32(lm);

@@ -69,6 +69,25 @@ def test_wide_group_mfma_band(gpu, dtype, Hq, Hkv, Tb, K):
     log(f"[band] err={err:.3g}")
 
 
+@pytest.mark.parametrize("dtype,Hq,Hkv", [("f16", 64, 4), ("bf16", 32, 4)])
+def test_wide_group_partial_last_chunk(gpu, dtype, Hq, Hkv):
+    """The scoring chunks' floors at each kind of last chunk (256 candidates a
+    chunk, 16 per tile; the longest sequence's 4091 candidates make 16 chunks
+    and a floor rank of 128 / 16 = 8): 3880 candidates leave 40 in the last
+    chunk (3 tiles: the floor is that chunk's 8th largest score), 3184 leave
+    112 (7 tiles, likewise), 2673 leave 113 (8 tiles, the last holding one
+    candidate: the 8th largest tile maximum), 4091 leave 251."""
+    Tb = 32
+    lens = [3884 * Tb + 22, 3188 * Tb + 1, 2678 * Tb, 4096 * Tb]
+    log(f"[last chunk] {dtype} G={Hq // Hkv}")
+    w = make_workload(5300 + Hq, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype=dtype,
+                      top_k=128, ns=1, nr=4, lens=lens, salient_frac=0.01)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    err = check(cache, w, gpu)
+    log(f"[last chunk] err={err:.3g}")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_wide_group_ties_and_duplicates(gpu, dtype):
     """Sequence 0: every block has the same keys (all scores tie: the band is
