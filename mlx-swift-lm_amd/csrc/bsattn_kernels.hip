@@ -175,18 +175,22 @@ __device__ __forceinline__ void score_body(const Geometry& geo, const SeqBatch& 
   const int seq = sb.ids[bi];
   const int c = tid & 15;
   const int j0 = geo.ns + chunk * CH + (tid >> 4);
-  // summary rows below the block-table width are always in bounds, so the
-  // loads are issued before the sequence length is known
+  // the query first: loads complete in issue order, so each row's dots
+  // below wait only for that row and run while the later rows arrive
+  u32x4 qr[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qr[g] = *(const u32x4*)(q + q_row(sb, bi, h * G + g) + 8 * c);
+  // every row load is issued before the sequence length is known and
+  // without a branch: rows are clamped into the table (a row past the
+  // candidates is read and not used)
   const uint16_t* sbase = summary_row(geo, seq, h, 0) + 8 * c;
   u32x4 raw[P];
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int j = j0 + 16 * p;
-    raw[p] = (j < geo.mbps) ? *(const u32x4*)(sbase + (size_t)j * kHeadDim) : u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int p = 0; p < P; ++p)
+    raw[p] = *(const u32x4*)(sbase + (size_t)min(j0 + 16 * p, geo.mbps - 1) * kHeadDim);
   float qv[G][8];
 #pragma unroll
-  for (int g = 0; g < G; ++g) unpack8<DT>(*(const u32x4*)(q + q_row(sb, bi, h * G + g) + 8 * c), qv[g]);
+  for (int g = 0; g < G; ++g) unpack8<DT>(qr[g], qv[g]);
   const int len = entry_len(geo, sb, bi, seq);
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int c1 = nb - geo.nr;
