@@ -55,14 +55,18 @@ __device__ __forceinline__ float group_score(const float (&qv)[G][8], const u32x
 }
 
 // Loads the summaries of scoring chunk `ch` (rounds kScoreChunk * ch + i)
-// for lane group lg: rows below `lim` (exclusive) are read, the rest are 0.
+// for lane group lg: rows below `lim` (exclusive); the rest are not scored.
 template <int W>
 __device__ __forceinline__ void load_score_chunk(const uint16_t* __restrict__ srow0, int c0, int lg,
                                                  int ch, int lim, u32x4 (&raw)[kScoreChunk]) {
+  // no branch around a load (a load under one is waited for where the
+  // branch joins): rows from lim on all read row lim - 1 (one cached line
+  // per lane group; never scored)
+  const int last = max(lim - 1, 0);
 #pragma unroll
   for (int i = 0; i < kScoreChunk; ++i) {
     const int j = c0 + lg + 4 * W * (kScoreChunk * ch + i);
-    raw[i] = j < lim ? *(const u32x4*)(srow0 + (size_t)j * kHeadDim) : u32x4{0u, 0u, 0u, 0u};
+    raw[i] = *(const u32x4*)(srow0 + (size_t)min(j, last) * kHeadDim);
   }
 }
 
