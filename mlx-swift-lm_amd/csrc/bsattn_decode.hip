@@ -214,11 +214,10 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
     const int lim = len_first ? c0 + max(nc, 0) : geo.mbps;
     // block-table entries of the selection's keys: slot k of wave w, lane l
     // holds candidate c0 + 64 (W k + w) + l
+    // (unconditional: slots from lim on read entry lim - 1 and are never
+    // selected)
 #pragma unroll
-    for (int k = 0; k < kWgKeys; ++k) {
-      const int j = c0 + 64 * (W * k + wave) + lane;
-      wgc.page[k] = j < lim ? bt[j] : 0;
-    }
+    for (int k = 0; k < kWgKeys; ++k) wgc.page[k] = bt[min(c0 + 64 * (W * k + wave) + lane, max(lim - 1, 0))];
     // slots known from the length alone (sinks, recent, every block when
     // nothing is ranked): their pages are requested now
     {

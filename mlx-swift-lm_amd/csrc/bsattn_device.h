@@ -369,12 +369,14 @@ __device__ __forceinline__ void wave_cand_load(const float* __restrict__ srow,
                                                const int32_t* __restrict__ bt, int c0, int mbps,
                                                WaveCand& wc) {
   const int lane = threadIdx.x & 63;
+  // unconditional loads, every score before any page: loads complete in
+  // issue order, and a load under a branch is waited for where the branch
+  // joins.  Slots past the table read its last row; the selection reads
+  // only slots below nc <= mbps - c0.
 #pragma unroll
-  for (int k = 0; k < kSelKeysPerLane; ++k) {
-    const int j = c0 + lane + 64 * k;
-    wc.score[k] = j < mbps ? srow[j] : 0.0f;
-    wc.page[k] = (bt != nullptr && j < mbps) ? bt[j] : 0;
-  }
+  for (int k = 0; k < kSelKeysPerLane; ++k) wc.score[k] = srow[min(c0 + lane + 64 * k, mbps - 1)];
+#pragma unroll
+  for (int k = 0; k < kSelKeysPerLane; ++k) wc.page[k] = bt != nullptr ? bt[min(c0 + lane + 64 * k, mbps - 1)] : 0;
 }
 
 template <int S>
@@ -451,12 +453,16 @@ __device__ __forceinline__ void wg_cand_load(const float* __restrict__ srow,
                                              const int32_t* __restrict__ bt, int c0, int mbps,
                                              int wave, WgCand& wc) {
   const int lane = threadIdx.x & 63;
+  // unconditional loads, every score before any page: loads complete in
+  // issue order (the selection needs the scores first, the pages only once
+  // it is done), and a load under a branch is waited for where the branch
+  // joins.  Slots past the table read its last row; the selection reads
+  // only slots below nc <= mbps - c0.
 #pragma unroll
-  for (int k = 0; k < kWgKeys; ++k) {
-    const int j = c0 + 64 * (W * k + wave) + lane;
-    wc.score[k] = j < mbps ? srow[j] : 0.0f;
-    wc.page[k] = (bt != nullptr && j < mbps) ? bt[j] : 0;
-  }
+  for (int k = 0; k < kWgKeys; ++k) wc.score[k] = srow[min(c0 + 64 * (W * k + wave) + lane, mbps - 1)];
+#pragma unroll
+  for (int k = 0; k < kWgKeys; ++k)
+    wc.page[k] = bt != nullptr ? bt[min(c0 + 64 * (W * k + wave) + lane, mbps - 1)] : 0;
 }
 
 template <int S, int W>
