@@ -485,6 +485,39 @@ __global__ __launch_bounds__(128) void k_combine(Geometry geo, SeqBatch sb,
   out[q_row(sb, bi, hq) + d] = from_f32<DT>(a * inv);
 }
 
+// The same combine for nsplit <= NS <= 128 with every load issued first:
+// thread t loads (m, l) of split t, then o[d] of every split into registers
+// (split indices clamped to nsplit - 1, so no load sits under a branch).
+// Loads complete in issue order, so the weights (one exp2 per split, shared
+// through LDS) wait only for (m, l) while the o loads arrive; M, the sum and
+// o are reduced in the order of k_combine, with the same result.
+template <int DT, int NS>
+__global__ __launch_bounds__(128) void k_combine_x(Geometry geo, SeqBatch sb,
+                                                   const float* __restrict__ partials,
+                                                   uint16_t* __restrict__ out, int nsplit) {
+  static_assert(NS <= 128, "one split's (m, l) per thread");
+  __shared__ float s_w[NS];
+  __shared__ float s_red[2];
+  const int hq = blockIdx.x, bi = blockIdx.y, d = threadIdx.x;
+  const float* pp = partials + ((size_t)bi * geo.hq + hq) * nsplit * (kHeadDim + 2);
+  const float* pd = pp + min(d, nsplit - 1) * (kHeadDim + 2);
+  const float md = pd[kHeadDim], ld = pd[kHeadDim + 1];
+  float o[NS];
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp) o[sp] = pp[min(sp, nsplit - 1) * (kHeadDim + 2) + d];
+  const bool mine = d < nsplit;
+  const float M = block_reduce_128(mine ? fmaxf(-INFINITY, md) : -INFINITY, true, s_red);
+  const float w = (!mine || md == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(md - M);
+  if (d < NS) s_w[d] = w;
+  const float wl = block_reduce_128(mine ? 0.f + w * ld : 0.f, false, s_red);  // also orders the s_w writes
+  const float inv = wl > 0.f ? 1.f / wl : 0.f;
+  float a = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp)
+    if (sp < nsplit) a += s_w[sp] * o[sp];
+  out[q_row(sb, bi, hq) + d] = from_f32<DT>(a * inv);
+}
+
 // The same combine for nsplit <= NS in one round of loads: every thread
 // (dim d) loads all splits' (m, l, o[d]) at once (the m / l loads of a wave
 // share one address) and reduces them in registers, with no LDS or barriers.
@@ -710,10 +743,15 @@ static void combine_dispatch(const Geometry& g, const SeqBatch& b, const float* 
                              uint16_t* oo, hipStream_t s, Timing* prof) {
   const dim3 grid(g.hq, b.n), blk(128);
   const int kc = kProfCombine;
-  // one round of loads pays up to 16 splits (C2-sized batches: 4.1 against
-  // 4.3 us); with 34 splits it was slower (5.8 against 4.6 us)
+  // one round of loads: up to 16 splits with every split's (m, l) in each
+  // thread (C2-sized batches: 4.1 against 4.3 us for the loop), up to 64
+  // with one exp2 per split shared through LDS (17 splits: 4.0 against 4.3
+  // us, 34: 4.1 against 4.6 us); the loop beyond
   if (nsplit <= 8) launch(k_combine_r<DT, 8>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
   else if (nsplit <= 16) launch(k_combine_r<DT, 16>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
+  else if (nsplit <= 32) launch(k_combine_x<DT, 32>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
+  else if (nsplit <= 48) launch(k_combine_x<DT, 48>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
+  else if (nsplit <= 64) launch(k_combine_x<DT, 64>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
   else launch(k_combine<DT>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
 }
 
