@@ -84,6 +84,24 @@ def test_ragged_paged(gpu, dtype, Tb, Hq, Hkv):
     run_and_check(cache, w, gpu)
 
 
+@pytest.mark.parametrize("K,dtype", [(26, "f16"), (58, "bf16"), (110, "f16"), (170, "bf16"), (230, "f16"),
+                                     (300, "bf16")])
+def test_split_combine_variants(gpu, K, dtype):
+    """top_k + sink + newest = 4 x splits: 7, 15, 28, 43, 58 and 76 splits, one
+    per combine variant (up to 8 and 16 splits with every (m, l) in each
+    thread, up to 32, 48 and 64 with the weights shared through LDS, the loop
+    beyond); ragged lengths leave the last split of the shorter sequence
+    partly empty."""
+    Tb = 32
+    lens = [Tb * 700 - 5, Tb * (K + 40)]
+    log(f"[combine] K={K} splits={(K + 2 + 3) // 4} {dtype}")
+    w = make_workload(3050 + K, B=2, Hq=32, Hkv=8, T=max(lens), Tb=Tb, dtype=dtype, top_k=K, lens=lens)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    err = run_and_check(cache, w, gpu)
+    log(f"[combine] K={K} err={err:.3g}")
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_topk_covering_all_blocks_is_dense(gpu, dtype):
     """top_k >= number of blocks -> every block is attended and the result is
