@@ -76,6 +76,21 @@ __device__ __forceinline__ void append_body(const Geometry& geo, int seq, int bi
   const int tg = threadIdx.x >> 4, c = threadIdx.x & 15;
   const int tok = blockIdx.x * 16 + tg;
   const int32_t* bt = block_table(geo, seq);
+  // the workgroup's token 0 (the only one) fills its block: uniform.  Then
+  // the keys of the block's other tokens (written by earlier launches) are
+  // requested first, all at once and without a branch (token indices
+  // clamped; blocks of 32 or 64 tokens: at most four keys per thread), so
+  // that they arrive with the token's own
+  const int blk0 = base / geo.tb;
+  const bool fills = fuse_summary && base - blk0 * geo.tb == geo.tb - 1;
+  u32x4 pre[4];
+  if (fills) {
+    const int page = page_given >= 0 ? page_given : bt[blk0];
+    const uint16_t* Kt =
+        (const uint16_t*)(geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes + geo.k_off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pre[i] = *(const u32x4*)(Kt + k_elem(min(tg + 16 * i, geo.tb - 2), 8 * c));
+  }
   u32x4 kr = u32x4{0u, 0u, 0u, 0u};
   if (tok < L) {
     const int pos = base + tok;
@@ -95,15 +110,12 @@ __device__ __forceinline__ void append_body(const Geometry& geo, int seq, int bi
       Vt[v_elem(geo.tb, slot, 8 * c + e)] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xFFFFu));
     }
   }
-  if (!fuse_summary) return;
-  // the workgroup's token 0 (the only one) fills its block: uniform branch
-  const int blk = base / geo.tb;
-  if (base - blk * geo.tb != geo.tb - 1) return;
-  const int page = page_given >= 0 ? page_given : bt[blk];
-  const uint16_t* Kt =
-      (const uint16_t*)(geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes + geo.k_off);
-  // keys 0 .. Tb-2 were written by earlier launches; key Tb-1 is kr of tg 0
-  for (int t = tg; t < geo.tb - 1; t += 16) s_blk[t][c] = *(const u32x4*)(Kt + k_elem(t, 8 * c));
+  if (!fills) return;
+  const int blk = blk0;
+  // keys 0 .. Tb-2 (loaded above); key Tb-1 is kr of tg 0
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (tg + 16 * i < geo.tb - 1) s_blk[tg + 16 * i][c] = pre[i];
   if (tg == 0) s_blk[geo.tb - 1][c] = kr;
   __syncthreads();
   if (tg != 0) return;
