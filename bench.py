@@ -135,6 +135,17 @@ def torch_dtype(torch, cfg):
     return torch.bfloat16 if cfg.dtype == "bf16" else torch.float16
 
 
+def calibration_copy(torch, dev):
+    """One plain 256 MiB device copy, for scaling the hardware byte counters."""
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log("[bench] calibration copy: 256 MiB read + 256 MiB written")
+    del src, dst
+
+
 def make_layer(cfg: Config, layer, dev, torch, bsattn):
     g = torch.Generator(device=dev)
     seeds = {"c2": 1001, "c3": 1003, "c5": 1005}
@@ -392,6 +403,8 @@ def bench_layers(args, cfg: Config):
         torch.cuda.synchronize()
         log(f"[bench] counters run done: {args.steps} decode steps and {args.steps} given-index "
             f"attention passes over {L} layers")
+        if args.copy_calibration:
+            calibration_copy(torch, dev)
         return
 
     # graph of one step (all layers)
@@ -419,13 +432,7 @@ def bench_layers(args, cfg: Config):
         f"us/layer-step")
 
     if args.copy_calibration:
-        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log("[bench] calibration copy: 256 MiB read + 256 MiB written")
-        del src, dst
+        calibration_copy(torch, dev)
 
     # kernel times of one decode layer-step (eager, profiled)
     for cache, _ in layers:
