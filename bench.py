@@ -713,7 +713,7 @@ def bench_loop(args):
 
 def bench_prefill(args, bits=0):
     """Dense causal prefill attention of a 512-token chunk at the end of a
-    32768-token context (C2 geometry: B=8, Hq=32, Hkv=8, Tb=64; bf16 caches,
+    32768-token context (B=8, Hq=32, Hkv=8, Tb=64; bf16 caches,
     or with bits = 4 MLX-affine int4 caches, group 64, fp16), over 4 layer
     caches (beyond the 256 MB Infinity Cache).  MFMA-bound: algorithmic
     FLOPs = 4 * D * sum over queries of the tokens they see."""
@@ -772,7 +772,7 @@ def bench_prefill(args, bits=0):
 
 
 def bench_multi(args, cfg: Config, L: int = 4):
-    """Speculative verify at the C2 geometry: decodeMulti of L query tokens per
+    """Speculative verify at B=8, Hq=32, Hkv=8, 32k tokens, Tb=64, bf16: decodeMulti of L query tokens per
     sequence (each selects its own blocks over its own prefix), over the
     config's distinct layer caches, as a replayed HIP graph; against L
     single-token decodes of the same layer caches."""

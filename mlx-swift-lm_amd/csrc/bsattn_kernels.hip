@@ -756,9 +756,9 @@ static void combine_dispatch(const Geometry& g, const SeqBatch& b, const float* 
   const dim3 grid(g.hq, b.n), blk(128);
   const int kc = kProfCombine;
   // one round of loads: up to 16 splits with every split's (m, l) in each
-  // thread (C2-sized batches: 4.1 against 4.3 us for the loop), up to 64
-  // with one exp2 per split shared through LDS (17 splits: 4.0 against 4.3
-  // us, 34: 4.1 against 4.6 us); the loop beyond
+  // thread (8 sequences x 32 heads, 9 splits: 4.1 against 4.3 us for the
+  // loop), up to 64 with one exp2 per split shared through LDS (17 splits:
+  // 4.0 against 4.3 us, 34: 4.1 against 4.6 us); the loop beyond
   if (nsplit <= 8) launch(k_combine_r<DT, 8>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
   else if (nsplit <= 16) launch(k_combine_r<DT, 16>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
   else if (nsplit <= 32) launch(k_combine_x<DT, 32>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
