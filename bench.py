@@ -772,10 +772,10 @@ def bench_prefill(args, bits=0):
 
 
 def bench_multi(args, cfg: Config, L: int = 4):
-    """Speculative verify at B=8, Hq=32, Hkv=8, 32k tokens, Tb=64, bf16: decodeMulti of L query tokens per
-    sequence (each selects its own blocks over its own prefix), over the
-    config's distinct layer caches, as a replayed HIP graph; against L
-    single-token decodes of the same layer caches."""
+    """Speculative verify at B=8, Hq=32, Hkv=8, 32k tokens, Tb=64, bf16:
+    decodeMulti of L query tokens per sequence (each selects its own blocks
+    over its own prefix), over the workload's distinct layer caches, as a
+    replayed HIP graph; against L single-token decodes of the same caches."""
     import torch
     import bsattn
     dev = torch.device("cuda", 0)
