@@ -27,13 +27,44 @@ CASES = {
 
 @pytest.mark.parametrize("case", list(CASES))
 def test_append_decode_equals_append_then_decode(gpu, case):
-    import torch
-    dtype, Tb, Hq, Hkv, K, ns, nr, bits, lens0, steps, ids = CASES[case]
     log(f"[append-decode] {case}")
+    run_case(gpu, case, 4100, *CASES[case])
+
+
+def random_case(seed: int):
+    r = np.random.default_rng(4300 + seed)
+    bits = int(r.choice([0, 0, 4, 8]))
+    dtype = "f16" if bits else str(r.choice(["f16", "bf16"]))
+    Tb = int(r.choice([32, 64]))
+    G = int(r.choice([1, 2, 4, 8, 16]))
+    Hkv = int(r.choice([1, 2, 4]))
+    B = int(r.integers(1, 5))
+    # starting lengths near block boundaries, inside blocks and tiny
+    lens0 = [int(r.choice([Tb - 1, Tb, 3 * Tb - 2, int(r.integers(1, 40 * Tb))])) for _ in range(B)]
+    ids = None
+    if B > 1 and seed % 3 == 0:
+        ids = [int(x) for x in r.permutation(B)[: int(r.integers(1, B + 1))]]
+    return (dtype, Tb, Hkv * G, Hkv, int(r.choice([1, 2, 3, 5, 9])), int(r.integers(0, 3)),
+            int(r.choice([1, 2, 4])), bits, lens0, int(r.integers(10, 2 * Tb + 10)), ids)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_append_decode_random(gpu, seed):
+    """Seeded random shapes through the same checks: cache type (fp16, bf16,
+    int4, int8), block size, GQA group, batch, starting lengths at and around
+    block boundaries, top_k, sinks, recent blocks, steps (up to two block
+    fills), and a reordered subset of the sequences."""
+    c = random_case(seed)
+    log(f"[append-decode random {seed}] {c}")
+    run_case(gpu, f"random {seed}", 4400 + seed, *c)
+
+
+def run_case(gpu, case, wseed, dtype, Tb, Hq, Hkv, K, ns, nr, bits, lens0, steps, ids):
+    import torch
     B = len(lens0)
     ids_l = list(range(B)) if ids is None else ids
     total = [l + (steps if b in ids_l else 0) for b, l in enumerate(lens0)]
-    w = make_workload(4100, B=B, Hq=Hq, Hkv=Hkv, T=max(total), Tb=Tb, dtype=dtype, top_k=K,
+    w = make_workload(wseed, B=B, Hq=Hq, Hkv=Hkv, T=max(total), Tb=Tb, dtype=dtype, top_k=K,
                       ns=ns, nr=nr, lens=total)
     a = new_cache(w, kv_bits=bits)
     w0 = Workload(w.seed, B, Hq, Hkv, w.D, Tb, dtype, lens0, K, ns, nr)
