@@ -83,6 +83,27 @@ def test_multi_decode_equals_sequential_decodes(gpu, dtype, Hq, Hkv, Tb, K, L, k
                     assert err <= TOL, f"seq {b} query {i} head {h}: error {err:.3g}"
 
 
+def _random_multi(seed: int):
+    r = np.random.default_rng(6500 + seed)
+    kv_bits = int(r.choice([0, 0, 4, 8]))
+    dtype = "f16" if kv_bits else str(r.choice(["f16", "bf16"]))
+    Tb = int(r.choice([32, 64]))
+    G = int(r.choice([1, 2, 4, 8, 16]))
+    Hkv = int(r.choice([1, 2, 4]))
+    L = int(r.integers(2, 13))
+    lens = [int(r.integers(L + 1, int(r.choice([40, 900])) * Tb)) for _ in range(int(r.integers(1, 4)))]
+    return dtype, Hkv * G, Hkv, Tb, int(r.choice([2, 5, 16, 33, 70])), L, kv_bits, lens
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_multi_decode_random(gpu, seed):
+    """Seeded random shapes through the same checks: cache type, block size,
+    GQA group, top_k, 2 - 12 query tokens, ragged lengths up to 900 blocks."""
+    c = _random_multi(seed)
+    log(f"[multi random {seed}] {c}")
+    test_multi_decode_equals_sequential_decodes(gpu, *c)
+
+
 def test_attention_with_cache_update_verify_pass(gpu):
     """attentionWithCacheUpdate with L > 1 and the causal mask appends the
     L tokens and runs the multi-token decode; other masks are refused."""
