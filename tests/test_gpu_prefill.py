@@ -235,3 +235,35 @@ def test_prefill_timed_shape(gpu, bits):
     worst = max(errs)
     log(f"[prefill-timed] max error {worst:.3g}")
     assert worst <= (TOL if bits == 0 else 1e-2), f"max error {worst:.3g}"
+
+
+def _random_prefill(seed: int):
+    r = np.random.default_rng(7900 + seed)
+    bits = int(r.choice([0, 0, 4, 8]))
+    dtype = "f16" if bits else str(r.choice(["f16", "bf16"]))
+    G = int(r.choice([1, 2, 4, 8, 16]))
+    Hkv = int(r.choice([1, 2, 4])) if G >= 8 else int(r.choice([1, 2, 4, 8]))
+    Tb = int(r.choice([32, 64]))
+    L = int(r.integers(17, 401))
+    # a whole prompt from an empty cache (16-bit caches) or a chunk after earlier tokens
+    lens = [L + int(r.choice([0 if bits == 0 else 1, int(r.integers(1, 3000))]))
+            for _ in range(int(r.integers(1, 4)))]
+    return bits, dtype, Hkv * G, Hkv, Tb, lens, L
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_prefill_random(gpu, seed):
+    """Seeded random shapes: cache type (fp16, bf16, int4, int8), GQA group,
+    block size, 17 - 400 query tokens, ragged lengths (some the whole prompt
+    from an empty cache); the first, second, middle and last two queries of
+    every head against the oracle's attention over the query's prefix."""
+    bits, dtype, Hq, Hkv, Tb, lens, L = _random_prefill(seed)
+    log(f"[prefill random {seed}] bits={bits} {dtype} Hq={Hq} Hkv={Hkv} Tb={Tb} lens={lens} L={L}")
+    if bits:
+        test_prefill_quantized_cache(gpu, bits, Hq, Hkv, Tb, lens, L)
+        return
+    w = make_workload(7950 + seed, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype=dtype,
+                      top_k=4, lens=lens, salient_frac=0.01)
+    got, qm, _ = _run(w, gpu, L)
+    err = _check(w, got, qm, L, sorted({0, 1, L // 2, L - 2, L - 1}))
+    log(f"[prefill random {seed}] err={err:.3g}")
