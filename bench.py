@@ -24,8 +24,8 @@ Other workloads (one JSON line each, not the headline):
                (seeded counter stream), pages taken from a seeded
                permutation of the free list (shuffled physical order), 256 steps of
                (append one token per sequence, score + top-32 + attend) as
-               one appendDecode call each (append + scoring in one launch;
-               the two-call figure is reported beside it); eager, since
+               one appendDecode call each (one launch: the append inside the
+               fused decode; the two-call figure is reported beside it); eager, since
                every append changes host-side page tables;
   --config pf  dense causal prefill attention of a 512-token chunk at the end
                of 32768 tokens (B=8, Hq=32, Hkv=8, bf16), MFMA-bound;
@@ -617,8 +617,8 @@ def bench_loop(args):
     vn = torch.randn(steps + args.warmup, B, HKV, 1, D, device=dev, generator=g).half()
     qs = torch.randn(steps + args.warmup, B, HQ, 1, D, device=dev, generator=g).half()
     scale = 1.0 / math.sqrt(D)
-    # a step = attentionWithCacheUpdate's decode step: appendDecode (append +
-    # score in one launch, then select + attend + combine)
+    # a step = attentionWithCacheUpdate's decode step: appendDecode (here one
+    # launch of the fused decode, which also appends the token)
     for i in range(args.warmup):
         cache.appendDecode(kn[i], vn[i], qs[i], scale)
     torch.cuda.synchronize()
@@ -699,7 +699,7 @@ def bench_loop(args):
                    "lengths": [int(x) for x in lens], "block_size": TB, "top_k": K,
                    "sink_blocks": 1, "recent_blocks": 1, "pages": pages, "page_order": "shuffled",
                    "timing": "eager wall clock per step (ctypes launches included)",
-                   "step_call": "appendDecode (append + scoring in one launch)"},
+                   "step_call": "appendDecode (one launch: append, patches and summary fold inside the fused decode)"},
         "two_calls_us_per_step": round(us_two, 3),
         "kernels_us_per_step": kern, "kernel_us_per_step_total": round(total, 3),
         "graph_us_per_step": round(us_graph, 3),

@@ -173,8 +173,9 @@ int bsattn_decode_noalloc(bsattn_cache* cache, const void* q, const int32_t* seq
  * token per listed sequence (k, v [n_seqs, Hkv, 1, D]) and decodes q
  * [n_seqs, Hq, 1, D] over the caches that now hold it -> out; idx_out as
  * in bsattn_decode.  Same results, bit for bit, as bsattn_append followed
- * by bsattn_decode; on a 16-bit cache the append and the block scoring
- * share one launch. */
+ * by bsattn_decode; on a 16-bit cache whose batch takes the fused decode
+ * the whole step is one launch (the append inside the decode kernel),
+ * otherwise the append and the block scoring share one launch. */
 int bsattn_append_decode(bsattn_cache* cache, const void* k, const void* v,
                          const void* q, const int32_t* seq_ids, int32_t n_seqs,
                          float scale, void* out, int32_t* idx_out, void* stream);

@@ -340,8 +340,9 @@ class BlockSparseKVCache:
         """One decode step (attentionWithCacheUpdate with L = 1): appends
         keys / values [B, Hkv, 1, D] and decodes queries [B, Hq, 1, D] over
         the caches that now hold them; the same results as append() then
-        decode(), with the append and the block scoring in one launch where
-        the cache allows it."""
+        decode(), in one launch (the append inside the fused decode) or with
+        the append and the block scoring in one launch where the cache allows
+        it."""
         self._check_kv(keys, "keys")
         self._check_kv(values, "values")
         if keys.shape != values.shape or keys.shape[2] != 1:

@@ -24,14 +24,29 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "bsattn_device.h"
 
 namespace bsattn {
 
 // k_decode modes: score + select + attend (fused), attend over given
-// indices (given)
-constexpr int kModeFused = 0, kModeGiven = 1;
+// indices (given), append each entry's new token, then score + select +
+// attend (fused append)
+constexpr int kModeFused = 0, kModeGiven = 1, kModeFusedAppend = 2;
+
+// the fused append's extra arguments: the page of each entry's newest block,
+// metadata words to patch for the launches that follow, and the new tokens'
+// keys and values ([n][Hkv][128])
+struct AppendArgs {
+  StepPages sp;
+  PatchBatch pb;
+  const uint16_t* k;
+  const uint16_t* v;
+};
+struct NoAppend {};
+template <int MODE>
+using ModeArgs = std::conditional_t<MODE == kModeFusedAppend, AppendArgs, NoAppend>;
 
 // candidate blocks of a pair the fused kernel scores and selects from
 constexpr int kFusedMaxCand = 2048;
@@ -124,8 +139,8 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
                                                    int32_t* __restrict__ idx, float sl2,
                                                    uint16_t* __restrict__ out,
                                                    float* __restrict__ partials, int S, int R,
-                                                   int len_first) {
-  constexpr bool GIVEN = MODE == kModeGiven;
+                                                   int len_first, ModeArgs<MODE> ap) {
+  constexpr bool GIVEN = MODE == kModeGiven, APPEND = MODE == kModeFusedAppend;
   constexpr int NT = TB / 16;   // QK token tiles
   constexpr int EPL = TB / 4;   // scores per lane
   constexpr int KS2 = TB / 32;  // PV k-steps
@@ -135,6 +150,7 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
   __shared__ float s_m[W][16], s_l[W][16];
   __shared__ float s_o[W][G][kHeadDim];
   __shared__ int s_jr[W][kMaxRounds], s_pr[W][kMaxRounds];
+  __shared__ u32x4 s_blk[APPEND ? TB : 1][16];  // keys of a block the append fills
 
   // (pair, split); the S splits of a pair share workgroup index mod 8 (XCD)
   const int L = blockIdx.x, xcd = L & 7, r8 = L >> 3;
@@ -150,8 +166,16 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
   const uint16_t* srow0 = summary_row(geo, seq, h, 0) + 8 * c;
   const int c0 = geo.ns;
 
-  // --- loads that need nothing else: q in both layouts, the first
-  // summaries (unless the length comes first), the length
+  // --- loads that need nothing else: the new token (append), q in both
+  // layouts, the first summaries (unless the length comes first), the length
+  [[maybe_unused]] u32x4 tk, tv;
+  if constexpr (APPEND) {
+    // dims 8c .. 8c+7 of the token's key and value, in every lane (no
+    // branch, so that no wait lands on the loads that follow)
+    const size_t src = ((size_t)bi * geo.hkv + h) * kHeadDim + 8 * c;
+    tk = *(const u32x4*)(ap.k + src);
+    tv = *(const u32x4*)(ap.v + src);
+  }
   u32x4 qf[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
@@ -160,10 +184,41 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = *(const u32x4*)(src + 32 * s);
   }
+  // append, further loads whose results wait until after the scoring: when
+  // the token completes its block, split 0 folds the block's summary, whose
+  // other keys (written by earlier launches) are requested now; workgroup 0
+  // requests the metadata words it patches for the launches that follow
+  // (nothing in this launch reads a patched word: lengths come from sb, the
+  // newest block's page from ap.sp, and the scored candidates end before the
+  // newest block, since recent >= 1)
+  constexpr int NP = APPEND ? ((TB - 1) * 16 + 64 * W - 1) / (64 * W) : 1;
+  [[maybe_unused]] u32x4 pre[NP];
+  [[maybe_unused]] int pidx = 0, pval = 0;
+  [[maybe_unused]] bool fills = false;
+  if constexpr (APPEND) {
+    fills = split == 0 && sb.len[bi] % TB == 0;
+    if (fills) {
+      const uint16_t* Kt = (const uint16_t*)(geo.pool + ((size_t)ap.sp.page[bi] * geo.hkv + h) * geo.slab_bytes +
+                                             geo.k_off);
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        const int e = min((int)threadIdx.x + 64 * W * i, (TB - 1) * 16 - 1);
+        pre[i] = *(const u32x4*)(Kt + k_elem(e >> 4, 8 * (e & 15)));
+      }
+    }
+    if (L == 0) {
+      const int t = min((int)threadIdx.x, kMaxPatch - 1);
+      pidx = ap.pb.idx[t];
+      pval = ap.pb.val[t];
+    }
+  }
   // block and page of each of this wave's rounds (-1: nothing), kept in the
   // wave's own row of s_jr / s_pr (written and read by this wave only, in
   // program order)
   int len;
+  // append: newest block, and whether this wave gathers it
+  [[maybe_unused]] int jn = -1;
+  [[maybe_unused]] bool owner = false;
   if constexpr (GIVEN) {
     // indices from idx; the block-table entry is requested before the
     // length check (every j in [0, mbps) has one; others read entry 0 and
@@ -212,6 +267,33 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
     const bool ranked = nc > K;           // sinks, the K picked, recent
     const bool select = ranked && K > 0;  // (top_k 0: sinks and recent only)
     const int lim = len_first ? c0 + max(nc, 0) : geo.mbps;
+    // append: the token goes to the newest block jn, on page ap.sp.page[bi]
+    // (its block-table entry may be patched by this launch).  The block's
+    // slot is the last one (sinks, picked, recent; or every block in order);
+    // lanes 0..15 of the wave that gathers it store the token, and that wave
+    // waits for the store before its gather of the block
+    jn = APPEND ? (len - 1) / TB : -1;
+    if constexpr (APPEND) {
+      const int slot_n = ranked ? geo.ns + K + geo.nr - 1 : nb - 1;
+      owner = split == slot_n % S && wave == (slot_n / S) % W;
+    }
+    // (called where every load above has arrived): the token's store, the
+    // patches, and the keys of a completed block into LDS (the new key from
+    // the registers of lanes 0..15)
+    auto append_stage = [&]() {
+      if constexpr (APPEND) {
+        if (owner && lane < 16) put_token<true>(geo, ap.sp.page[bi], h, len - 1 - jn * TB, c, tk, tv);
+        if (L == 0 && (int)threadIdx.x < ap.pb.n) geo.meta[pidx] = pval;
+        if (fills) {
+#pragma unroll
+          for (int i = 0; i < NP; ++i) {
+            const int e = threadIdx.x + 64 * W * i;
+            if (e < (TB - 1) * 16) s_blk[e >> 4][e & 15] = pre[i];
+          }
+          if (threadIdx.x < 16) s_blk[TB - 1][threadIdx.x] = tk;
+        }
+      }
+    };
     // block-table entries of the selection's keys: slot k of wave w, lane l
     // holds candidate c0 + 64 (W k + w) + l
     // (unconditional: slots from lim on read entry lim - 1 and are never
@@ -227,7 +309,8 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
         const int slot = (rr * W + wave) * S + split;
         const bool picked = ranked && slot >= geo.ns && slot < geo.ns + K;
         jr[rr] = rr < R && !picked ? selected_block(slot, nb, ranked, geo.ns, geo.nr, K, nullptr) : -1;
-        pr[rr] = jr[rr] >= 0 ? uniform(bt[jr[rr]]) : -1;
+        if constexpr (APPEND) pr[rr] = jr[rr] == jn ? ap.sp.page[bi] : jr[rr] >= 0 ? uniform(bt[jr[rr]]) : -1;
+        else pr[rr] = jr[rr] >= 0 ? uniform(bt[jr[rr]]) : -1;
       }
       if (lane == 0) {
 #pragma unroll
@@ -252,6 +335,7 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
           if (ch + 3 < nch) load_score_chunk<W>(srow0, c0, lg, ch + 3, lim, rawB);
         }
       }
+      append_stage();
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < kWgKeys; ++k) {
@@ -276,6 +360,7 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
       for (int p = lane; p < geo.nsel_max; p += 64)
         row[p] = selected_block(p, nb, ranked, geo.ns, geo.nr, K, s_sel);
     }
+    if (!select) append_stage();
   }
 
   // --- gather + attention: this wave's slots, online softmax over rounds;
@@ -288,6 +373,10 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
   for (int rr = 0; rr < R; ++rr) {
     const int j = uniform(s_jr[wave][rr]), page = uniform(s_pr[wave][rr]);
     if (j < 0) continue;
+    // the newest block of an append: this wave stored its token; the store is
+    // complete before the block is read
+    if constexpr (APPEND)
+      if (j == jn) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const int valid = min(TB, len - j * TB);
     const uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
     const u32x4* Kf = (const u32x4*)(slab + geo.k_off) + lane;
@@ -389,6 +478,12 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
   }
   __syncthreads();
   attend_merge<DT, G, W>(geo, sb, bi, h, split, S, s_m, s_l, s_o, out, partials);
+  if constexpr (APPEND) {
+    // the completed block's summary: 16 lanes fold its keys from LDS (written
+    // before the barriers of the merge) in token order
+    if (fills && threadIdx.x < 16)
+      *(u32x4*)(summary_row(geo, seq, h, jn) + 8 * threadIdx.x) = fold_block<DT>(s_blk, TB, threadIdx.x);
+  }
 }
 
 // ===========================================================================
@@ -419,34 +514,34 @@ FusedPlan fused_plan(const Geometry& g, int n) {
 
 template <int DT, int TB, int G, int MD>
 void decode_w(const Geometry& g, const FusedPlan& p, dim3 grid, const SeqBatch& b, const uint16_t* q,
-              int32_t* idx, float sl2, uint16_t* out, float* part, int lf, hipStream_t s,
-              Timing* prof) {
+              int32_t* idx, float sl2, uint16_t* out, float* part, int lf, const ModeArgs<MD>& ap,
+              hipStream_t s, Timing* prof) {
   const int kd = kProfAttend;
   switch (p.W) {
-    case 4: launch(k_decode<DT, TB, G, 4, MD>, grid, dim3(256), 0, s, prof, kd, g, b, q, idx, sl2, out, part, p.S, p.R, lf); break;
-    case 8: launch(k_decode<DT, TB, G, 8, MD>, grid, dim3(512), 0, s, prof, kd, g, b, q, idx, sl2, out, part, p.S, p.R, lf); break;
+    case 4: launch(k_decode<DT, TB, G, 4, MD>, grid, dim3(256), 0, s, prof, kd, g, b, q, idx, sl2, out, part, p.S, p.R, lf, ap); break;
+    case 8: launch(k_decode<DT, TB, G, 8, MD>, grid, dim3(512), 0, s, prof, kd, g, b, q, idx, sl2, out, part, p.S, p.R, lf, ap); break;
     default:  // fused_plan gives W = 12 for 32-token blocks only
       if constexpr (TB == 32)
-        launch(k_decode<DT, TB, G, 12, MD>, grid, dim3(768), 0, s, prof, kd, g, b, q, idx, sl2, out, part, p.S, p.R, lf);
+        launch(k_decode<DT, TB, G, 12, MD>, grid, dim3(768), 0, s, prof, kd, g, b, q, idx, sl2, out, part, p.S, p.R, lf, ap);
       break;
   }
 }
 
 template <int DT, int TB, int MD>
 void decode_g(const Geometry& g, const FusedPlan& p, dim3 grid, const SeqBatch& b, const uint16_t* q,
-              int32_t* idx, float sl2, uint16_t* out, float* part, int lf, hipStream_t s,
-              Timing* prof) {
+              int32_t* idx, float sl2, uint16_t* out, float* part, int lf, const ModeArgs<MD>& ap,
+              hipStream_t s, Timing* prof) {
   switch (g.group) {
-    case 1: decode_w<DT, TB, 1, MD>(g, p, grid, b, q, idx, sl2, out, part, lf, s, prof); break;
-    case 2: decode_w<DT, TB, 2, MD>(g, p, grid, b, q, idx, sl2, out, part, lf, s, prof); break;
-    default: decode_w<DT, TB, 4, MD>(g, p, grid, b, q, idx, sl2, out, part, lf, s, prof); break;
+    case 1: decode_w<DT, TB, 1, MD>(g, p, grid, b, q, idx, sl2, out, part, lf, ap, s, prof); break;
+    case 2: decode_w<DT, TB, 2, MD>(g, p, grid, b, q, idx, sl2, out, part, lf, ap, s, prof); break;
+    default: decode_w<DT, TB, 4, MD>(g, p, grid, b, q, idx, sl2, out, part, lf, ap, s, prof); break;
   }
 }
 
 template <int MD>
 hipError_t decode_impl(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
-                       bool len_first, float scale, void* out, float* partials, hipStream_t s,
-                       Timing* prof) {
+                       bool len_first, float scale, void* out, float* partials,
+                       const ModeArgs<MD>& ap, hipStream_t s, Timing* prof) {
   const FusedPlan p = fused_plan(g, b.n);
   const int pairs = b.n * g.hkv;
   const dim3 grid(8 * ((pairs + 7) / 8) * p.S);
@@ -455,11 +550,11 @@ hipError_t decode_impl(const Geometry& g, const SeqBatch& b, const void* q, int3
   uint16_t* oo = (uint16_t*)out;
   const int lf = len_first ? 1 : 0;
   if (g.dtype == 0) {
-    if (g.tb == 64) decode_g<0, 64, MD>(g, p, grid, b, qq, idx, sl2, oo, partials, lf, s, prof);
-    else decode_g<0, 32, MD>(g, p, grid, b, qq, idx, sl2, oo, partials, lf, s, prof);
+    if (g.tb == 64) decode_g<0, 64, MD>(g, p, grid, b, qq, idx, sl2, oo, partials, lf, ap, s, prof);
+    else decode_g<0, 32, MD>(g, p, grid, b, qq, idx, sl2, oo, partials, lf, ap, s, prof);
   } else {
-    if (g.tb == 64) decode_g<1, 64, MD>(g, p, grid, b, qq, idx, sl2, oo, partials, lf, s, prof);
-    else decode_g<1, 32, MD>(g, p, grid, b, qq, idx, sl2, oo, partials, lf, s, prof);
+    if (g.tb == 64) decode_g<1, 64, MD>(g, p, grid, b, qq, idx, sl2, oo, partials, lf, ap, s, prof);
+    else decode_g<1, 32, MD>(g, p, grid, b, qq, idx, sl2, oo, partials, lf, ap, s, prof);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.S == 1) return e;
@@ -485,12 +580,21 @@ bool fused_decode_ok(const Geometry& g, int n, int max_nc) {
 hipError_t launch_fused_decode(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx_out,
                                bool len_first, float scale, void* out, float* partials,
                                hipStream_t s, Timing* prof) {
-  return decode_impl<kModeFused>(g, b, q, idx_out, len_first, scale, out, partials, s, prof);
+  return decode_impl<kModeFused>(g, b, q, idx_out, len_first, scale, out, partials, NoAppend{}, s, prof);
+}
+
+hipError_t launch_fused_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
+                                      const PatchBatch& pb, const void* k, const void* v, const void* q,
+                                      int32_t* idx_out, float scale, void* out, float* partials,
+                                      hipStream_t s, Timing* prof) {
+  const AppendArgs ap{sp, pb, (const uint16_t*)k, (const uint16_t*)v};
+  return decode_impl<kModeFusedAppend>(g, b, q, idx_out, true, scale, out, partials, ap, s, prof);
 }
 
 hipError_t launch_fused_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
                                float scale, void* out, float* partials, hipStream_t s, Timing* prof) {
-  return decode_impl<kModeGiven>(g, b, q, const_cast<int32_t*>(idx), false, scale, out, partials, s, prof);
+  return decode_impl<kModeGiven>(g, b, q, const_cast<int32_t*>(idx), false, scale, out, partials, NoAppend{},
+                                 s, prof);
 }
 
 }  // namespace bsattn

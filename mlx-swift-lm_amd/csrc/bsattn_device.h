@@ -128,6 +128,56 @@ __device__ __forceinline__ void unpack8(const u32x4 raw, float* out) {
     out[e] = to_f32<DT>((uint16_t)((e & 1) ? (raw[e >> 1] >> 16) : (raw[e >> 1] & 0xFFFFu)));
 }
 
+// dims 8c .. 8c+7 of one token's key kr and value vr into slot `slot` of the
+// (page, kv head h) slab: 16 contiguous bytes of the K tile, eight scattered
+// elements of the V tile.  THROUGH: device-scope stores, which write through
+// the XCD's L2 at once (for a kernel that writes the token early and runs on:
+// the partial lines are then not left to the write-back at its end)
+template <bool THROUGH = false>
+__device__ __forceinline__ void put_token(const Geometry& g, int page, int h, int slot, int c,
+                                          const u32x4 kr, const u32x4 vr) {
+  uint8_t* slab = g.pool + ((size_t)page * g.hkv + h) * g.slab_bytes;
+  uint16_t* Kt = (uint16_t*)(slab + g.k_off);
+  uint16_t* Vt = (uint16_t*)(slab + g.v_off);
+  if constexpr (THROUGH) {
+    uint64_t* kd = (uint64_t*)(Kt + k_elem(slot, 8 * c));
+    __hip_atomic_store(kd, (uint64_t)kr[0] | ((uint64_t)kr[1] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(kd + 1, (uint64_t)kr[2] | ((uint64_t)kr[3] << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *(u32x4*)(Kt + k_elem(slot, 8 * c)) = kr;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t w = vr[e >> 1];
+    const uint16_t x = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xFFFFu));
+    uint16_t* vd = Vt + v_elem(g.tb, slot, 8 * c + e);
+    if constexpr (THROUGH) __hip_atomic_store(vd, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *vd = x;
+  }
+}
+
+// dims 8c .. 8c+7 of a full block's summary: the mean of its tb keys (held in
+// LDS as blk[token][c]), summed in token order, each add and the final scale
+// rounded once in fp32 (the order summary16 follows)
+template <int DT>
+__device__ __forceinline__ u32x4 fold_block(const u32x4 (*blk)[16], int tb, int c) {
+  float acc[8];
+  unpack8<DT>(blk[0][c], acc);
+  for (int t = 1; t < tb; ++t) {
+    float x[8];
+    unpack8<DT>(blk[t][c], x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = __fadd_rn(acc[e], x[e]);
+  }
+  const float inv = 1.0f / (float)tb;
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack2<DT>(__fmul_rn(acc[2 * e], inv), __fmul_rn(acc[2 * e + 1], inv));
+  return o;
+}
+
 // Candidates are ranked only when they outnumber top_k.
 __host__ __device__ inline bool ranked_select(const Geometry& g, int nc) {
   return nc > g.top_k && g.top_k > 0;

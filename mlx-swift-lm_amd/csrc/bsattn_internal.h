@@ -150,11 +150,12 @@ hipError_t launch_decode_attend(const Geometry& g, const SeqBatch& b, const void
                                 int32_t* idx_out, int max_nc, float scale, void* out,
                                 float* partials, hipStream_t s, Timing* prof);
 // one decode step of a 16-bit cache with one new token per entry (b.len =
-// the lengths after it): the patches pb and the appends (k / v [n, Hkv, 1, D]
-// into the pages sp) in one launch, then the fused decode kernel (fused:
-// requires fused_decode_ok), or with the scoring in the append launch and
-// then the selection + attention (+ combine) launches of launch_decode
-// (requires max_nc <= fused_select_limit(top_k)).  Every cache has recent
+// the lengths after it): fused (requires fused_decode_ok): one launch of the
+// fused decode kernel that also applies the patches pb and the appends (k / v
+// [n, Hkv, 1, D] into the pages sp), plus the combine when it splits;
+// otherwise the patches, the appends and the scoring in one launch, then the
+// selection + attention (+ combine) launches of launch_decode (requires
+// max_nc <= fused_select_limit(top_k)).  Every cache has recent
 // >= 1, so the block an append completes is forced, never scored.
 hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
                                 const PatchBatch& pb, const void* k, const void* v, const void* q,
@@ -182,6 +183,14 @@ hipError_t launch_fused_decode(const Geometry& g, const SeqBatch& b, const void*
 // decode == select + attend bit for bit)
 hipError_t launch_fused_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
                                float scale, void* out, float* partials, hipStream_t s, Timing* prof);
+// one launch per decode step: each entry's new token (k, v: [n][Hkv][128]) is
+// stored at position b.len[i] - 1 on page sp.page[i] before the fused decode
+// gathers it, the block it fills gets its summary, and the metadata patches
+// pb are applied for the launches that follow (requires recent >= 1)
+hipError_t launch_fused_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
+                                      const PatchBatch& pb, const void* k, const void* v, const void* q,
+                                      int32_t* idx_out, float scale, void* out, float* partials,
+                                      hipStream_t s, Timing* prof);
 // dense causal attention of the last L tokens of each sequence
 hipError_t launch_prefill(const Geometry& g, const SeqBatch& b, int L, const void* q, float scale,
                           void* out, hipStream_t s, Timing* prof);

@@ -99,16 +99,7 @@ __device__ __forceinline__ void append_body(const Geometry& geo, int seq, int bi
     const size_t src = (((size_t)bi * geo.hkv + h) * L + tok) * kHeadDim + 8 * c;
     kr = *(const u32x4*)(k + src);
     const u32x4 vr = *(const u32x4*)(v + src);
-    uint8_t* slab = geo.pool + ((size_t)page * geo.hkv + h) * geo.slab_bytes;
-    // dims 8c .. 8c+7 of a key are 16 contiguous bytes of the K tile
-    uint16_t* Kt = (uint16_t*)(slab + geo.k_off);
-    *(u32x4*)(Kt + k_elem(slot, 8 * c)) = kr;
-    uint16_t* Vt = (uint16_t*)(slab + geo.v_off);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t w = vr[e >> 1];
-      Vt[v_elem(geo.tb, slot, 8 * c + e)] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xFFFFu));
-    }
+    put_token(geo, page, h, slot, c, kr, vr);
   }
   if (!fills) return;
   const int blk = blk0;
@@ -119,20 +110,7 @@ __device__ __forceinline__ void append_body(const Geometry& geo, int seq, int bi
   if (tg == 0) s_blk[geo.tb - 1][c] = kr;
   __syncthreads();
   if (tg != 0) return;
-  float acc[8];
-  unpack8<DT>(s_blk[0][c], acc);
-  for (int t = 1; t < geo.tb; ++t) {
-    float x[8];
-    unpack8<DT>(s_blk[t][c], x);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = __fadd_rn(acc[e], x[e]);
-  }
-  const float inv = 1.0f / (float)geo.tb;
-  u32x4 o;
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    o[e] = pack2<DT>(__fmul_rn(acc[2 * e], inv), __fmul_rn(acc[2 * e + 1], inv));
-  *(u32x4*)(summary_row(geo, seq, h, blk) + 8 * c) = o;
+  *(u32x4*)(summary_row(geo, seq, h, blk) + 8 * c) = fold_block<DT>(s_blk, geo.tb, c);
 }
 
 template <int DT>
@@ -809,11 +787,13 @@ hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const Step
                                 const PatchBatch& pb, const void* k, const void* v, const void* q,
                                 float* scores, int32_t* idx_out, int max_nc, bool fused, float scale,
                                 void* out, float* partials, hipStream_t s, Timing* prof) {
-  // the scoring chunk size follows launch_score; the fused decode scores
-  // itself, so its append launch has no scoring workgroups
+  // the fused decode appends, scores and attends in one launch
+  if (fused)
+    return launch_fused_append_decode(g, b, sp, pb, k, v, q, idx_out, scale, out, partials, s, prof);
+  // the scoring chunk size follows launch_score
   const bool small = (int64_t)((max_nc + 63) / 64) * g.hkv * b.n <= 1024;
   const int ch = small ? 32 : 64;
-  const int chunks = !fused && ranked_select(g, max_nc) ? (max_nc + ch - 1) / ch : 0;
+  const int chunks = ranked_select(g, max_nc) ? (max_nc + ch - 1) / ch : 0;
   const uint16_t *kk = (const uint16_t*)k, *vv = (const uint16_t*)v, *qq = (const uint16_t*)q;
   if (g.dtype == 0) {
     if (small) append_score_dispatch<0, 32>(g, b, sp, pb, chunks, kk, vv, qq, scores, s, prof);
@@ -824,7 +804,6 @@ hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const Step
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (fused) return launch_fused_decode(g, b, q, idx_out, true, scale, out, partials, s, prof);
   return launch_decode_attend(g, b, q, scores, idx_out, max_nc, scale, out, partials, s, prof);
 }
 
