@@ -3,8 +3,9 @@ call) against bsattn_append followed by bsattn_decode on a deep copy of the
 same cache: outputs and selected blocks bit-identical at every step, across
 block fills (the summary is written in the launch that also scores), new
 pages, ragged lengths with interleaved pages, a reordered subset of the
-sequences, GQA 4 / 8 / 16, and the affine int4 cache (which takes the two
-calls); after the last step also against the oracle."""
+sequences, GQA 4 / 8 / 16, the one-launch step over several splits per
+(sequence, kv head), and the affine int4 cache (which takes the two calls);
+after the last step also against the oracle."""
 from __future__ import annotations
 
 import numpy as np
@@ -22,6 +23,11 @@ CASES = {
     "f16-tb32-g8-subset": ("f16", 32, 32, 4, 3, 1, 2, 0, [31, 95, 200], 40, [2, 0]),
     "f16-tb32-g16-recent4": ("f16", 32, 64, 4, 3, 1, 4, 0, [40, 300, 129], 40, None),
     "int4": ("f16", 64, 32, 8, 2, 1, 1, 4, [100, 130], 30, None),
+    # one launch over 3 splits per (sequence, kv head): the newest block's
+    # slot (the last one) lies in split 2 while ranked and in split 1 while
+    # every block is taken, and the blocks the tokens fill are folded in split 0
+    "f16-tb32-splits-fill": ("f16", 32, 4, 2, 9, 1, 2, 0, [447, 60], 40, None),
+    "bf16-tb64-splits-fill": ("bf16", 64, 8, 2, 9, 1, 2, 0, [830, 120], 80, None),
 }
 
 
