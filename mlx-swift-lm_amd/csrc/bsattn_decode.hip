@@ -277,9 +277,10 @@ __global__ __launch_bounds__(64 * W) void k_decode(Geometry geo, SeqBatch sb,
       const int slot_n = ranked ? geo.ns + K + geo.nr - 1 : nb - 1;
       owner = split == slot_n % S && wave == (slot_n / S) % W;
     }
-    // (called where every load above has arrived): the token's store, the
-    // patches, and the keys of a completed block into LDS (the new key from
-    // the registers of lanes 0..15)
+    // the token's store, the patches, and the keys of a completed block into
+    // LDS (the new key from the registers of lanes 0..15); called after the
+    // scoring, whose waits have covered those loads, or, when nothing is
+    // scored, at the end of this branch (where it waits for them)
     auto append_stage = [&]() {
       if constexpr (APPEND) {
         if (owner && lane < 16) put_token<true>(geo, ap.sp.page[bi], h, len - 1 - jn * TB, c, tk, tv);
