@@ -28,6 +28,8 @@ CASES = {
     # every block is taken, and the blocks the tokens fill are folded in split 0
     "f16-tb32-splits-fill": ("f16", 32, 4, 2, 9, 1, 2, 0, [447, 60], 40, None),
     "bf16-tb64-splits-fill": ("bf16", 64, 8, 2, 9, 1, 2, 0, [830, 120], 80, None),
+    # top_k 0 (sinks and recent only) over 2 splits, with block fills
+    "f16-tb32-topk0": ("f16", 32, 8, 2, 0, 2, 3, 0, [300, 62], 40, None),
 }
 
 
