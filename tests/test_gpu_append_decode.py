@@ -67,6 +67,30 @@ def test_append_decode_random(gpu, seed):
     run_case(gpu, f"random {seed}", 4400 + seed, *c)
 
 
+def random_fused_case(seed: int):
+    """16-bit caches with GQA groups of at most 4, where the step is one launch
+    of the fused decode: batches of 1-6 sequences (one split per (sequence, kv
+    head) at the larger ones, several at the smaller, where the newest
+    block's slot can lie in any split), lengths at and around block
+    boundaries."""
+    r = np.random.default_rng(4700 + seed)
+    Tb = int(r.choice([32, 64]))
+    G = int(r.choice([1, 2, 4]))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    B = int(r.integers(1, 7))
+    lens0 = [int(r.choice([Tb - 1, 2 * Tb - 3, int(r.integers(1, 9 * Tb)), int(r.integers(8 * Tb, 30 * Tb))]))
+             for _ in range(B)]
+    return (str(r.choice(["f16", "bf16"])), Tb, Hkv * G, Hkv, int(r.choice([0, 1, 4, 9, 20])),
+            int(r.integers(0, 3)), int(r.choice([1, 2, 3])), 0, lens0, int(r.integers(Tb, 2 * Tb + 5)), None)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_append_decode_random_fused(gpu, seed):
+    c = random_fused_case(seed)
+    log(f"[append-decode fused random {seed}] {c}")
+    run_case(gpu, f"fused random {seed}", 4800 + seed, *c)
+
+
 def run_case(gpu, case, wseed, dtype, Tb, Hq, Hkv, K, ns, nr, bits, lens0, steps, ids):
     import torch
     B = len(lens0)
