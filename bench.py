@@ -13,7 +13,14 @@ per layer-step.  Steps are replayed from a HIP graph (captured once) so the
 timing is the GPU's, not the Python launcher's; the eager (ctypes per call)
 figure is reported alongside.
 
-Other workloads (one JSON line each, not the headline):
+The default run (no --config) also measures configs c3, c5 and c4 below,
+without their CPU legs, and reports them under "other_configs" in the same
+JSON line (µs per layer-step, or per step for c4, the attention kernel's µs,
+achieved GB/s, fraction of peak and traffic source); --no-others skips them.
+The headline's cpu_baseline leg also checks layer 0's GPU output against the
+oracle's (output_vs_gpu: raw and net-of-rounding max-abs error).
+
+Other workloads (one JSON line each with --config, not the headline):
   --config c3  int4 affine KV (group 64, fp16 scale / bias): B=4, Hq=32,
                Hkv=8, 131072 tokens, 64-token blocks, top-64 + sink + recent;
   --config c5  int8 affine KV, wide GQA: B=8, Hq=64, Hkv=4 (G=16), 262144
@@ -121,6 +128,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
+    ap.add_argument("--no-others", action="store_true",
+                    help="default run: skip the other decode workloads (c3, c5, c4) after the headline")
     ap.add_argument("--counters", action="store_true",
                     help="short run for hardware-counter profiling (rocprofv3 --pmc): build the "
                          "layer caches, run --steps eager decode steps and --steps given-index "
@@ -368,7 +377,10 @@ def copy_bandwidth(torch, dev, mib: int = 1024, reps: int = 10) -> dict:
                     f"event time), median of {reps}"}
 
 
-def bench_layers(args, cfg: Config):
+def bench_layers(args, cfg: Config, light: bool = False):
+    """One workload's layer-step benchmark -> the result dict.  light: no
+    CPU legs, recall or copy reference (the other configurations of the
+    default run)."""
     import torch
     import bsattn
     dev = torch.device("cuda", 0)
@@ -492,25 +504,26 @@ def bench_layers(args, cfg: Config):
         f"given-index attend {given_us:.2f} us ({100 * given_achieved / HBM_PEAK_GBPS:.1f}%)")
 
     recall = None
-    if cfg.key == "c5" and not args.no_recall:
+    if cfg.key == "c5" and not args.no_recall and not light:
         t0 = time.time()
         recall = recall_report(cfg, layers[0][0], layers[0][1], idx[0], seqs=[0, 1])
         log(f"[bench] recall ({time.time() - t0:.0f}s): {recall}")
 
     cpu = None
     cpu_dense_path = None
-    if not args.no_cpu and args.cpu_seconds > 0:
-        cpu_us, n, thr, cidx, _ = cpu_baseline(cfg, layers[0][0], layers[0][1], args.cpu_seconds)
+    if not args.no_cpu and args.cpu_seconds > 0 and not light:
+        cpu_us, n, thr, cidx, cout = cpu_baseline(cfg, layers[0][0], layers[0][1], args.cpu_seconds)
         same = bool((cidx == idx[0].cpu().numpy()).all())
+        out_check = output_check(cfg, layers[0][0].decode(layers[0][1], scale), cout)
         cpu = {"value": round(cpu_us, 1), "unit": "us/layer-step", "cores": thr, "kind": "port",
                "cpu_model": cpu_model(),
                "sample": f"layer 0 of the same workload ({cfg.B} seq x {cfg.HKV} kv heads x {cfg.T} "
                          f"tokens): the C oracle's score + select + attend of every (seq, kv head) "
                          f"given the block summaries, pairs over {thr} OpenMP threads, median of "
                          f"{n} layer-steps",
-               "selection_matches_gpu": same}
+               "selection_matches_gpu": same, "output_vs_gpu": out_check}
         log(f"[bench] cpu oracle: {cpu_us:.0f} us/layer-step ({thr} threads, {cpu_model()}); "
-            f"selection equal to the GPU's: {same}")
+            f"selection equal to the GPU's: {same}; output {out_check}")
         dense_us, nd, thr = cpu_dense(cfg, layers[0][0], layers[0][1], args.cpu_seconds)
         cpu_dense_path = {"value": round(dense_us, 1), "unit": "us/layer-step", "cores": thr,
                           "kind": "reference path (dense)",
@@ -519,8 +532,9 @@ def bench_layers(args, cfg: Config):
                                     f"median of {nd} repetitions, x{cfg.B} sequences"}
         log(f"[bench] cpu dense (reference path): {dense_us:.0f} us/layer-step, {thr} threads")
 
-    copy_bw = copy_bandwidth(torch, dev)
-    log(f"[bench] same-run copy bandwidth: {copy_bw['value']} GB/s")
+    copy_bw = None if light else copy_bandwidth(torch, dev)
+    if copy_bw:
+        log(f"[bench] same-run copy bandwidth: {copy_bw['value']} GB/s")
     traffic, traffic_src = recorded_traffic(cfg)
     kv = cfg.dtype if cfg.bits == 0 else f"int{cfg.bits} affine, group 64, fp16 scale/bias"
     result = {
@@ -557,7 +571,7 @@ def bench_layers(args, cfg: Config):
                                      "combine_us": round(given_combine_us, 3)}},
         "decode_kernels_us": decode_kernels,
         "copy_bandwidth": copy_bw,
-        "attend_frac_of_copy": round(achieved / copy_bw["value"], 4),
+        "attend_frac_of_copy": round(achieved / copy_bw["value"], 4) if copy_bw else None,
         "layer_step_GBps": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "eager_us_per_layer_step": round(eager_ms * 1e3 / L, 3),
         "us_per_layer_step_distribution": dist,
@@ -566,7 +580,48 @@ def bench_layers(args, cfg: Config):
     }
     if recall is not None:
         result["recall"] = recall
-    print(json.dumps(result), flush=True)
+    del layers, idx
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return result
+
+
+def output_check(cfg: Config, gpu_out, ref):
+    """GPU output of a layer against the oracle's fp64 output on the same
+    inputs: raw max-abs error, and the error net of the final rounding to
+    the output dtype (|gpu - ref| - ulp(ref) / 2), against the bar (2e-3 for
+    16-bit caches, 1e-2 for affine ones)."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    dt = cfg.dtype
+    got = O.to_f32(host16(gpu_out, torch, np).reshape(ref.shape), dt).astype(np.float64)
+    mant = 10 if dt == "f16" else 7
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -14))) - mant)
+    raw = float(np.max(np.abs(got - ref)))
+    net = float(np.max(np.abs(got - ref) - 0.5 * ulp))
+    bar = 2e-3 if cfg.bits == 0 else 1e-2
+    return {"max_abs": raw, "max_abs_net_of_output_rounding": net, "bar": bar, "within_bar": net <= bar,
+            "out_max_abs": float(np.max(np.abs(ref))), "what": "layer 0's GPU decode output against the "
+            "oracle's fp64 output (the cpu_baseline leg's last repetition)"}
+
+
+def other_summary(r: dict, per: str) -> dict:
+    """The figures of a non-headline workload's result kept in the headline line."""
+    keep = {"metric": r["metric"], per: r["value"], "config": r["config"]}
+    if "roofline" in r:
+        ro = r["roofline"]
+        keep.update({"attend_kernel": ro["kernel"], "attend_us": ro["launch_us"],
+                     "attend_bytes_per_launch": ro["bytes_per_launch"], "attend_achieved_GBps": ro["achieved"],
+                     "attend_frac": ro["frac"], "traffic": ro["traffic"], "traffic_source": ro["traffic_source"],
+                     "given_index": ro["given_index"], "decode_kernels_us": r["decode_kernels_us"],
+                     "layer_step_GBps": r["layer_step_GBps"]})
+    else:
+        keep.update({k: r[k] for k in ("kernels_us_per_step", "kernel_us_per_step_total",
+                                       "kernel_GBps", "kernel_frac", "bytes_per_step",
+                                       "traffic_note") if k in r})
+    return keep
 
 
 def _hash3(seed: int, stream: int, index: int) -> int:
@@ -579,8 +634,10 @@ def _hash3(seed: int, stream: int, index: int) -> int:
     return mix((mix((mix(seed) + stream) & 0xFFFFFFFFFFFFFFFF) + index) & 0xFFFFFFFFFFFFFFFF)
 
 
-def bench_loop(args):
-    """Config 4: decode loop with appends, eager (page tables change every step)."""
+def bench_loop(args, light: bool = False):
+    """Config 4: decode loop with appends, eager (page tables change every
+    step) -> the result dict.  light: only the one-call loop and its kernel
+    times (no two-call or graph legs, no copy reference)."""
     import numpy as np
     import torch
     import bsattn
@@ -627,15 +684,17 @@ def bench_loop(args):
         cache.appendDecode(kn[i], vn[i], qs[i], scale)
     torch.cuda.synchronize()
     us_step = (time.perf_counter() - t0) * 1e6 / steps
-    # the same steps as two calls (append, then decode)
-    cache.trim(steps, list(range(B)))
-    t0 = time.perf_counter()
-    for i in range(args.warmup, args.warmup + steps):
-        cache.append(kn[i], vn[i])
-        cache.decode(qs[i], scale)
-    torch.cuda.synchronize()
-    us_two = (time.perf_counter() - t0) * 1e6 / steps
-    log(f"[bench] c4: {us_step:.2f} us/step (appendDecode), {us_two:.2f} (append + decode)")
+    us_two = None
+    if not light:
+        # the same steps as two calls (append, then decode)
+        cache.trim(steps, list(range(B)))
+        t0 = time.perf_counter()
+        for i in range(args.warmup, args.warmup + steps):
+            cache.append(kn[i], vn[i])
+            cache.decode(qs[i], scale)
+        torch.cuda.synchronize()
+        us_two = (time.perf_counter() - t0) * 1e6 / steps
+    log(f"[bench] c4: {us_step:.2f} us/step (appendDecode), {us_two} (append + decode)")
     # kernel time per step: the same steps again (trimmed back first), profiled
     cache.trim(steps, list(range(B)))
     cache.profile(True)
@@ -654,6 +713,39 @@ def bench_loop(args):
             total += ms * 1e3 / steps
     cache.profile(False)
     log(f"[bench] c4: {us_step:.2f} us/step eager, kernels {total:.2f} us/step")
+    nsel = K + 2
+    gather = int(B * HKV * nsel * TB * 2 * D * 2)
+    # scoring reads every full block's summary of every (sequence, kv head)
+    summ = int(sum(HKV * ((int(n) + steps // 2) // TB) * D * 2 for n in lens))
+    per_step = gather + summ + B * HQ * D * 2 * 2
+    k_gbps = per_step / (total * 1e-6) / 1e9 if total else None
+    result = {
+        "metric": "block-sparse decode loop with appends µs/step, B=32 variable lengths",
+        "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic: torch RNG on device, K/V/q ~ N(0,1); lengths from splitmix64 "
+                "(seed 1004, stream 4); physical page order shuffled from seed 1004 (stream 5)",
+        "config": {"workload": "decode loop: append 1 token per sequence, score + top-K + attend",
+                   "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
+                   "lengths": [int(x) for x in lens], "block_size": TB, "top_k": K,
+                   "sink_blocks": 1, "recent_blocks": 1, "pages": pages, "page_order": "shuffled",
+                   "timing": "eager wall clock per step (ctypes launches included)",
+                   "step_call": "appendDecode (one launch: append, patches and summary fold inside the fused decode)"},
+        "kernels_us_per_step": kern, "kernel_us_per_step_total": round(total, 3),
+        "gather_bytes_per_step": gather,
+        "bytes_per_step": per_step,
+        "kernel_GBps": round(k_gbps, 1) if k_gbps else None,
+        "kernel_frac": round(k_gbps / HBM_PEAK_GBPS, 4) if k_gbps else None,
+        "traffic_note": "bytes_per_step = selected K/V + every full block's summary + q + out; one "
+                        "layer cache (4.8 GB of K/V) is re-read every step, so the 37.7 MB of "
+                        "summaries can stay in the 256 MB Infinity Cache",
+    }
+    if light:
+        del cache, kn, vn, qs
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        return result
     # the same steps as a HIP graph: reserve pages, capture one [appendStep,
     # decode] step, replay it per step with that step's inputs copied in
     cache.trim(steps, list(range(B)))
@@ -685,30 +777,14 @@ def bench_loop(args):
             "reps": steps, "what": "GPU time of one replayed step (input copies excluded)"}
     cache.sync()
     log(f"[bench] c4: {us_graph:.2f} us/step as a replayed HIP graph (inputs copied in per step)")
-    nsel = K + 2
-    gather = int(B * HKV * nsel * TB * 2 * D * 2)
-    result = {
-        "metric": "block-sparse decode loop with appends µs/step, B=32 variable lengths",
-        "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": steps,
-        "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 5), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16",
-        "data": "synthetic: torch RNG on device, K/V/q ~ N(0,1); lengths from splitmix64 "
-                "(seed 1004, stream 4); physical page order shuffled from seed 1004 (stream 5)",
-        "config": {"workload": "decode loop: append 1 token per sequence, score + top-K + attend",
-                   "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
-                   "lengths": [int(x) for x in lens], "block_size": TB, "top_k": K,
-                   "sink_blocks": 1, "recent_blocks": 1, "pages": pages, "page_order": "shuffled",
-                   "timing": "eager wall clock per step (ctypes launches included)",
-                   "step_call": "appendDecode (one launch: append, patches and summary fold inside the fused decode)"},
+    result.update({
         "two_calls_us_per_step": round(us_two, 3),
-        "kernels_us_per_step": kern, "kernel_us_per_step_total": round(total, 3),
         "graph_us_per_step": round(us_graph, 3),
         "graph_step_us_distribution": dist,
         "copy_bandwidth": copy_bandwidth(torch, dev),
-        "gather_bytes_per_step": gather,
         "gather_GBps_at_kernel_time": round(gather / (total * 1e-6) / 1e9, 1) if total else None,
-    }
-    print(json.dumps(result), flush=True)
+    })
+    return result
 
 
 def bench_prefill(args, bits=0):
@@ -838,15 +914,32 @@ def main():
                                    "--gpus 1"}))
         sys.exit(2)
     if args.config == "c4":
-        bench_loop(args)
+        print(json.dumps(bench_loop(args)), flush=True)
     elif args.config == "pf":
         bench_prefill(args)
     elif args.config == "pfq":
         bench_prefill(args, bits=4)
     elif args.config == "mq":
         bench_multi(args, CONFIGS["c2"])
+    elif args.config == "c2" and not args.no_others and not args.counters:
+        # the headline, then the other decode workloads (no CPU legs), all
+        # in the one JSON line
+        result = bench_layers(args, CONFIGS["c2"])
+        others = {}
+        for key in ("c3", "c5"):
+            t0 = time.time()
+            others[key] = other_summary(bench_layers(args, CONFIGS[key], light=True), "us_per_layer_step")
+            log(f"[bench] other config {key}: {others[key]['us_per_layer_step']} us/layer-step "
+                f"({time.time() - t0:.0f}s)")
+        t0 = time.time()
+        others["c4"] = other_summary(bench_loop(args, light=True), "us_per_step")
+        log(f"[bench] other config c4: {others['c4']['us_per_step']} us/step ({time.time() - t0:.0f}s)")
+        result["other_configs"] = others
+        print(json.dumps(result), flush=True)
     else:
-        bench_layers(args, CONFIGS[args.config])
+        r = bench_layers(args, CONFIGS[args.config])
+        if r is not None:
+            print(json.dumps(r), flush=True)
 
 
 if __name__ == "__main__":

@@ -162,7 +162,11 @@ int bsattn_decode(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
  * sequences per call; a call whose workspaces exceed the scratch fails with
  * BSATTN_ERR_RANGE.  Calls on one GPU that may overlap (other streams, other
  * threads, other caches) race on the scratch: serialize them.  Profiling is
- * not recorded. */
+ * not recorded.  Like bsattn_decode it sizes its launches from the held
+ * pages and reads the device-side lengths, so it may follow
+ * bsattn_append_step without bsattn_sync (e.g. a captured
+ * [bsattn_append_step, bsattn_decode_noalloc] step; make one call before
+ * capture so that the scratch's address is looked up outside it). */
 int bsattn_decode_noalloc(bsattn_cache* cache, const void* q, const int32_t* seq_ids,
                           int32_t n_seqs, float scale, void* out, int32_t* idx_out,
                           void* stream);

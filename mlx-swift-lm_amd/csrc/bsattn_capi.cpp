@@ -781,9 +781,12 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
 int bsattn_decode_noalloc(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_t n_seqs,
                           float scale, void* out, int32_t* idx_out, void* stream) try {
   // no device or host allocation on the way: the entries live on the stack,
-  // the workspaces in the device's fixed scratch, profiling is not recorded
+  // the workspaces in the device's fixed scratch, profiling is not recorded.
+  // Like bsattn_decode, the launches are sized from each sequence's held
+  // pages and the kernels read the device-side lengths, so the call follows
+  // bsattn_append_step without a bsattn_sync (a captured [append_step,
+  // decode_noalloc] loop).
   if (!c || !q || !out) return fail(BSATTN_ERR_INVALID, "null argument");
-  if (int rs = check_synced(c)) return rs;
   if (n_seqs < 1 || n_seqs > kMaxBatch || n_seqs > c->d.max_seqs)
     return fail(BSATTN_ERR_RANGE, "n_seqs %d out of range [1, %d] for the no-allocation decode", n_seqs,
                 std::min(kMaxBatch, c->d.max_seqs));

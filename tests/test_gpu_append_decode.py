@@ -91,8 +91,48 @@ def test_append_decode_random_fused(gpu, seed):
     run_case(gpu, f"fused random {seed}", 4800 + seed, *c)
 
 
-def run_case(gpu, case, wseed, dtype, Tb, Hq, Hkv, K, ns, nr, bits, lens0, steps, ids):
+def one_launch_lengths(seed: int, n_ranked: int, n_short: int, m_ranked, m_short):
+    """Starting lengths 64 m - d (d in [1, 60]): every sequence completes a
+    block within the first 60 appended tokens; n_ranked with m in m_ranked
+    (more candidates than top_k: the newest block takes the last slot), the
+    rest in m_short (every block taken in order: the newest block's slot is
+    nb - 1)."""
+    r = np.random.default_rng(seed)
+    ms = [int(r.integers(*m_ranked)) for _ in range(n_ranked)] + \
+         [int(r.integers(*m_short)) for _ in range(n_short)]
+    r.shuffle(ms)
+    return [64 * m - int(r.integers(1, 61)) for m in ms]
+
+
+# Shapes where bsattn_append_decode is one launch of the fused decode with
+# several gather rounds per wave, the newest block past round 0:
+#  - 32 sequences x 8 kv heads (256 pairs, as the decode loop of 32
+#    sequences): one split, 8 waves, 5 rounds; ranked sequences put the newest
+#    block in slot 33 = round 4 of wave 1, the short ones in slot nb - 1;
+#  - 8 sequences x 8 kv heads, top_k 64 (66 slots): 4 splits, 8 waves, 3
+#    rounds; the newest block's slot 65 is round 2 of wave 0 in split 1.
+ONE_LAUNCH = {
+    "b32-hkv8-k32-r5": ("f16", 64, 32, 8, 32, 1, 1, 0, one_launch_lengths(51, 24, 8, (36, 52), (4, 33)), 70, None),
+    "b32-hkv8-k32-r5-bf16": ("bf16", 64, 32, 8, 32, 1, 1, 0, one_launch_lengths(52, 28, 4, (36, 45), (2, 30)), 66, None),
+    "b8-hkv8-k64-s4-r3": ("f16", 64, 32, 8, 64, 1, 1, 0, one_launch_lengths(53, 6, 2, (68, 250), (10, 66)), 70, None),
+}
+
+
+@pytest.mark.parametrize("case", list(ONE_LAUNCH))
+def test_append_decode_one_launch_rounds(gpu, case):
+    """The one-launch step where the newest block is gathered in a round
+    past the first (the decode loop of 32 sequences runs it so): bit-identical
+    to append + decode at every step, one fused decode launch per step (plus
+    the split combine with several splits; no append, scoring or selection
+    launch), pages in a shuffled physical order, then selection, output and
+    summaries against the oracle."""
+    log(f"[append-decode one launch] {case}")
+    run_case(gpu, case, 4900 + len(case), *ONE_LAUNCH[case], one_launch=True)
+
+
+def run_case(gpu, case, wseed, dtype, Tb, Hq, Hkv, K, ns, nr, bits, lens0, steps, ids, one_launch=False):
     import torch
+    from bsattn import _lib
     B = len(lens0)
     ids_l = list(range(B)) if ids is None else ids
     total = [l + (steps if b in ids_l else 0) for b, l in enumerate(lens0)]
@@ -102,8 +142,14 @@ def run_case(gpu, case, wseed, dtype, Tb, Hq, Hkv, K, ns, nr, bits, lens0, steps
     w0 = Workload(w.seed, B, Hq, Hkv, w.D, Tb, dtype, lens0, K, ns, nr)
     w0.keys = [w.keys[b][:, :lens0[b]] for b in range(B)]
     w0.values = [w.values[b][:, :lens0[b]] for b in range(B)]
-    fill(a, w0, gpu, chunk=40)
+    if one_launch:
+        a.shuffleFreePages(wseed)
+        fill(a, w0, gpu)
+    else:
+        fill(a, w0, gpu, chunk=40)
     b_ = a.copy()
+    if one_launch:
+        a.profile(True)
     q = to_dev(w.q[ids_l][:, :, None, :], dtype, gpu)
     nsel = ns + nr + K
     cur = list(lens0)
@@ -121,6 +167,17 @@ def run_case(gpu, case, wseed, dtype, Tb, Hq, Hkv, K, ns, nr, bits, lens0, steps
         torch.cuda.synchronize()
         assert np.array_equal(ia.cpu().numpy(), ib.cpu().numpy()), f"step {s}: selected blocks differ"
         assert np.array_equal(from_dev(out_a), from_dev(out_b)), f"step {s}: outputs differ"
+    if one_launch:
+        # one fused decode launch per step (followed by the split combine
+        # when a (sequence, kv head) has several splits), and no append,
+        # scoring, summary or selection launch
+        n_att = a.profileRead(_lib.KERNEL_ATTEND)[1]
+        n_comb = a.profileRead(_lib.KERNEL_COMBINE)[1]
+        others = {k: a.profileRead(getattr(_lib, k))[1] for k in
+                  ("KERNEL_APPEND", "KERNEL_SCORE", "KERNEL_SUMMARY", "KERNEL_TOPK")}
+        a.profile(False)
+        assert n_att == steps and n_comb in (0, steps) and not any(others.values()), \
+            f"not one decode launch per step: attend {n_att}, combine {n_comb}, others {others}"
     for b in range(B):
         assert a.seqLen(b) == b_.seqLen(b) == cur[b]
     if bits == 0:

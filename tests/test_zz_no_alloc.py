@@ -73,3 +73,49 @@ def test_noalloc_refuses_what_the_scratch_cannot_hold(gpu):
     with pytest.raises(BsattnError) as e:
         c2.decodeNoAlloc(q65, 0.1, torch.empty_like(q65))
     assert e.value.code == _lib.ERR_RANGE
+
+
+def test_noalloc_captured_after_append_step(gpu):
+    """A captured [appendStep, decodeNoAlloc] step (device-side lengths, no
+    bsattn_sync in between), replayed with new inputs copied in, equals the
+    eager append + decode bit for bit at every step, across block fills;
+    the scratch address is looked up by one call before the capture."""
+    import torch
+    STEPS, Tb = 40, 64
+    lens = [900, 2 * Tb - 3, 2500]
+    w = make_workload(9800, B=3, Hq=32, Hkv=8, T=max(lens), Tb=Tb, dtype="bf16", top_k=8, lens=lens,
+                      salient_frac=0.01)
+    mbps = (max(lens) + STEPS) // Tb + 3
+    a, b = new_cache(w, mbps=mbps), new_cache(w, mbps=mbps)
+    fill(a, w, gpu)
+    fill(b, w, gpu)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(9801)
+    K_ = torch.randn(STEPS, 3, 8, 1, 128, device=gpu, generator=g).to(torch.bfloat16)
+    V_ = torch.randn(STEPS, 3, 8, 1, 128, device=gpu, generator=g).to(torch.bfloat16)
+    Q_ = torch.randn(STEPS, 3, 32, 1, 128, device=gpu, generator=g).to(torch.bfloat16)
+    a.reserve(STEPS)
+    kbuf, vbuf, qbuf = K_[0].clone(), V_[0].clone(), Q_[0].clone()
+    out = torch.empty_like(qbuf)
+    # step 0 eagerly (warms the scratch lookup before the capture)
+    a.appendStep(kbuf, vbuf)
+    a.decodeNoAlloc(qbuf, w.scale, out)
+    b.append(K_[0], V_[0])
+    ref = b.decode(Q_[0], w.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), "step 0 differs"
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        a.appendStep(kbuf, vbuf)
+        a.decodeNoAlloc(qbuf, w.scale, out)
+    for i in range(1, STEPS):
+        kbuf.copy_(K_[i])
+        vbuf.copy_(V_[i])
+        qbuf.copy_(Q_[i])
+        gr.replay()
+        b.append(K_[i], V_[i])
+        ref = b.decode(Q_[i], w.scale)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"step {i} differs"
+    a.sync()
+    assert [a.seqLen(s) for s in range(3)] == [n + STEPS for n in lens]
