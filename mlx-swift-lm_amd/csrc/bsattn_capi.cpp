@@ -321,6 +321,11 @@ int bsattn_cache_create(const bsattn_desc* desc, bsattn_cache** out) try {
   g.nr = d.recent_blocks;
   g.nsel_max = d.top_k + d.sink_blocks + d.recent_blocks;
   g.nsplit = (g.nsel_max + kWaves - 1) / kWaves;
+  {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, desc->device) != hipSuccess) cus = 0;
+    g.cus = cus;  // 0: attention workgroups keep kWaves waves
+  }
   g.mbps = d.max_blocks_per_seq;
   g.sstride = (g.mbps + 63) & ~63;
   g.bt_off = d.max_seqs;
@@ -693,14 +698,16 @@ static Workspace cache_workspace(const bsattn_cache* c) {
 // kMaxBatch entries: the fused decode kernel where it applies, else scoring
 // and selection inside the attention kernel when every entry's candidates
 // fit it, else separate selection.  The workspaces are per launch (launches
-// on one stream run in order).  profile: time the launches when profiling
-// is on.
+// on one stream run in order).  nseq: the call's sequences (n / nseq query
+// tokens each), from which every launch's splits are planned.  profile:
+// time the launches when profiling is on.
 enum class Op { Select, Attend, Decode };
-static int run_entries(bsattn_cache* c, Op op, const void* q, const Entry* es, int n, int qhs,
+static int run_entries(bsattn_cache* c, Op op, const void* q, const Entry* es, int n, int nseq, int qhs,
                        const int32_t* idx_in, int32_t* idx_out, float scale, void* out, hipStream_t s,
                        const Workspace& ws, bool profile = true) {
   const Geometry& g = c->geo;
   const size_t idx_row = (size_t)g.hkv * g.nsel_max;
+  const int waves = attend_waves(g, nseq);
   for (int e0 = 0; e0 < n; e0 += kMaxBatch) {
     const SeqBatch b = make_batch(es, e0, std::min(kMaxBatch, n - e0), qhs);
     int max_nc = 0;
@@ -714,18 +721,18 @@ static int run_entries(bsattn_cache* c, Op op, const void* q, const Entry* es, i
     if (op == Op::Select) {
       e = launch_select(g, b, qq, ws.scores, ws.err, io, max_nc, s, prof);
     } else if (op == Op::Attend) {
-      if (fused_decode_ok(g, b.n, max_nc))
-        e = launch_fused_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, ws.partials, s, prof);
+      if (fused_decode_ok(g, nseq, max_nc))
+        e = launch_fused_attend(g, b, nseq, qq, idx_in + e0 * idx_row, scale, oo, ws.partials, s, prof);
       else
-        e = launch_attend(g, b, qq, idx_in + e0 * idx_row, scale, oo, ws.partials, s, prof);
-    } else if (fused_decode_ok(g, b.n, max_nc)) {
-      e = launch_fused_decode(g, b, qq, io, len_first(c, es, e0, b.n), scale, oo, ws.partials, s, prof);
+        e = launch_attend(g, b, qq, idx_in + e0 * idx_row, waves, scale, oo, ws.partials, s, prof);
+    } else if (fused_decode_ok(g, nseq, max_nc)) {
+      e = launch_fused_decode(g, b, nseq, qq, io, len_first(c, es, e0, b.n), scale, oo, ws.partials, s, prof);
     } else if (max_nc > fused_select_limit(g.top_k)) {
       int32_t* sel = io ? io : ws.idx;
       e = launch_select(g, b, qq, ws.scores, ws.err, sel, max_nc, s, prof);
-      if (e == hipSuccess) e = launch_attend(g, b, qq, sel, scale, oo, ws.partials, s, prof);
+      if (e == hipSuccess) e = launch_attend(g, b, qq, sel, waves, scale, oo, ws.partials, s, prof);
     } else {
-      e = launch_decode(g, b, qq, ws.scores, io, max_nc, scale, oo, ws.partials, s, prof);
+      e = launch_decode(g, b, qq, ws.scores, io, max_nc, waves, scale, oo, ws.partials, s, prof);
     }
     prof_collect(c, prof);
     if (e != hipSuccess) return hip_fail(e, op == Op::Select ? "select launch" : op == Op::Attend ? "attend launch" : "decode launch");
@@ -742,7 +749,8 @@ int bsattn_select(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   const std::vector<Entry> es = entries(c, seqs, 1);
-  return run_entries(c, Op::Select, q, es.data(), (int)es.size(), kHeadDim, nullptr, idx_out, 0.0f, nullptr,
+  return run_entries(c, Op::Select, q, es.data(), (int)es.size(), (int)seqs.size(), kHeadDim, nullptr, idx_out,
+                     0.0f, nullptr,
                      (hipStream_t)stream, cache_workspace(c));
 } catch (...) {
   return on_exception();
@@ -757,7 +765,8 @@ int bsattn_attend(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   const std::vector<Entry> es = entries(c, seqs, 1);
-  return run_entries(c, Op::Attend, q, es.data(), (int)es.size(), kHeadDim, idx, nullptr, scale, out,
+  return run_entries(c, Op::Attend, q, es.data(), (int)es.size(), (int)seqs.size(), kHeadDim, idx, nullptr,
+                     scale, out,
                      (hipStream_t)stream, cache_workspace(c));
 } catch (...) {
   return on_exception();
@@ -772,7 +781,8 @@ int bsattn_decode(bsattn_cache* c, const void* q, const int32_t* seq_ids, int32_
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   const std::vector<Entry> es = entries(c, seqs, 1);
-  return run_entries(c, Op::Decode, q, es.data(), (int)es.size(), kHeadDim, nullptr, idx_out, scale, out,
+  return run_entries(c, Op::Decode, q, es.data(), (int)es.size(), (int)seqs.size(), kHeadDim, nullptr, idx_out,
+                     scale, out,
                      (hipStream_t)stream, cache_workspace(c));
 } catch (...) {
   return on_exception();
@@ -823,8 +833,8 @@ int bsattn_decode_noalloc(bsattn_cache* c, const void* q, const int32_t* seq_ids
   HIP_TRY(noalloc_scratch(c->d.device, &base), "hipGetSymbolAddress(scratch)");
   char* b = (char*)base;
   const Workspace ws{(float*)(b + o_sc), (float*)(b + o_err), (int32_t*)(b + o_idx), (float*)(b + o_part)};
-  return run_entries(c, Op::Decode, q, es, n_seqs, kHeadDim, nullptr, idx_out, scale, out, (hipStream_t)stream,
-                     ws, false);
+  return run_entries(c, Op::Decode, q, es, n_seqs, n_seqs, kHeadDim, nullptr, idx_out, scale, out,
+                     (hipStream_t)stream, ws, false);
 } catch (...) {
   return on_exception();
 }
@@ -885,8 +895,8 @@ int bsattn_append_decode(bsattn_cache* c, const void* k, const void* v, const vo
   }
   Timing tm[kProfKinds];
   Timing* prof = prof_slots(c, s, tm);
-  hipError_t e = launch_append_decode(g, b, sp, pb, k, v, q, c->scores, idx_out, max_nc, fused, scale,
-                                     out, c->partials, s, prof);
+  hipError_t e = launch_append_decode(g, b, sp, pb, k, v, q, c->scores, idx_out, max_nc, fused,
+                                     attend_waves(g, n_seqs), scale, out, c->partials, s, prof);
   prof_collect(c, prof);
   if (e != hipSuccess) return hip_fail(e, "append-decode launch");
   for (int sq : seqs) c->len[sq] += 1;
@@ -911,8 +921,8 @@ int bsattn_decode_multi(bsattn_cache* c, const void* q, const int32_t* seq_ids, 
   DeviceGuard dg(c->d.device);
   if (!dg.ok) return fail(BSATTN_ERR_HIP, "hipSetDevice(%d) failed", c->d.device);
   const std::vector<Entry> es = entries(c, seqs, n_query);
-  return run_entries(c, Op::Decode, q, es.data(), (int)es.size(), n_query * kHeadDim, nullptr, idx_out,
-                     scale, out, (hipStream_t)stream, cache_workspace(c));
+  return run_entries(c, Op::Decode, q, es.data(), (int)es.size(), (int)seqs.size(), n_query * kHeadDim, nullptr,
+                     idx_out, scale, out, (hipStream_t)stream, cache_workspace(c));
 } catch (...) {
   return on_exception();
 }

@@ -539,11 +539,13 @@ void decode_g(const Geometry& g, const FusedPlan& p, dim3 grid, const SeqBatch& 
   }
 }
 
+// nseq: the call's sequences, which the splits are planned for (a launch of
+// a multi-token decode holds several entries per sequence)
 template <int MD>
-hipError_t decode_impl(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
+hipError_t decode_impl(const Geometry& g, const SeqBatch& b, int nseq, const void* q, int32_t* idx,
                        bool len_first, float scale, void* out, float* partials,
                        const ModeArgs<MD>& ap, hipStream_t s, Timing* prof) {
-  const FusedPlan p = fused_plan(g, b.n);
+  const FusedPlan p = fused_plan(g, nseq);
   const int pairs = b.n * g.hkv;
   const dim3 grid(8 * ((pairs + 7) / 8) * p.S);
   const float sl2 = scale * 1.4426950408889634f;
@@ -564,9 +566,9 @@ hipError_t decode_impl(const Geometry& g, const SeqBatch& b, const void* q, int3
 
 }  // namespace
 
-bool fused_decode_ok(const Geometry& g, int n, int max_nc) {
+bool fused_decode_ok(const Geometry& g, int nseq, int max_nc) {
   if (g.kv_bits != 0 || g.group > 4 || max_nc > kFusedMaxCand || g.top_k > kSelMaxK) return false;
-  const FusedPlan p = fused_plan(g, n);
+  const FusedPlan p = fused_plan(g, nseq);
   // every split of a pair scores all of the pair's candidates: worth it with
   // one split (no redundancy, and no combine), or with few candidates.  (A CU
   // pulls ~20 GB/s while every CU loads: the 128 KiB of summaries of a
@@ -578,10 +580,10 @@ bool fused_decode_ok(const Geometry& g, int n, int max_nc) {
   return max_nc <= 64 * p.W * kWgKeys;
 }
 
-hipError_t launch_fused_decode(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx_out,
-                               bool len_first, float scale, void* out, float* partials,
+hipError_t launch_fused_decode(const Geometry& g, const SeqBatch& b, int nseq, const void* q,
+                               int32_t* idx_out, bool len_first, float scale, void* out, float* partials,
                                hipStream_t s, Timing* prof) {
-  return decode_impl<kModeFused>(g, b, q, idx_out, len_first, scale, out, partials, NoAppend{}, s, prof);
+  return decode_impl<kModeFused>(g, b, nseq, q, idx_out, len_first, scale, out, partials, NoAppend{}, s, prof);
 }
 
 hipError_t launch_fused_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
@@ -589,13 +591,14 @@ hipError_t launch_fused_append_decode(const Geometry& g, const SeqBatch& b, cons
                                       int32_t* idx_out, float scale, void* out, float* partials,
                                       hipStream_t s, Timing* prof) {
   const AppendArgs ap{sp, pb, (const uint16_t*)k, (const uint16_t*)v};
-  return decode_impl<kModeFusedAppend>(g, b, q, idx_out, true, scale, out, partials, ap, s, prof);
+  return decode_impl<kModeFusedAppend>(g, b, b.n, q, idx_out, true, scale, out, partials, ap, s, prof);
 }
 
-hipError_t launch_fused_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
-                               float scale, void* out, float* partials, hipStream_t s, Timing* prof) {
-  return decode_impl<kModeGiven>(g, b, q, const_cast<int32_t*>(idx), false, scale, out, partials, NoAppend{},
-                                 s, prof);
+hipError_t launch_fused_attend(const Geometry& g, const SeqBatch& b, int nseq, const void* q,
+                               const int32_t* idx, float scale, void* out, float* partials, hipStream_t s,
+                               Timing* prof) {
+  return decode_impl<kModeGiven>(g, b, nseq, q, const_cast<int32_t*>(idx), false, scale, out, partials,
+                                 NoAppend{}, s, prof);
 }
 
 }  // namespace bsattn

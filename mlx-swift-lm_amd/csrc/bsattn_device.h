@@ -494,14 +494,22 @@ constexpr int kWgKeys = 8;
 // per-(slot, wave) counts of keys above / at the threshold
 constexpr int kWgScratch = kWaveBins + 64 + 4 + 2 * 16 + 2 * 64;
 
-struct WgCand {
-  float score[kWgKeys];
-  int page[kWgKeys];
+template <int NK>
+struct WgCandT {
+  float score[NK];
+  int page[NK];
 };
+using WgCand = WgCandT<kWgKeys>;
+// keys per lane the attention workgroup's selection holds: its W waves
+// cover the fused selection's 2048 candidates (8 at 4 waves, 4 at 9)
 template <int W>
+constexpr int attend_keys() {
+  return W <= 4 ? kWgKeys : 4;
+}
+template <int W, int NK = kWgKeys>
 __device__ __forceinline__ void wg_cand_load(const float* __restrict__ srow,
                                              const int32_t* __restrict__ bt, int c0, int mbps,
-                                             int wave, WgCand& wc) {
+                                             int wave, WgCandT<NK>& wc) {
   const int lane = threadIdx.x & 63;
   // unconditional loads, every score before any page: loads complete in
   // issue order (the selection needs the scores first, the pages only once
@@ -509,9 +517,9 @@ __device__ __forceinline__ void wg_cand_load(const float* __restrict__ srow,
   // joins.  Slots past the table read its last row; the selection reads
   // only slots below nc <= mbps - c0.
 #pragma unroll
-  for (int k = 0; k < kWgKeys; ++k) wc.score[k] = srow[min(c0 + 64 * (W * k + wave) + lane, mbps - 1)];
+  for (int k = 0; k < NK; ++k) wc.score[k] = srow[min(c0 + 64 * (W * k + wave) + lane, mbps - 1)];
 #pragma unroll
-  for (int k = 0; k < kWgKeys; ++k)
+  for (int k = 0; k < NK; ++k)
     wc.page[k] = bt != nullptr ? bt[min(c0 + 64 * (W * k + wave) + lane, mbps - 1)] : 0;
 }
 
@@ -655,9 +663,10 @@ __device__ __forceinline__ uint32_t wg_kth_key(const uint32_t (&key)[S], const b
 // wg_cand_load left them; writes the K chosen block indices, ascending, to
 // sel_blk and their pages to sel_page.  Every wave of the workgroup calls
 // it (it contains workgroup barriers); ws: kWgScratch words of LDS.
-template <int S, int W>
-__device__ __forceinline__ void wg_topk_s(const WgCand& wc, int c0, int nc, int K, int* sel_blk,
+template <int S, int W, int NK>
+__device__ __forceinline__ void wg_topk_s(const WgCandT<NK>& wc, int c0, int nc, int K, int* sel_blk,
                                           int* sel_page, uint32_t* ws) {
+  static_assert(S <= NK && S * W <= 64, "slots beyond the loaded keys or the (slot, wave) counts");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint32_t key[S];
   bool real[S];
@@ -703,14 +712,17 @@ __device__ __forceinline__ void wg_topk_s(const WgCand& wc, int c0, int nc, int 
   }
 }
 
-// S = smallest power of two with 64 * W * S >= nc (nc <= 64 * W * kWgKeys)
-template <int W>
-__device__ __forceinline__ void wg_topk(const WgCand& wc, int c0, int nc, int K, int* sel_blk,
+// S = smallest power of two with 64 * W * S >= nc (nc <= 64 * W * NK; the
+// callers' hosts keep nc within 64 * W * min(NK, 64 / W), so the S = 8 path
+// of a workgroup of more than 8 waves is never taken)
+template <int W, int NK>
+__device__ __forceinline__ void wg_topk(const WgCandT<NK>& wc, int c0, int nc, int K, int* sel_blk,
                                         int* sel_page, uint32_t* ws) {
-  if (nc <= 64 * W) wg_topk_s<1, W>(wc, c0, nc, K, sel_blk, sel_page, ws);
-  else if (nc <= 128 * W) wg_topk_s<2, W>(wc, c0, nc, K, sel_blk, sel_page, ws);
-  else if (nc <= 256 * W) wg_topk_s<4, W>(wc, c0, nc, K, sel_blk, sel_page, ws);
-  else wg_topk_s<8, W>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  if (nc <= 64 * W) wg_topk_s<1, W, NK>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else if (nc <= 128 * W) wg_topk_s<2, W, NK>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else if constexpr (NK < 8 || 8 * W > 64) wg_topk_s<4, W, NK>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else if (nc <= 256 * W) wg_topk_s<4, W, NK>(wc, c0, nc, K, sel_blk, sel_page, ws);
+  else wg_topk_s<8, W, NK>(wc, c0, nc, K, sel_blk, sel_page, ws);
 }
 
 // Block in output slot p of the selection for nb blocks: sinks [0, ns),
@@ -841,7 +853,7 @@ struct QCode {
 // Block (j) and physical page of this wave's slot, -1 when the slot is empty.
 // SEL 1 / 2: the selection is computed here from the block scores (1: wave 0
 // runs wave_topk over up to 64 * kSelKeysPerLane candidates; 2: every wave
-// runs wg_topk over up to 64 * W * kWgKeys), the candidates' block-table
+// runs wg_topk over up to 64 * W * attend_keys<W>()), the candidates' block-table
 // entries loaded alongside their scores, blocks and pages shared through
 // s_sel / s_selp; forced slots load their page before the selection is
 // known.  Split 0 then writes the selected indices to idx (if not null).
@@ -858,7 +870,7 @@ template <int TB, int W, int SEL>
 __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, int seq, int len,
                                             int slot, bool first, int wave, int lane,
                                             int32_t* __restrict__ idx, int jg,
-                                            const WaveCand* wc, const WgCand* wgc, int* s_sel,
+                                            const WaveCand* wc, const WgCandT<attend_keys<W>()>* wgc, int* s_sel,
                                             int* s_selp, uint32_t* s_ws, int& j_out,
                                             int& page_out) {
   int j = -1, page = -1;

@@ -16,6 +16,12 @@ constexpr int kMaxPatch = 240;  // metadata words patched per launch
 #define BSATTN_WAVES 4
 #endif
 constexpr int kWaves = BSATTN_WAVES;  // waves per attention workgroup (one block each)
+// The wide attention workgroup, one per CU: a call whose selected blocks
+// fill every CU with one such workgroup (8 sequences x 8 kv heads x 34
+// blocks = 4 splits of 9 waves = 256 workgroups) reads them with no CU
+// holding more waves than another, where 4-wave workgroups (576) put 3 on
+// some CUs and 2 on the rest.
+constexpr int kWavesWide = 9;
 constexpr int kMaxSplits = 512;       // attention splits per (sequence, kv head)
 // device scratch of the no-allocation decode (bsattn_noalloc.hip), per GPU
 constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
@@ -31,7 +37,8 @@ struct Geometry {
   int32_t dtype;              // 0 f16, 1 bf16
   int32_t kv_bits;            // 0, 4, 8
   int32_t gsize;              // affine group size
-  int32_t top_k, ns, nr, nsel_max, nsplit;
+  int32_t top_k, ns, nr, nsel_max, nsplit;  // nsplit: splits of kWaves (the partial workspace's)
+  int32_t cus;                // compute units of the device
   int32_t mbps;               // block-table width
   int32_t sstride;            // block-score row stride (mbps rounded up to 64)
   int32_t bt_off;             // offset of the block table inside meta
@@ -119,7 +126,7 @@ hipError_t launch_append_quantized(const Geometry& g, const AppendBatch& ab,
 hipError_t launch_summary_q(const Geometry& g, const SummaryBatch& sb, int max_count,
                             hipStream_t s, Timing* prof);
 hipError_t launch_attend_q(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
-                           const float* scores, int sel_mode, float sl2, void* out,
+                           const float* scores, int sel_mode, int waves, float sl2, void* out,
                            float* partials, hipStream_t s, Timing* prof);
 hipError_t launch_summary(const Geometry& g, const SummaryBatch& sb, int max_count,
                           hipStream_t s, Timing* prof);
@@ -136,18 +143,25 @@ int mfma_err_stride(const Geometry& g);
 hipError_t launch_select_large(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
                                float* err, int max_nc, int32_t* idx, hipStream_t s, Timing* prof,
                                bool scores_ready);
+// Waves per attention workgroup (kWaves or kWavesWide) for one call over
+// nseq sequences, from the geometry and nseq alone.  Every launch of a call
+// takes the same count, and calls that must agree bit for bit (decode and
+// select + attend, append + decode and the one-call step, a multi-token
+// decode and its single-token decodes) pass the same nseq, so their splits,
+// and the order their partials merge in, are the same.
+int attend_waves(const Geometry& g, int nseq);
 hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q,
-                         const int32_t* idx, float scale, void* out, float* partials,
+                         const int32_t* idx, int waves, float scale, void* out, float* partials,
                          hipStream_t s, Timing* prof);
 // decode = scoring + attention with the top-K selection done inside the
 // attention kernel; valid while every sequence has at most
 // fused_select_limit(top_k) candidate blocks.  idx_out may be null.
 int fused_select_limit(int top_k);
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                         int32_t* idx_out, int max_nc, float scale, void* out,
+                         int32_t* idx_out, int max_nc, int waves, float scale, void* out,
                          float* partials, hipStream_t s, Timing* prof);
 hipError_t launch_decode_attend(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                                int32_t* idx_out, int max_nc, float scale, void* out,
+                                int32_t* idx_out, int max_nc, int waves, float scale, void* out,
                                 float* partials, hipStream_t s, Timing* prof);
 // one decode step of a 16-bit cache with one new token per entry (b.len =
 // the lengths after it): fused (requires fused_decode_ok): one launch of the
@@ -159,30 +173,32 @@ hipError_t launch_decode_attend(const Geometry& g, const SeqBatch& b, const void
 // >= 1, so the block an append completes is forced, never scored.
 hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
                                 const PatchBatch& pb, const void* k, const void* v, const void* q,
-                                float* scores, int32_t* idx_out, int max_nc, bool fused, float scale,
-                                void* out, float* partials, hipStream_t s, Timing* prof);
+                                float* scores, int32_t* idx_out, int max_nc, bool fused, int waves,
+                                float scale, void* out, float* partials, hipStream_t s, Timing* prof);
 // split combine of nsplit partials per (entry, q head) into out
 hipError_t launch_combine(const Geometry& g, const SeqBatch& b, const float* partials, int nsplit,
                           void* out, hipStream_t s, Timing* prof);
 // fused decode (bsattn_decode.hip): scoring, selection, gather + attention
 // (+ combine) for 16-bit caches with GQA groups up to 4; fused_decode_ok
-// tells whether a launch of n entries with at most max_nc candidate blocks
-// each fits it.  len_first: each workgroup reads its entry's length before
-// the summaries (for ragged batches; otherwise every row of the block-table
-// width is read at once).  idx_out may be null.
-bool fused_decode_ok(const Geometry& g, int n, int max_nc);
+// tells whether the launches of a call over nseq sequences (its splits are
+// planned for them, whatever a launch's entry count) with at most max_nc
+// candidate blocks per entry fit it.  len_first: each workgroup reads its
+// entry's length before the summaries (for ragged batches; otherwise every
+// row of the block-table width is read at once).  idx_out may be null.
+bool fused_decode_ok(const Geometry& g, int nseq, int max_nc);
 // exact (canonical) block scores of every ranked candidate into `scores`
 hipError_t launch_score(const Geometry& g, const SeqBatch& b, const void* q, float* scores, int max_nc,
                         hipStream_t s, Timing* prof);
 
-hipError_t launch_fused_decode(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx_out,
-                               bool len_first, float scale, void* out, float* partials,
+hipError_t launch_fused_decode(const Geometry& g, const SeqBatch& b, int nseq, const void* q,
+                               int32_t* idx_out, bool len_first, float scale, void* out, float* partials,
                                hipStream_t s, Timing* prof);
 // the same kernel's gather + attention over given indices (used by
 // bsattn_attend exactly where decode takes the fused path, so that
 // decode == select + attend bit for bit)
-hipError_t launch_fused_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
-                               float scale, void* out, float* partials, hipStream_t s, Timing* prof);
+hipError_t launch_fused_attend(const Geometry& g, const SeqBatch& b, int nseq, const void* q,
+                               const int32_t* idx, float scale, void* out, float* partials, hipStream_t s,
+                               Timing* prof);
 // one launch per decode step: each entry's new token (k, v: [n][Hkv][128]) is
 // stored at position b.len[i] - 1 on page sp.page[i] before the fused decode
 // gathers it, the block it fills gets its summary, and the metadata patches

@@ -290,7 +290,7 @@ __global__ __launch_bounds__(64) void k_topk(Geometry geo, SeqBatch sb,
 // (o, m, l) for k_combine.  grid (nsplit, Hkv, n)
 // ---------------------------------------------------------------------------
 template <int DT, int TB, int G, int W, int SEL>
-__global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
+__global__ __launch_bounds__(64 * W, W > 4 ? 1 : 3) void k_attend(Geometry geo, SeqBatch sb,
                                                    const uint16_t* __restrict__ q,
                                                    int32_t* __restrict__ idx,
                                                    const float* __restrict__ scores,
@@ -323,13 +323,14 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
   // the selecting wave loads every candidate's score and page before the
   // sequence length is known
   WaveCand wc;
-  WgCand wgc;
+  WgCandT<attend_keys<W>()> wgc;
   if constexpr (SEL == 1) {
     if (wave == 0)
       wave_cand_load(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns,
                      geo.mbps, wc);
   } else if constexpr (SEL == 2) {
-    wg_cand_load<W>(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns, geo.mbps, wave,
+    wg_cand_load<W, attend_keys<W>()>(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns,
+                                      geo.mbps, wave,
                     wgc);
   }
   const int len = uniform(entry_len(geo, sb, bi, seq));
@@ -429,7 +430,7 @@ __global__ __launch_bounds__(64 * W, 3) void k_attend(Geometry geo, SeqBatch sb,
     store_empty<G>(s_m[wave], s_l[wave], s_o[wave], lane);
   }
   __syncthreads();
-  attend_merge<DT, G, W>(geo, sb, bi, h, split, geo.nsplit, s_m, s_l, s_o, out, partials);
+  attend_merge<DT, G, W>(geo, sb, bi, h, split, (int)gridDim.x, s_m, s_l, s_o, out, partials);
 }
 
 // ---------------------------------------------------------------------------
@@ -689,43 +690,81 @@ hipError_t launch_select(const Geometry& g, const SeqBatch& b, const void* q, fl
   return hipGetLastError();
 }
 
-template <int DT, int TB, int SEL>
-static void attend_dispatch(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
-                            int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
-                            hipStream_t s, Timing* prof) {
-  constexpr int W = kWaves;
+template <int DT, int TB, int SEL, int W>
+static void attend_dispatch_w(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
+                              int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
+                              hipStream_t s, Timing* prof) {
   const dim3 blk(64 * W);
   const int kd = kProfAttend;
-  switch (g.group) {
-    case 1: launch(k_attend<DT, TB, 1, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
-    case 2: launch(k_attend<DT, TB, 2, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
-    case 4: launch(k_attend<DT, TB, 4, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
-    case 8: launch(k_attend<DT, TB, 8, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
-    default: launch(k_attend<DT, TB, 16, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+  if constexpr (W != kWaves) {  // the wide workgroup serves groups of up to 4 heads
+    switch (g.group) {
+      case 1: launch(k_attend<DT, TB, 1, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+      case 2: launch(k_attend<DT, TB, 2, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+      default: launch(k_attend<DT, TB, 4, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    }
+  } else {
+    switch (g.group) {
+      case 1: launch(k_attend<DT, TB, 1, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+      case 2: launch(k_attend<DT, TB, 2, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+      case 4: launch(k_attend<DT, TB, 4, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+      case 8: launch(k_attend<DT, TB, 8, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+      default: launch(k_attend<DT, TB, 16, W, SEL>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+    }
   }
+}
+
+template <int DT, int TB, int SEL>
+static void attend_dispatch(const Geometry& g, int waves, dim3 grid, const SeqBatch& b, const uint16_t* q,
+                            int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
+                            hipStream_t s, Timing* prof) {
+  if constexpr (SEL != 1) {  // one selecting wave runs in kWaves-wave workgroups only
+    if (waves == kWavesWide) {
+      attend_dispatch_w<DT, TB, SEL, kWavesWide>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
+      return;
+    }
+  }
+  attend_dispatch_w<DT, TB, SEL, kWaves>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
+}
+
+int attend_waves(const Geometry& g, int nseq) {
+  // the wide workgroup: groups of up to 4 heads, and splits that fit one
+  // workgroup per CU; then only where no CU holds more waves than with
+  // kWaves-wave workgroups spread over the CUs.  (Its fused selection holds
+  // 64 * kWavesWide * attend_keys = 2304 candidates, more than the 2048 a
+  // decode selects inside the attention kernel; beyond those it takes the
+  // given-index kernel, as kWaves does.)
+  if (kWaves != 4 || g.group > 4 || g.cus <= 0) return kWaves;
+  const int64_t pairs = (int64_t)std::min(std::max(nseq, 1), kMaxBatch) * g.hkv;
+  const int64_t wide = pairs * ((g.nsel_max + kWavesWide - 1) / kWavesWide);
+  if (wide > g.cus) return kWaves;
+  const int64_t base = pairs * g.nsplit;
+  const int64_t base_waves = (int64_t)kWaves * ((base + g.cus - 1) / g.cus);
+  return kWavesWide < base_waves ? kWavesWide : kWaves;
 }
 
 template <int SEL>
 static hipError_t attend_impl(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
-                              const float* scores, float scale, void* out, float* partials,
+                              const float* scores, int waves, float scale, void* out, float* partials,
                               hipStream_t s, Timing* prof) {
   const float sl2 = scale * 1.4426950408889634f;
-  dim3 grid(g.nsplit, g.hkv, b.n);
+  // splits of this launch: the partial workspace holds g.nsplit (kWaves-wave) splits, the most
+  const int nsplit = (g.nsel_max + waves - 1) / waves;
+  dim3 grid(nsplit, g.hkv, b.n);
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* oo = (uint16_t*)out;
   if (g.kv_bits != 0) {
-    hipError_t e = launch_attend_q(g, b, q, idx, scores, SEL, sl2, out, partials, s, prof);
+    hipError_t e = launch_attend_q(g, b, q, idx, scores, SEL, waves, sl2, out, partials, s, prof);
     if (e != hipSuccess) return e;
   } else if (g.dtype == 0) {
-    if (g.tb == 64) attend_dispatch<0, 64, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
-    else attend_dispatch<0, 32, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+    if (g.tb == 64) attend_dispatch<0, 64, SEL>(g, waves, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+    else attend_dispatch<0, 32, SEL>(g, waves, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
   } else {
-    if (g.tb == 64) attend_dispatch<1, 64, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
-    else attend_dispatch<1, 32, SEL>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+    if (g.tb == 64) attend_dispatch<1, 64, SEL>(g, waves, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+    else attend_dispatch<1, 32, SEL>(g, waves, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
   }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || g.nsplit == 1) return e;
-  return launch_combine(g, b, partials, g.nsplit, out, s, prof);
+  if (e != hipSuccess || nsplit == 1) return e;
+  return launch_combine(g, b, partials, nsplit, out, s, prof);
 }
 
 template <int DT>
@@ -754,8 +793,8 @@ hipError_t launch_combine(const Geometry& g, const SeqBatch& b, const float* par
 }
 
 hipError_t launch_attend(const Geometry& g, const SeqBatch& b, const void* q, const int32_t* idx,
-                         float scale, void* out, float* partials, hipStream_t s, Timing* prof) {
-  return attend_impl<0>(g, b, q, const_cast<int32_t*>(idx), nullptr, scale, out, partials, s,
+                         int waves, float scale, void* out, float* partials, hipStream_t s, Timing* prof) {
+  return attend_impl<0>(g, b, q, const_cast<int32_t*>(idx), nullptr, waves, scale, out, partials, s,
                             prof);
 }
 
@@ -764,29 +803,31 @@ int fused_select_limit(int top_k) {
 }
 
 hipError_t launch_decode_attend(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                                int32_t* idx_out, int max_nc, float scale, void* out,
+                                int32_t* idx_out, int max_nc, int waves, float scale, void* out,
                                 float* partials, hipStream_t s, Timing* prof) {
   // every wave of the workgroup takes a share of the candidates (measured
   // faster than one wave selecting, also for 510 candidates: the per-key
   // work of each pass shrinks W-fold for a few workgroup barriers); with
   // few waves per workgroup, one wave's larger capacity is used beyond that
+  // (both callers keep max_nc within fused_select_limit, so the one-wave
+  // selection, which runs in kWaves-wave workgroups only, is not reached)
   if (max_nc <= 64 * kWaves * kWgKeys)
-    return attend_impl<2>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
-  return attend_impl<1>(g, b, q, idx_out, scores, scale, out, partials, s, prof);
+    return attend_impl<2>(g, b, q, idx_out, scores, waves, scale, out, partials, s, prof);
+  return attend_impl<1>(g, b, q, idx_out, scores, kWaves, scale, out, partials, s, prof);
 }
 
 hipError_t launch_decode(const Geometry& g, const SeqBatch& b, const void* q, float* scores,
-                         int32_t* idx_out, int max_nc, float scale, void* out,
+                         int32_t* idx_out, int max_nc, int waves, float scale, void* out,
                          float* partials, hipStream_t s, Timing* prof) {
   hipError_t e = launch_score(g, b, q, scores, max_nc, s, prof);
   if (e != hipSuccess) return e;
-  return launch_decode_attend(g, b, q, scores, idx_out, max_nc, scale, out, partials, s, prof);
+  return launch_decode_attend(g, b, q, scores, idx_out, max_nc, waves, scale, out, partials, s, prof);
 }
 
 hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const StepPages& sp,
                                 const PatchBatch& pb, const void* k, const void* v, const void* q,
-                                float* scores, int32_t* idx_out, int max_nc, bool fused, float scale,
-                                void* out, float* partials, hipStream_t s, Timing* prof) {
+                                float* scores, int32_t* idx_out, int max_nc, bool fused, int waves,
+                                float scale, void* out, float* partials, hipStream_t s, Timing* prof) {
   // the fused decode appends, scores and attends in one launch
   if (fused)
     return launch_fused_append_decode(g, b, sp, pb, k, v, q, idx_out, scale, out, partials, s, prof);
@@ -804,7 +845,7 @@ hipError_t launch_append_decode(const Geometry& g, const SeqBatch& b, const Step
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_decode_attend(g, b, q, scores, idx_out, max_nc, scale, out, partials, s, prof);
+  return launch_decode_attend(g, b, q, scores, idx_out, max_nc, waves, scale, out, partials, s, prof);
 }
 
 hipError_t launch_export(const Geometry& g, const SeqBatch& b, int T, void* k_out, void* v_out,

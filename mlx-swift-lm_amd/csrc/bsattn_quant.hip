@@ -336,7 +336,7 @@ __global__ __launch_bounds__(128) void k_summary_q(Geometry geo, SummaryBatch sb
 // grid (nsplit, Hkv, n)
 // ---------------------------------------------------------------------------
 template <int TB, int G, int W, int SEL, int KB>
-__global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch sb,
+__global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo, SeqBatch sb,
                                                      const uint16_t* __restrict__ q,
                                                      int32_t* __restrict__ idx,
                                                      const float* __restrict__ scores,
@@ -371,13 +371,14 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
   // the selecting wave loads every candidate's score and page before the
   // sequence length is known
   WaveCand wc;
-  WgCand wgc;
+  WgCandT<attend_keys<W>()> wgc;
   if constexpr (SEL == 1) {
     if (wave == 0)
       wave_cand_load(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns,
                      geo.mbps, wc);
   } else if constexpr (SEL == 2) {
-    wg_cand_load<W>(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns, geo.mbps, wave,
+    wg_cand_load<W, attend_keys<W>()>(score_row(geo, scores, bi, h), block_table(geo, seq), geo.ns,
+                                      geo.mbps, wave,
                     wgc);
   }
   const int len = uniform(entry_len(geo, sb, bi, seq));
@@ -629,7 +630,7 @@ __global__ __launch_bounds__(64 * W, 2) void k_attend_q(Geometry geo, SeqBatch s
     store_empty<G>(s_m[wave], s_l[wave], s_o[wave], lane);
   }
   __syncthreads();
-  attend_merge<0, G, W>(geo, sb, bi, h, split, geo.nsplit, s_m, s_l, s_o, out, partials);
+  attend_merge<0, G, W>(geo, sb, bi, h, split, (int)gridDim.x, s_m, s_l, s_o, out, partials);
 }
 
 // ---------------------------------------------------------------------------
@@ -717,12 +718,24 @@ hipError_t launch_summary_q(const Geometry& g, const SummaryBatch& sb, int max_c
 }
 
 template <int TB, int SEL, int KB>
-static void attend_q_group(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
+static void attend_q_group(const Geometry& g, int waves, dim3 grid, const SeqBatch& b, const uint16_t* q,
                            int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
                            hipStream_t s, Timing* prof) {
+  const int kd = kProfAttend;
+  if constexpr (SEL != 1) {  // the wide workgroup: groups of up to 4 heads, never one selecting wave
+    if (waves == kWavesWide) {
+      constexpr int W = kWavesWide;
+      const dim3 blk(64 * W);
+      switch (g.group) {
+        case 1: launch(k_attend_q<TB, 1, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+        case 2: launch(k_attend_q<TB, 2, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+        default: launch(k_attend_q<TB, 4, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+      }
+      return;
+    }
+  }
   constexpr int W = kWaves;
   const dim3 blk(64 * W);
-  const int kd = kProfAttend;
   switch (g.group) {
     case 1: launch(k_attend_q<TB, 1, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
     case 2: launch(k_attend_q<TB, 2, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
@@ -733,27 +746,28 @@ static void attend_q_group(const Geometry& g, dim3 grid, const SeqBatch& b, cons
 }
 
 template <int SEL>
-static void attend_q_sel(const Geometry& g, dim3 grid, const SeqBatch& b, const uint16_t* q,
+static void attend_q_sel(const Geometry& g, int waves, dim3 grid, const SeqBatch& b, const uint16_t* q,
                          int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
                          hipStream_t s, Timing* prof) {
   if (g.kv_bits == 4) {
-    if (g.tb == 64) attend_q_group<64, SEL, 4>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
-    else attend_q_group<32, SEL, 4>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
+    if (g.tb == 64) attend_q_group<64, SEL, 4>(g, waves, grid, b, q, idx, sc, sl2, out, part, s, prof);
+    else attend_q_group<32, SEL, 4>(g, waves, grid, b, q, idx, sc, sl2, out, part, s, prof);
   } else {
-    if (g.tb == 64) attend_q_group<64, SEL, 8>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
-    else attend_q_group<32, SEL, 8>(g, grid, b, q, idx, sc, sl2, out, part, s, prof);
+    if (g.tb == 64) attend_q_group<64, SEL, 8>(g, waves, grid, b, q, idx, sc, sl2, out, part, s, prof);
+    else attend_q_group<32, SEL, 8>(g, waves, grid, b, q, idx, sc, sl2, out, part, s, prof);
   }
 }
 
+// grid (splits of `waves`, Hkv, n); the caller combines the splits
 hipError_t launch_attend_q(const Geometry& g, const SeqBatch& b, const void* q, int32_t* idx,
-                           const float* scores, int sel_mode, float sl2, void* out,
+                           const float* scores, int sel_mode, int waves, float sl2, void* out,
                            float* partials, hipStream_t s, Timing* prof) {
-  const dim3 grid(g.nsplit, g.hkv, b.n);
+  const dim3 grid((g.nsel_max + waves - 1) / waves, g.hkv, b.n);
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* oo = (uint16_t*)out;
-  if (sel_mode == 1) attend_q_sel<1>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
-  else if (sel_mode == 2) attend_q_sel<2>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
-  else attend_q_sel<0>(g, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+  if (sel_mode == 1) attend_q_sel<1>(g, waves, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+  else if (sel_mode == 2) attend_q_sel<2>(g, waves, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
+  else attend_q_sel<0>(g, waves, grid, b, qq, idx, scores, sl2, oo, partials, s, prof);
   return hipGetLastError();
 }
 

@@ -30,6 +30,11 @@ CASES = {
     "bf16-tb64-splits-fill": ("bf16", 64, 8, 2, 9, 1, 2, 0, [830, 120], 80, None),
     # top_k 0 (sinks and recent only) over 2 splits, with block fills
     "f16-tb32-topk0": ("f16", 32, 8, 2, 0, 2, 3, 0, [300, 62], 40, None),
+    # 2 sequences x 8 kv heads, 130 slots, more than 256 candidates: the
+    # step's attention runs in 9-wave workgroups (15 splits, one workgroup
+    # per CU), with block fills
+    "bf16-tb64-g4-wide": ("bf16", 64, 32, 8, 128, 1, 1, 0, [20000, 19050], 40, None),
+    "f16-tb32-g2-wide": ("f16", 32, 16, 8, 128, 1, 1, 0, [9990, 9650], 40, None),
 }
 
 
