@@ -725,6 +725,245 @@ __device__ __forceinline__ void wg_topk(const WgCandT<NK>& wc, int c0, int nc, i
   else wg_topk_s<8, W, NK>(wc, c0, nc, K, sel_blk, sel_page, ws);
 }
 
+// ---------------------------------------------------------------------------
+// The attention workgroup's top-K where each wave needs only its own slot's
+// block.  The candidates spread over the W waves as for wg_topk (slot k of
+// wave w, lane l holds candidate c0 + 64 g + l, group g = W k + w), and the
+// selection is the same (K largest keys, ties to the lower index), with four
+// workgroup barriers where wg_topk and the read of its output take seven:
+//  1. the waves' key bounds, the histogram cleared behind the same barrier;
+//  2. the histogram fill;
+//  3. the keys of the bin that holds the K-th (no barrier after: the small
+//     set is not written again);
+//  4. every group's masks of keys above and at the K-th key, and every
+//     candidate's page at a fixed position.
+// Each wave then counts the groups' taken blocks (ties to the lowest
+// indices), finds the group and lane of its rank-th selected block, and
+// reads its page.  A K-th bin of more than 64 keys takes another histogram
+// pass (two barriers more).
+// ---------------------------------------------------------------------------
+template <int W>
+constexpr int slot_scratch_words() {
+  return kWaveBins + 64 + 4 + 2 * 16 + 4 * 64 + 64 * W * attend_keys<W>();
+}
+
+template <int S, int W, int NK>
+__device__ __forceinline__ void wg_topk_slot_s(const WgCandT<NK>& wc, int c0, int nc, int K, int rank,
+                                               int* j_out, int* page_out, int* row, uint32_t* ws) {
+  static_assert(S <= NK && S * W <= 64, "slots beyond the loaded keys or the 64 groups");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  uint32_t* hist = ws;
+  uint32_t* small = ws + kWaveBins;
+  uint32_t* small_n = small + 64;
+  uint32_t* xlo = small_n + 4;
+  uint32_t* xhi = xlo + 16;
+  uint64_t* gmask = (uint64_t*)(xhi + 16);
+  uint64_t* emask = gmask + 64;
+  int* gpage = (int*)(emask + 64);
+  uint32_t key[S];
+  bool real[S];
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    real[k] = 64 * (W * k + wave) + lane < nc;
+    key[k] = real[k] ? score_key(wc.score[k]) : 0u;
+  }
+  // 1. bounds; the histogram is cleared behind the same barrier
+  uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+#pragma unroll
+  for (int k = 0; k < S; ++k)
+    if (real[k]) {
+      lo = min(lo, key[k]);
+      hi = max(hi, key[k]);
+    }
+  lo = wave_min_u32(lo);
+  hi = wave_max_u32(hi);
+  if (lane == 0) {
+    xlo[wave] = lo;
+    xhi[wave] = hi;
+  }
+  for (int i = threadIdx.x; i < kWaveBins / 4; i += 64 * W) ((u32x4*)hist)[i] = u32x4{0u, 0u, 0u, 0u};
+  if (threadIdx.x == 0) *small_n = 0u;
+  __syncthreads();
+  lo = xlo[0];
+  hi = xhi[0];
+#pragma unroll
+  for (int w = 1; w < W; ++w) {
+    lo = min(lo, xlo[w]);
+    hi = max(hi, xhi[w]);
+  }
+  int need = K;
+  bool by_value = true;
+  uint32_t tau;
+#pragma unroll 1
+  while (true) {
+    if (lo == hi) {
+      tau = lo;
+      break;
+    }
+    const float vlo = key_value(lo), span = key_value(hi) - vlo;
+    const bool use_v = by_value && __builtin_isfinite(vlo) && __builtin_isfinite(span) && span > 0.0f;
+    // bins need only be monotone in the key: an approximate reciprocal will do
+    const float scale = use_v ? (float)(kWaveBins - 1) * __builtin_amdgcn_rcpf(span) : 0.0f;
+    const int sh = use_v ? 0 : max(0, 32 - __clz(hi - lo) - 10);
+    auto bin = [&](uint32_t k) -> int {
+      return use_v ? min(kWaveBins - 1, (int)((key_value(k) - vlo) * scale)) : (int)((k - lo) >> sh);
+    };
+    // 2. the histogram
+    int bk[S];  // each key's bin in this pass, -1 outside the range
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+      bk[k] = real[k] && key[k] >= lo && key[k] <= hi ? bin(key[k]) : -1;
+      if (bk[k] >= 0) atomicAdd(&hist[bk[k]], 1u);
+    }
+    __syncthreads();
+    int b_star, abv, cnt;
+    find_kth_bin(hist, need, b_star, abv, cnt);
+    need -= abv;
+    if (!use_v && sh == 0) {  // one-value bin
+      tau = lo + (uint32_t)b_star;
+      break;
+    }
+    if (cnt <= 64) {
+      // 3. the bin's keys from every wave, in any order
+      int mine_n = 0;
+      uint64_t m[S];
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        m[k] = __ballot(bk[k] == b_star);
+        mine_n += __popcll(m[k]);
+      }
+      uint32_t base = 0u;
+      if (lane == 0 && mine_n > 0) base = atomicAdd(small_n, (uint32_t)mine_n);
+      base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        if ((m[k] >> lane) & 1ull) small[base + __popcll(m[k] & below)] = key[k];
+        base += __popcll(m[k]);
+      }
+      __syncthreads();
+      const bool valid = lane < cnt;
+      const uint32_t x = valid ? small[lane] : 0u;
+      if (cnt <= 16) {
+        int gt = 0, ge = 0;
+        for (int jj = 0; jj < cnt; ++jj) {
+          const uint32_t xj = (uint32_t)__builtin_amdgcn_readlane((int)x, jj);
+          gt += xj > x;
+          ge += xj >= x;
+        }
+        const int s2 = __ffsll((unsigned long long)__ballot(valid && gt < need && need <= ge)) - 1;
+        tau = (uint32_t)__builtin_amdgcn_readlane((int)x, s2);
+      } else {
+        const uint32_t mn = wave_min_u32(valid ? x : 0xFFFFFFFFu), mx = wave_max_u32(x);
+        const uint32_t off = x - mn;
+        uint32_t t = 0u;
+        for (int bit = mx == mn ? -1 : 31 - __clz(mx - mn); bit >= 0; --bit) {
+          const uint32_t cand = t | (1u << bit);
+          if (__popcll(__ballot(valid && off >= cand)) >= need) t = cand;
+        }
+        tau = mn + t;
+      }
+      break;
+    }
+    // another pass over the K-th bin: its bounds, then a cleared histogram
+    if (use_v) {
+      uint32_t nlo = 0xFFFFFFFFu, nhi = 0u;
+#pragma unroll
+      for (int k = 0; k < S; ++k)
+        if (bk[k] == b_star) {
+          nlo = min(nlo, key[k]);
+          nhi = max(nhi, key[k]);
+        }
+      nlo = wave_min_u32(nlo);
+      nhi = wave_max_u32(nhi);
+      if (lane == 0) {
+        xlo[wave] = nlo;
+        xhi[wave] = nhi;
+      }
+      __syncthreads();  // every wave has read the histogram; the bounds are in
+      lo = xlo[0];
+      hi = xhi[0];
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        lo = min(lo, xlo[w]);
+        hi = max(hi, xhi[w]);
+      }
+    } else {
+      const uint32_t nlo = lo + ((uint32_t)b_star << sh);
+      const uint32_t span_k = (1u << sh) - 1u;
+      hi = (hi - nlo < span_k) ? hi : nlo + span_k;
+      lo = nlo;
+      __syncthreads();  // every wave has read the histogram
+    }
+    for (int i = threadIdx.x; i < kWaveBins / 4; i += 64 * W) ((u32x4*)hist)[i] = u32x4{0u, 0u, 0u, 0u};
+    by_value = false;
+    __syncthreads();  // cleared; every wave has read the bounds
+  }
+  // 4. the groups' masks of keys above and at tau, and every candidate's page
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    const int g = W * k + wave;
+    const uint64_t gtm = __ballot(real[k] && key[k] > tau);
+    const uint64_t eqm = __ballot(real[k] && key[k] == tau);
+    if (lane == 0) {
+      gmask[g] = gtm;
+      emask[g] = eqm;
+    }
+    gpage[64 * g + lane] = wc.page[k];
+  }
+  __syncthreads();
+  // lane g: group g's counts; ties go to the lowest indices
+  constexpr int NG = S * W;
+  const uint64_t gm = lane < NG ? gmask[lane] : 0ull, em = lane < NG ? emask[lane] : 0ull;
+  const int ng = __popcll(gm), ne = __popcll(em);
+  const int gt_total = wave_sum_i32(ng);
+  const int krem = K - gt_total;
+  const int e_excl = wave_scan_incl(ne) - ne;
+  const int t_eq = min(max(krem - e_excl, 0), ne);
+  const int taken = ng + t_eq;
+  const int t_excl = wave_scan_incl(taken) - taken;
+  auto group_take = [&](uint64_t gms, uint64_t ems, int tq) -> uint64_t {
+    // taken lanes of a group: above tau, or the tq lowest at tau
+    const bool eb = (ems >> lane) & 1ull;
+    const bool take = ((gms >> lane) & 1ull) || (eb && __popcll(ems & below) < tq);
+    return __ballot(take);
+  };
+  if (rank >= 0) {
+    const int src = __ffsll((unsigned long long)__ballot(lane < NG && t_excl <= rank && rank < t_excl + taken)) - 1;
+    const int r_in = rank - __builtin_amdgcn_readlane(t_excl, src);
+    const uint64_t gms = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(gm >> 32), src) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)gm, src);
+    const uint64_t ems = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(em >> 32), src) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)em, src);
+    const uint64_t tm = group_take(gms, ems, __builtin_amdgcn_readlane(t_eq, src));
+    const bool mine = ((tm >> lane) & 1ull) && __popcll(tm & below) == r_in;
+    const int b = __ffsll((unsigned long long)__ballot(mine)) - 1;
+    *j_out = c0 + 64 * src + b;
+    *page_out = gpage[64 * src + b];
+  }
+  if (row != nullptr) {  // the whole selection, ascending (one wave)
+    for (int g = 0; g < NG; ++g) {
+      const uint64_t gms = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(gm >> 32), g) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)gm, g);
+      const uint64_t ems = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(em >> 32), g) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)em, g);
+      const uint64_t tm = group_take(gms, ems, __builtin_amdgcn_readlane(t_eq, g));
+      if ((tm >> lane) & 1ull) row[__builtin_amdgcn_readlane(t_excl, g) + __popcll(tm & below)] = c0 + 64 * g + lane;
+    }
+  }
+}
+
+// S = smallest power of two with 64 * W * S >= nc (nc <= 64 * W * NK)
+template <int W, int NK>
+__device__ __forceinline__ void wg_topk_slot(const WgCandT<NK>& wc, int c0, int nc, int K, int rank, int* j_out,
+                                             int* page_out, int* row, uint32_t* ws) {
+  if (nc <= 64 * W) wg_topk_slot_s<1, W, NK>(wc, c0, nc, K, rank, j_out, page_out, row, ws);
+  else if (nc <= 128 * W) wg_topk_slot_s<2, W, NK>(wc, c0, nc, K, rank, j_out, page_out, row, ws);
+  else if constexpr (NK < 8 || 8 * W > 64) wg_topk_slot_s<4, W, NK>(wc, c0, nc, K, rank, j_out, page_out, row, ws);
+  else if (nc <= 256 * W) wg_topk_slot_s<4, W, NK>(wc, c0, nc, K, rank, j_out, page_out, row, ws);
+  else wg_topk_slot_s<8, W, NK>(wc, c0, nc, K, rank, j_out, page_out, row, ws);
+}
+
 // Block in output slot p of the selection for nb blocks: sinks [0, ns),
 // then the K ranked candidates (sel), then recent [nb - nr, nb); when the
 // candidates do not outnumber K (ranked false) every block is kept.  sel is
@@ -853,7 +1092,7 @@ struct QCode {
 // Block (j) and physical page of this wave's slot, -1 when the slot is empty.
 // SEL 1 / 2: the selection is computed here from the block scores (1: wave 0
 // runs wave_topk over up to 64 * kSelKeysPerLane candidates; 2: every wave
-// runs wg_topk over up to 64 * W * attend_keys<W>()), the candidates' block-table
+// runs wg_topk_slot over up to 64 * W * attend_keys<W>()), the candidates' block-table
 // entries loaded alongside their scores, blocks and pages shared through
 // s_sel / s_selp; forced slots load their page before the selection is
 // known.  Split 0 then writes the selected indices to idx (if not null).
@@ -885,9 +1124,21 @@ __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, 
       j = selected_block(slot, nb, ranked, geo.ns, geo.nr, K, s_sel);
       if (j >= 0) page = uniform(bt[j]);
     }
-    if (ranked && K > 0) {  // the workgroup shares the selection through LDS
-      if constexpr (SEL == 2) wg_topk<W>(*wgc, c0, nc, K, s_sel, s_selp, s_ws);
-      else if (wave == 0) wave_topk(*wc, c0, nc, K, s_sel, s_selp, s_ws);
+    if constexpr (SEL == 2) {
+      // each wave finds its own slot's block; the first wave of split 0
+      // also writes the whole selection for the index row
+      if (ranked && K > 0) {
+        int jr = -1, pr = -1;
+        wg_topk_slot<W>(*wgc, c0, nc, K, picked ? slot - geo.ns : -1, &jr, &pr,
+                        idx != nullptr && first ? s_sel : nullptr, s_ws);
+        if (picked) {
+          j = jr;
+          page = pr;
+        }
+        wave_lds_order();
+      }
+    } else if (ranked && K > 0) {  // wave 0 selects, the workgroup reads it through LDS
+      if (wave == 0) wave_topk(*wc, c0, nc, K, s_sel, s_selp, s_ws);
       __syncthreads();
       if (picked) {
         j = s_sel[slot - geo.ns];

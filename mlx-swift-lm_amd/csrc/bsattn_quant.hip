@@ -352,7 +352,7 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
   __shared__ float s_o[W][G][kHeadDim];
   __shared__ int s_sel[SEL ? kSelMaxK : 1];
   __shared__ int s_selp[SEL ? kSelMaxK : 1];
-  __shared__ __align__(16) uint32_t s_ws[SEL == 2 ? kWgScratch : SEL ? kWaveScratch : 4];
+  __shared__ __align__(16) uint32_t s_ws[SEL == 2 ? slot_scratch_words<W>() : SEL ? kWaveScratch : 4];
   const int split = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;

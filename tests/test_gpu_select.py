@@ -236,3 +236,71 @@ def test_decode_workgroup_selection(gpu, case):
     if case == "ties":
         assert list(got[0, 0][:41]) == list(range(41))
     log(f"[wg-select] {case} err={err:.3g}")
+
+
+# (B, Hq, Hkv, K, lengths in blocks): a 4-wave shape and a 9-wave one
+# (2 sequences x 8 kv heads x 130 slots = 240 workgroups of 9 waves)
+ALL_KEYS_SHAPES = {
+    "w4": (32, 8, 2, 40, [514, 300, 70, 40]),
+    "w9": (64, 32, 8, 128, [514, 331]),
+}
+
+
+@pytest.mark.parametrize("shape", list(ALL_KEYS_SHAPES))
+@pytest.mark.parametrize("case", ["plain", "ties", "near", "crowd"])
+def test_decode_all_keys_selection(gpu, case, shape):
+    """Decode with at most 512 candidate blocks: every wave of the attention
+    workgroup holds all candidates and selects with one workgroup barrier.
+    Sequences of 512, 329, 67 (and 38, fewer than top_k: every block)
+    candidates; ordinary scores, all-tied and duplicated blocks, near-equal
+    scores, and a crowd of near-equal scores under a few large ones (the
+    K-th key's value bin then holds more than 64 keys, so a second pass bins
+    by key bits).  Indices (written by the decode itself) bit-exact against
+    the oracle, outputs within the tolerance, decode == select + attend."""
+    import torch
+    Tb = 64
+    B, Hq, Hkv, K, nblk = ALL_KEYS_SHAPES[shape]
+    lens = [Tb * n - (3 if i % 2 else 0) for i, n in enumerate(nblk)][:B]
+    w = make_workload(5600 + len(case) + Hkv, B=len(lens), Hq=Hq, Hkv=Hkv, T=max(lens), Tb=Tb, dtype="bf16",
+                      top_k=K, ns=1, nr=1, lens=lens, salient_frac=0.01 if case == "plain" else 0.0)
+    rng = np.random.default_rng(len(case) + Hkv)
+    for b in range(w.B):
+        nbf = lens[b] // Tb
+        for h in range(w.Hkv):
+            if case == "ties":
+                if b == 0:
+                    blk = w.keys[b][h][:Tb].copy()
+                    for j in range(nbf):
+                        w.keys[b][h][j * Tb:(j + 1) * Tb] = blk
+                elif nbf > 20:
+                    for src in rng.choice(nbf - 10, 4, replace=False) + 5:
+                        for dst in rng.choice(nbf - 10, min(25, nbf - 10), replace=False) + 5:
+                            w.keys[b][h][dst * Tb:(dst + 1) * Tb] = w.keys[b][h][src * Tb:(src + 1) * Tb]
+            elif case in ("near", "crowd"):
+                base = rng.standard_normal(128)
+                noise = rng.standard_normal((w.keys[b][h].shape[0], 128)) * (1e-3 if case == "near" else 2e-4)
+                rows = base[None, :] + noise
+                if case == "crowd" and nbf > 12:
+                    for j in rng.choice(nbf - 4, 3, replace=False) + 1:
+                        rows[j * Tb:(j + 1) * Tb] *= 6.0
+                w.keys[b][h][:] = O.from_f32(rows.astype(np.float32), w.dtype)
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    q = to_dev(w.q[:, :, None, :], w.dtype, gpu)
+    idx_ref, out_ref = oracle_decode(w)
+    idx = torch.full((w.B, w.Hkv, idx_ref.shape[2]), -7, dtype=torch.int32, device=gpu)
+    out = cache.decode(q, w.scale, idx_out=idx)
+    sel = cache.selectBlocks(q)
+    out2 = cache.attend(q, sel, w.scale)
+    torch.cuda.synchronize()
+    got = idx.cpu().numpy()
+    bad = np.argwhere(got != idx_ref)
+    assert bad.size == 0, f"selected blocks differ at {bad[:5]}"
+    assert np.array_equal(sel.cpu().numpy(), idx_ref)
+    a = from_dev(out).reshape(w.B, w.Hq, w.D)
+    assert np.array_equal(a, from_dev(out2).reshape(w.B, w.Hq, w.D)), "decode != select + attend"
+    err = output_error(O.to_f32(a, w.dtype).astype(np.float64), out_ref, w.dtype)
+    assert err <= TOL, f"output error {err:.3g}"
+    if case == "ties":
+        assert list(got[0, 0][:K + 1]) == list(range(K + 1))
+    log(f"[all-keys select] {case} {shape} err={err:.3g}")
