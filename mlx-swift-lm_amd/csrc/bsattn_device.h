@@ -729,22 +729,23 @@ __device__ __forceinline__ void wg_topk(const WgCandT<NK>& wc, int c0, int nc, i
 // The attention workgroup's top-K where each wave needs only its own slot's
 // block.  The candidates spread over the W waves as for wg_topk (slot k of
 // wave w, lane l holds candidate c0 + 64 g + l, group g = W k + w), and the
-// selection is the same (K largest keys, ties to the lower index), with four
+// selection is the same (K largest keys, ties to the lower index), with three
 // workgroup barriers where wg_topk and the read of its output take seven:
 //  1. the waves' key bounds, the histogram cleared behind the same barrier;
 //  2. the histogram fill;
-//  3. the keys of the bin that holds the K-th (no barrier after: the small
-//     set is not written again);
-//  4. every group's masks of keys above and at the K-th key, and every
-//     candidate's page at a fixed position.
-// Each wave then counts the groups' taken blocks (ties to the lowest
-// indices), finds the group and lane of its rank-th selected block, and
-// reads its page.  A K-th bin of more than 64 keys takes another histogram
-// pass (two barriers more).
+//  3. once the bin that holds the K-th key is known: every group's masks of
+//     keys above that bin and in it, every candidate's page at a fixed
+//     position and, when the bin holds more keys than are still needed and
+//     they need not be equal, the bin's keys with their candidate offsets.
+// Each wave then finds, per group, its taken blocks (the bin's keys by rank,
+// key descending and index ascending; equal keys by index), counts them,
+// finds the group and lane of its rank-th selected block, and reads its
+// page.  A K-th bin of more than 64 keys takes another histogram pass (two
+// barriers more).
 // ---------------------------------------------------------------------------
 template <int W>
 constexpr int slot_scratch_words() {
-  return kWaveBins + 64 + 4 + 2 * 16 + 4 * 64 + 64 * W * attend_keys<W>();
+  return kWaveBins + 2 * 64 + 4 + 2 * 16 + 4 * 64 + 64 * W * attend_keys<W>();
 }
 
 template <int S, int W, int NK>
@@ -754,13 +755,14 @@ __device__ __forceinline__ void wg_topk_slot_s(const WgCandT<NK>& wc, int c0, in
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   uint32_t* hist = ws;
-  uint32_t* small = ws + kWaveBins;
-  uint32_t* small_n = small + 64;
+  uint32_t* small = ws + kWaveBins;  // the K-th bin's keys
+  int* small_at = (int*)(small + 64);  // their offsets 64 g + l from c0
+  uint32_t* small_n = (uint32_t*)(small_at + 64);
   uint32_t* xlo = small_n + 4;
   uint32_t* xhi = xlo + 16;
   uint64_t* gmask = (uint64_t*)(xhi + 16);
-  uint64_t* emask = gmask + 64;
-  int* gpage = (int*)(emask + 64);
+  uint64_t* bmask = gmask + 64;
+  int* gpage = (int*)(bmask + 64);
   uint32_t key[S];
   bool real[S];
 #pragma unroll
@@ -792,13 +794,20 @@ __device__ __forceinline__ void wg_topk_slot_s(const WgCandT<NK>& wc, int c0, in
     lo = min(lo, xlo[w]);
     hi = max(hi, xhi[w]);
   }
-  int need = K;
-  bool by_value = true;
-  uint32_t tau;
+  // need: the keys still to take from the current range [lo, hi] (every key
+  // above it is taken); the loop ends with the bin b_star that holds the
+  // need-th largest of them, bk the keys' bins (-1 outside the range) and
+  // by_rank set when that bin's keys must be ranked (cnt of them, more than
+  // need, not known to be equal)
+  int need = K, cnt = 0, b_star = 0;
+  int bk[S];
+  bool by_value = true, by_rank = false;
 #pragma unroll 1
   while (true) {
-    if (lo == hi) {
-      tau = lo;
+    if (lo == hi) {  // every key in the range is equal
+#pragma unroll
+      for (int k = 0; k < S; ++k) bk[k] = real[k] && key[k] == lo ? 0 : -1;
+      b_star = 0;
       break;
     }
     const float vlo = key_value(lo), span = key_value(hi) - vlo;
@@ -810,59 +819,18 @@ __device__ __forceinline__ void wg_topk_slot_s(const WgCandT<NK>& wc, int c0, in
       return use_v ? min(kWaveBins - 1, (int)((key_value(k) - vlo) * scale)) : (int)((k - lo) >> sh);
     };
     // 2. the histogram
-    int bk[S];  // each key's bin in this pass, -1 outside the range
 #pragma unroll
     for (int k = 0; k < S; ++k) {
       bk[k] = real[k] && key[k] >= lo && key[k] <= hi ? bin(key[k]) : -1;
       if (bk[k] >= 0) atomicAdd(&hist[bk[k]], 1u);
     }
     __syncthreads();
-    int b_star, abv, cnt;
+    int abv;
     find_kth_bin(hist, need, b_star, abv, cnt);
     need -= abv;
-    if (!use_v && sh == 0) {  // one-value bin
-      tau = lo + (uint32_t)b_star;
-      break;
-    }
+    if (!use_v && sh == 0) break;  // one-value bin
     if (cnt <= 64) {
-      // 3. the bin's keys from every wave, in any order
-      int mine_n = 0;
-      uint64_t m[S];
-#pragma unroll
-      for (int k = 0; k < S; ++k) {
-        m[k] = __ballot(bk[k] == b_star);
-        mine_n += __popcll(m[k]);
-      }
-      uint32_t base = 0u;
-      if (lane == 0 && mine_n > 0) base = atomicAdd(small_n, (uint32_t)mine_n);
-      base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
-#pragma unroll
-      for (int k = 0; k < S; ++k) {
-        if ((m[k] >> lane) & 1ull) small[base + __popcll(m[k] & below)] = key[k];
-        base += __popcll(m[k]);
-      }
-      __syncthreads();
-      const bool valid = lane < cnt;
-      const uint32_t x = valid ? small[lane] : 0u;
-      if (cnt <= 16) {
-        int gt = 0, ge = 0;
-        for (int jj = 0; jj < cnt; ++jj) {
-          const uint32_t xj = (uint32_t)__builtin_amdgcn_readlane((int)x, jj);
-          gt += xj > x;
-          ge += xj >= x;
-        }
-        const int s2 = __ffsll((unsigned long long)__ballot(valid && gt < need && need <= ge)) - 1;
-        tau = (uint32_t)__builtin_amdgcn_readlane((int)x, s2);
-      } else {
-        const uint32_t mn = wave_min_u32(valid ? x : 0xFFFFFFFFu), mx = wave_max_u32(x);
-        const uint32_t off = x - mn;
-        uint32_t t = 0u;
-        for (int bit = mx == mn ? -1 : 31 - __clz(mx - mn); bit >= 0; --bit) {
-          const uint32_t cand = t | (1u << bit);
-          if (__popcll(__ballot(valid && off >= cand)) >= need) t = cand;
-        }
-        tau = mn + t;
-      }
+      by_rank = cnt > need;
       break;
     }
     // another pass over the K-th bin: its bounds, then a cleared histogram
@@ -899,22 +867,62 @@ __device__ __forceinline__ void wg_topk_slot_s(const WgCandT<NK>& wc, int c0, in
     by_value = false;
     __syncthreads();  // cleared; every wave has read the bounds
   }
-  // 4. the groups' masks of keys above and at tau, and every candidate's page
+  // 3. the groups' masks of keys above the K-th bin and in it, every
+  // candidate's page, and the bin's keys when they are ranked
+  uint64_t inm[S];
+  int mine_n = 0;
 #pragma unroll
   for (int k = 0; k < S; ++k) {
     const int g = W * k + wave;
-    const uint64_t gtm = __ballot(real[k] && key[k] > tau);
-    const uint64_t eqm = __ballot(real[k] && key[k] == tau);
+    const uint64_t gtm = __ballot(real[k] && (key[k] > hi || bk[k] > b_star));
+    inm[k] = __ballot(bk[k] == b_star);
+    mine_n += __popcll(inm[k]);
     if (lane == 0) {
       gmask[g] = gtm;
-      emask[g] = eqm;
+      bmask[g] = inm[k];
     }
     gpage[64 * g + lane] = wc.page[k];
   }
+  if (by_rank) {
+    uint32_t base = 0u;
+    if (lane == 0 && mine_n > 0) base = atomicAdd(small_n, (uint32_t)mine_n);
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+      if ((inm[k] >> lane) & 1ull) {
+        const uint32_t at = base + __popcll(inm[k] & below);
+        small[at] = key[k];
+        small_at[at] = 64 * (W * k + wave) + lane;
+      }
+      base += __popcll(inm[k]);
+    }
+  }
   __syncthreads();
-  // lane g: group g's counts; ties go to the lowest indices
+  // lane g: group g's masks; the K-th bin's keys are taken by index (gm
+  // above, em at the bin) or, when ranked, moved into gm by rank
   constexpr int NG = S * W;
-  const uint64_t gm = lane < NG ? gmask[lane] : 0ull, em = lane < NG ? emask[lane] : 0ull;
+  uint64_t gm = lane < NG ? gmask[lane] : 0ull, em = lane < NG ? bmask[lane] : 0ull;
+  if (by_rank) {
+    const bool valid = lane < cnt;
+    const uint32_t x = valid ? small[lane] : 0u;
+    const int xa = valid ? small_at[lane] : 0;
+    int r = 0;
+    for (int jj = 0; jj < cnt; ++jj) {
+      const uint32_t xj = (uint32_t)__builtin_amdgcn_readlane((int)x, jj);
+      const int aj = __builtin_amdgcn_readlane(xa, jj);
+      r += (xj > x || (xj == x && aj < xa)) ? 1 : 0;
+    }
+    uint64_t tk = __ballot(valid && r < need);
+    uint64_t bits = 0ull;
+    while (tk != 0ull) {
+      const int jj = __ffsll((unsigned long long)tk) - 1;
+      tk &= tk - 1ull;
+      const int aj = __builtin_amdgcn_readlane(xa, jj);
+      if ((aj >> 6) == lane) bits |= 1ull << (aj & 63);
+    }
+    gm |= bits;
+    em = 0ull;
+  }
   const int ng = __popcll(gm), ne = __popcll(em);
   const int gt_total = wave_sum_i32(ng);
   const int krem = K - gt_total;
@@ -923,7 +931,7 @@ __device__ __forceinline__ void wg_topk_slot_s(const WgCandT<NK>& wc, int c0, in
   const int taken = ng + t_eq;
   const int t_excl = wave_scan_incl(taken) - taken;
   auto group_take = [&](uint64_t gms, uint64_t ems, int tq) -> uint64_t {
-    // taken lanes of a group: above tau, or the tq lowest at tau
+    // taken lanes of a group: above, or the tq lowest of the K-th bin's
     const bool eb = (ems >> lane) & 1ull;
     const bool take = ((gms >> lane) & 1ull) || (eb && __popcll(ems & below) < tq);
     return __ballot(take);
