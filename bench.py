@@ -60,6 +60,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from dataclasses import dataclass
@@ -112,6 +113,30 @@ CONFIGS = {
                  8, 64, 4, 262144, 32, "f16", 8, 128, 1, 4, 0.0, 12,
                  "k_attend_q_b8_ctx256k_int8_traffic.md"),
 }
+
+
+def profiled_means(layers, kinds, step, reps, torch):
+    """Per repetition of step(), each kernel kind's mean dispatch time (us)
+    from the library's event timing; lists in repetition order."""
+    for cache, _ in layers:
+        cache.profile(True)
+    last = {name: (0.0, 0) for name in kinds}
+    out = {name: [] for name in kinds}
+    for _ in range(reps):
+        step()
+        torch.cuda.synchronize()
+        for name, kind in kinds.items():
+            tot, n = 0.0, 0
+            for cache, _ in layers:
+                ms, c = cache.profileRead(kind)
+                tot, n = tot + ms, n + c
+            dt, dn = tot - last[name][0], n - last[name][1]
+            last[name] = (tot, n)
+            if dn:
+                out[name].append(dt * 1e3 / dn)
+    for cache, _ in layers:
+        cache.profile(False)
+    return out
 
 
 def log(msg):
@@ -446,24 +471,16 @@ def bench_layers(args, cfg: Config, light: bool = False):
     if args.copy_calibration:
         calibration_copy(torch, dev)
 
-    # kernel times of one decode layer-step (eager, profiled)
-    for cache, _ in layers:
-        cache.profile(True)
-    for _ in range(max(3, args.steps // 4)):
-        step()
-    torch.cuda.synchronize()
+    # kernel times of one decode layer-step (eager, profiled): the median over
+    # steps of each step's mean dispatch time (one unprofiled step first)
     kinds = {"score": bsattn._lib.KERNEL_SCORE, "topk": bsattn._lib.KERNEL_TOPK,
              "attend": bsattn._lib.KERNEL_ATTEND, "combine": bsattn._lib.KERNEL_COMBINE}
-    decode_kernels = {}
-    for name, kind in kinds.items():
-        tot, n = 0.0, 0
-        for cache, _ in layers:
-            ms, c = cache.profileRead(kind)
-            tot, n = tot + ms, n + c
-        if n:
-            decode_kernels[name] = round(tot * 1e3 / n, 3)
-    for cache, _ in layers:
-        cache.profile(False)
+    step()
+    torch.cuda.synchronize()
+    per_step = profiled_means(layers, kinds, step, max(9, args.steps // 2), torch)
+    decode_kernels = {name: round(statistics.median(v), 3) for name, v in per_step.items() if v}
+    log("[bench] decode kernels per step (us): " + "; ".join(
+        f"{name} {min(v):.2f}-{max(v):.2f}" for name, v in per_step.items() if v))
 
     # the given-index gather + attention kernel alone (bsattn_attend on
     # precomputed indices), for comparison with the decode path's kernel.
@@ -475,21 +492,16 @@ def bench_layers(args, cfg: Config, light: bool = False):
     for (cache, q), ii in zip(layers, idx):  # warm
         cache.attend(q, ii, scale)
     torch.cuda.synchronize()
-    for cache, _ in layers:
-        cache.profile(True)
-    reps = max(5, args.steps)
-    for _ in range(reps):
+
+    def given_step():
         for (cache, q), ii in zip(layers, idx):
             cache.attend(q, ii, scale)
-    torch.cuda.synchronize()
-    tot_ms, launches, comb_ms = 0.0, 0, 0.0
-    for cache, _ in layers:
-        ms, n = cache.profileRead(bsattn._lib.KERNEL_ATTEND)
-        cms, _ = cache.profileRead(bsattn._lib.KERNEL_COMBINE)
-        tot_ms, launches, comb_ms = tot_ms + ms, launches + n, comb_ms + cms
-        cache.profile(False)
-    given_us = tot_ms * 1e3 / launches
-    given_combine_us = comb_ms * 1e3 / launches
+
+    per_rep = profiled_means(layers, {"attend": bsattn._lib.KERNEL_ATTEND,
+                                      "combine": bsattn._lib.KERNEL_COMBINE},
+                             given_step, max(9, args.steps), torch)
+    given_us = statistics.median(per_rep["attend"])
+    given_combine_us = statistics.median(per_rep["combine"]) if per_rep["combine"] else 0.0
     attn_bytes, summ_bytes = algorithmic_bytes(cfg, nsel)
     given_achieved = attn_bytes / (given_us * 1e-6) / 1e9
     # roofline: the gather + attention kernel the timed decode step runs
