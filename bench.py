@@ -180,30 +180,98 @@ def calibration_copy(torch, dev):
     del src, dst
 
 
-def make_layer(cfg: Config, layer, dev, torch, bsattn):
-    g = torch.Generator(device=dev)
-    seeds = {"c2": 1001, "c3": 1003, "c5": 1005}
-    g.manual_seed(seeds[cfg.key] * 1000 + layer)
+CFG_SEED = {"c2": 1002, "c3": 1003, "c5": 1005}  # 1000 + the configuration's number
+
+
+def query_inputs(cfg: Config, seed: int, torch, dev):
+    """q [B, Hq, 1, D] of the workload with this seed."""
+    q = round16(counter_normal(seed, S_Q, 0, cfg.B * cfg.HQ * D, torch, dev), cfg.dtype, torch)
+    return q.view(torch_dtype(torch, cfg)).reshape(cfg.B, cfg.HQ, 1, D)
+
+
+def sequence_inputs(cfg: Config, seed: int, b: int, torch, dev, tokens=None):
+    """Keys and values [Hkv, tokens, D] of sequence b (its first `tokens`
+    tokens; all of them by default) of the workload with this seed."""
+    import numpy as np
+    T, n = cfg.T, cfg.T if tokens is None else tokens
+    dt = torch_dtype(torch, cfg)
+    if n == T:  # the heads' streams are consecutive
+        kx = counter_normal(seed, S_K, b * cfg.HKV * T * D, cfg.HKV * T * D, torch, dev)
+        vx = counter_normal(seed, S_V, b * cfg.HKV * T * D, cfg.HKV * T * D, torch, dev)
+    else:
+        kx = torch.cat([counter_normal(seed, S_K, (b * cfg.HKV + h) * T * D, n * D, torch, dev)
+                        for h in range(cfg.HKV)])
+        vx = torch.cat([counter_normal(seed, S_V, (b * cfg.HKV + h) * T * D, n * D, torch, dev)
+                        for h in range(cfg.HKV)])
+    kx = kx.view(cfg.HKV, n, D)
+    n_sal = int(round(cfg.salient * T))
+    if n_sal:
+        pos = choose_positions(seed, S_SALIENT, [b * cfg.HKV + h for h in range(cfg.HKV)], T, n_sal)
+        mult = torch.ones(cfg.HKV, T, dtype=torch.float64, device=dev)
+        mult.scatter_(1, torch.from_numpy(pos).to(dev), 8.0)
+        kx = kx * mult[:, :n, None]
+        del mult
+    k = round16(kx, cfg.dtype, torch).view(dt)
+    del kx
+    v = round16(vx, cfg.dtype, torch).view(dt).view(cfg.HKV, n, D)
+    return k, v
+
+
+def make_layer(cfg: Config, layer, dev, torch, bsattn, digest=None):
+    """Layer `layer`'s cache and q from the counter-based generator with seed
+    CFG_SEED + 1000 * layer (layer 0 is the configuration's committed
+    workload).  digest: a dict that receives the SHA-256 of the inputs over
+    the lengths (int32), q, then each (sequence, kv head)'s keys and values
+    as 16-bit words ("prefix": their first 256 tokens; "full": all of them
+    when digest["full"] is set), the order of tests/golden/input_digests.json."""
+    import numpy as np
+    seed = CFG_SEED[cfg.key] + 1000 * layer
     dt = torch_dtype(torch, cfg)
     cache = bsattn.BlockSparseKVCache(max_seqs=cfg.B, num_q_heads=cfg.HQ, num_kv_heads=cfg.HKV,
                                       head_dim=D, block_size=cfg.TB, dtype=dt, kv_bits=cfg.bits,
                                       top_k=cfg.top_k, sink_blocks=cfg.ns, recent_blocks=cfg.nr,
                                       max_blocks_per_seq=cfg.T // cfg.TB + 2, device=dev.index)
-    n_sal = int(round(cfg.salient * cfg.T))
+    q = query_inputs(cfg, seed, torch, dev)
+    hashes = None
+    if digest is not None:
+        import hashlib
+        hashes = {"prefix": hashlib.sha256()}
+        if digest.get("full"):
+            hashes["full"] = hashlib.sha256()
+        head = np.full(cfg.B, cfg.T, "<i4").tobytes() + host16(q, torch, np).astype("<u2").tobytes()
+        for hh in hashes.values():
+            hh.update(head)
     for b in range(cfg.B):  # one sequence at a time keeps the temporaries small
-        if n_sal:
-            mult = torch.ones(cfg.HKV, cfg.T, device=dev)
-            pos = torch.rand(cfg.HKV, cfg.T, device=dev, generator=g).argsort(dim=1)[:, :n_sal]
-            mult.scatter_(1, pos, 8.0)
-            k = (torch.randn(cfg.HKV, cfg.T, D, device=dev, generator=g) * mult[..., None]).to(dt)
-            del mult, pos
-        else:
-            k = torch.randn(cfg.HKV, cfg.T, D, device=dev, generator=g).to(dt)
-        v = torch.randn(cfg.HKV, cfg.T, D, device=dev, generator=g).to(dt)
+        k, v = sequence_inputs(cfg, seed, b, torch, dev)
+        if hashes is not None:
+            kh, vh = host16(k, torch, np), host16(v, torch, np)
+            for h in range(cfg.HKV):
+                hashes["prefix"].update(kh[h, :256].astype("<u2").tobytes())
+                hashes["prefix"].update(vh[h, :256].astype("<u2").tobytes())
+                if "full" in hashes:
+                    hashes["full"].update(kh[h].astype("<u2").tobytes())
+                    hashes["full"].update(vh[h].astype("<u2").tobytes())
+            del kh, vh
         cache.append(k[None].contiguous(), v[None].contiguous(), seq_ids=[b])
         del k, v
-    q = torch.randn(cfg.B, cfg.HQ, 1, D, device=dev, generator=g).to(dt)
+    if hashes is not None:
+        for name, hh in hashes.items():
+            digest[name] = hh.hexdigest()
     return cache, q
+
+
+def input_check(cfg: Config, digest):
+    """Layer 0's input digests against the committed ones of the same
+    workload -> {"layer0_sha256": ..., "matches_committed": bool, ...}."""
+    name = {"c2": "C2", "c3": "C3", "c5": "C5"}[cfg.key]
+    with open(os.path.join(ROOT, "tests", "golden", "input_digests.json")) as f:
+        ref = json.load(f)[name]
+    out = {"workload": name, "prefix_tokens": 256, "prefix_sha256": digest["prefix"],
+           "prefix_matches_committed": digest["prefix"] == ref["prefix_sha256"]}
+    if isinstance(digest.get("full"), str):
+        out["layer0_sha256"] = digest["full"]
+        out["full_matches_committed"] = digest["full"] == ref["sha256"]
+    return out
 
 
 def algorithmic_bytes(cfg: Config, nsel):
@@ -412,10 +480,14 @@ def bench_layers(args, cfg: Config, light: bool = False):
     torch.cuda.set_device(dev)
     L = args.layers or cfg.layers
     t0 = time.time()
-    layers = [make_layer(cfg, i, dev, torch, bsattn) for i in range(L)]
+    # layer 0's inputs are checked against the committed digests (in full for
+    # the headline workload, the 256-token prefixes for the others)
+    digest = {"full": cfg.key == "c2" and not light}
+    layers = [make_layer(cfg, i, dev, torch, bsattn, digest if i == 0 else None) for i in range(L)]
     torch.cuda.synchronize()
+    inputs = input_check(cfg, digest)
     log(f"[bench] {cfg.key}: built {L} layer caches in {time.time() - t0:.1f}s "
-        f"({layers[0][0].poolBytes / 2**30:.2f} GiB each)")
+        f"({layers[0][0].poolBytes / 2**30:.2f} GiB each); layer 0 inputs: {inputs}")
     scale = 1.0 / math.sqrt(D)
 
     def step():
@@ -561,9 +633,11 @@ def bench_layers(args, cfg: Config, light: bool = False):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": cfg.dtype if cfg.bits == 0 else f"{cfg.dtype} (int{cfg.bits} KV)",
-        "data": "synthetic: torch RNG on device, K/V ~ N(0,1)"
+        "data": "synthetic: counter-based splitmix64 + Box-Muller N(0,1) K/V/q, seed "
+                f"{CFG_SEED[cfg.key]} + 1000 x layer"
                 + (f", {cfg.salient:.0%} of key positions x8" if cfg.salient else "")
-                + ", random-init q",
+                + "; layer 0 = the committed workload digest",
+        "inputs": inputs,
         "config": {"workload": f"block-sparse decode layer-step x{L} distinct layer caches",
                    "batch": cfg.B, "q_heads": cfg.HQ, "kv_heads": cfg.HKV, "head_dim": D,
                    "context": cfg.T, "block_size": cfg.TB, "kv": kv, "top_k": cfg.top_k,
@@ -628,7 +702,7 @@ def other_summary(r: dict, per: str) -> dict:
                      "attend_bytes_per_launch": ro["bytes_per_launch"], "attend_achieved_GBps": ro["achieved"],
                      "attend_frac": ro["frac"], "traffic": ro["traffic"], "traffic_source": ro["traffic_source"],
                      "given_index": ro["given_index"], "decode_kernels_us": r["decode_kernels_us"],
-                     "layer_step_GBps": r["layer_step_GBps"]})
+                     "layer_step_GBps": r["layer_step_GBps"], "data": r["data"], "inputs": r["inputs"]})
     else:
         keep.update({k: r[k] for k in ("kernels_us_per_step", "kernel_us_per_step_total",
                                        "kernel_GBps", "kernel_frac", "bytes_per_step",
@@ -636,14 +710,112 @@ def other_summary(r: dict, per: str) -> dict:
     return keep
 
 
+def _mix(x: int) -> int:
+    """splitmix64 finaliser on a Python int (mod 2^64)."""
+    z = (x + 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & 0xFFFFFFFFFFFFFFFF
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & 0xFFFFFFFFFFFFFFFF
+    return z ^ (z >> 31)
+
+
 def _hash3(seed: int, stream: int, index: int) -> int:
     """splitmix64 finaliser chained over (seed, stream, index)."""
-    def mix(x):
-        z = (x + 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF
-        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & 0xFFFFFFFFFFFFFFFF
-        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & 0xFFFFFFFFFFFFFFFF
-        return z ^ (z >> 31)
-    return mix((mix((mix(seed) + stream) & 0xFFFFFFFFFFFFFFFF) + index) & 0xFFFFFFFFFFFFFFFF)
+    return _mix((_mix((_mix(seed) + stream) & 0xFFFFFFFFFFFFFFFF) + index) & 0xFFFFFFFFFFFFFFFF)
+
+
+# ---------------------------------------------------------------------------
+# The benchmark inputs: the counter-based generator of the decode workloads
+# (element i of stream s under seed S is normal(S, s, i); keys of sequence b,
+# kv head h, token t, dim d are element ((b Hkv + h) T + t) D + d of stream 1,
+# values the same of stream 2, q element (b Hq + hq) D + d of stream 0; a
+# salient fraction of each (b, h)'s token positions, drawn on stream 3, have
+# their keys scaled by 8 before rounding), computed with torch on the device.
+# ---------------------------------------------------------------------------
+S_Q, S_K, S_V, S_SALIENT = 0, 1, 2, 3
+
+
+def _s64(c: int) -> int:
+    """A 64-bit pattern as the signed value torch's int64 holds."""
+    return c - (1 << 64) if c >= 1 << 63 else c
+
+
+def _mix_t(z):
+    """splitmix64 finaliser on an int64 tensor: products wrap mod 2^64, and the
+    right shifts are made logical by masking."""
+    z = z + _s64(0x9E3779B97F4A7C15)
+    z = (z ^ ((z >> 30) & ((1 << 34) - 1))) * _s64(0xBF58476D1CE4E5B9)
+    z = (z ^ ((z >> 27) & ((1 << 37) - 1))) * _s64(0x94D049BB133111EB)
+    return z ^ ((z >> 31) & ((1 << 33) - 1))
+
+
+def counter_normal(seed: int, stream: int, start: int, n: int, torch, dev):
+    """normal(seed, stream, start + i), i < n (start and n even), float64:
+    Box-Muller in double over the hash pair (2p, 2p + 1) of index pair p,
+    u1 = ((a >> 11) + 1) 2^-53 in (0, 1], u2 = (b >> 11) 2^-53; even
+    indices take r cos(2 pi u2), odd ones r sin(2 pi u2)."""
+    assert start % 2 == 0 and n % 2 == 0
+    p2 = 2 * torch.arange(start // 2, (start + n) // 2, device=dev, dtype=torch.int64)
+    base = _s64(_mix((_mix(seed) + stream) & 0xFFFFFFFFFFFFFFFF))
+    a = _mix_t(p2 + base)
+    b = _mix_t(p2 + (base + 1 if base + 1 < 1 << 63 else base + 1 - (1 << 64)))
+    del p2
+    u1 = (((a >> 11) & ((1 << 53) - 1)) + 1).double() * 2.0 ** -53
+    u2 = ((b >> 11) & ((1 << 53) - 1)).double() * 2.0 ** -53
+    del a, b
+    r = torch.sqrt(-2.0 * torch.log(u1))
+    t = 6.283185307179586476925286766559 * u2
+    return torch.stack((r * torch.cos(t), r * torch.sin(t)), dim=-1).reshape(-1)
+
+
+def round16(x, dtype: str, torch):
+    """float64 tensor -> bf16 / fp16 storage words (int16), rounded to nearest
+    even straight from the double (no float32 step, which would round twice):
+    the exponent and top mantissa bits of the double's pattern plus the round
+    bit, rebiased; results below the target's normal range are |x| scaled by
+    the smallest subnormal, rounded to an integer; beyond the largest finite,
+    infinity."""
+    mb, eb = (7, 127) if dtype == "bf16" else (10, 15)
+    sh = 52 - mb
+    bits = x.view(torch.int64)
+    sign = (bits < 0).to(torch.int64) << 15
+    mag = bits & 0x7FFFFFFFFFFFFFFF
+    v = mag >> sh
+    rem = mag & ((1 << sh) - 1)
+    half = 1 << (sh - 1)
+    up = (rem > half) | ((rem == half) & ((v & 1) == 1))
+    v = (v + up.to(torch.int64) - ((1023 - eb) << mb)).clamp(max=0xFF << mb if dtype == "bf16" else 0x1F << mb)
+    sub = torch.round(x.abs() * 2.0 ** (eb - 1 + mb)).to(torch.int64)
+    v = torch.where((mag >> 52) < 1023 - eb + 1, sub, v)
+    return (v | sign).to(torch.int16)
+
+
+def choose_positions(seed: int, stream: int, keys, n: int, count: int):
+    """For each key, the first `count` entries of a Fisher-Yates shuffle of
+    range(n) whose step i swaps entry i with entry i + hash3(seed, stream,
+    (key << 32) | i) mod (n - i) -> int64 array [len(keys), count]."""
+    import numpy as np
+    c = [np.uint64(x) for x in (0x9E3779B97F4A7C15, 0xBF58476D1CE4E5B9, 0x94D049BB133111EB)]
+
+    def mix_np(z):
+        z = z + c[0]
+        z = (z ^ (z >> np.uint64(30))) * c[1]
+        z = (z ^ (z >> np.uint64(27))) * c[2]
+        return z ^ (z >> np.uint64(31))
+
+    base = np.uint64(_mix((_mix(seed) + stream) & 0xFFFFFFFFFFFFFFFF))
+    kk = np.asarray(keys, np.uint64) << np.uint64(32)
+    rows = np.arange(len(keys))
+    perm = np.tile(np.arange(n, dtype=np.int64), (len(keys), 1))
+    out = np.empty((len(keys), count), np.int64)
+    with np.errstate(over="ignore"):
+        for i in range(min(count, n)):
+            h = mix_np(base + (kk | np.uint64(i)))
+            j = i + (h % np.uint64(n - i)).astype(np.int64)
+            t = perm[rows, i].copy()
+            perm[rows, i] = perm[rows, j]
+            perm[rows, j] = t
+            out[:, i] = perm[rows, i]
+    return out
 
 
 def bench_loop(args, light: bool = False):

@@ -86,7 +86,7 @@ float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
 static uint16_t f64_to_16(double x, int dtype) {
   if (isnan(x)) return dtype == ORC_F16 ? 0x7E00 : 0x7FC0;
   /* overflow threshold = largest finite + half an ulp (ties go to inf) */
-  double lim = dtype == ORC_F16 ? 65520.0 : 0x1.FF8p+127;
+  double lim = dtype == ORC_F16 ? 65520.0 : 0x1.FFp+127;
   if (fabs(x) >= lim) return (uint16_t)((x < 0 ? 0x8000 : 0) | (dtype == ORC_F16 ? 0x7C00 : 0x7F80));
   if (fabs(x) > (dtype == ORC_F16 ? 65504.0 : 0x1.FEp+127))
     return (uint16_t)((x < 0 ? 0x8000 : 0) | (dtype == ORC_F16 ? 0x7BFF : 0x7F7F));

@@ -72,6 +72,23 @@ def test_f64_to_16_single_rounding():
         assert O.to_f32(np.array([L.orc_f64_to_bf16(x)], np.uint16), "bf16")[0] == _rne_sig(x, 8)
 
 
+def test_f64_to_16_overflow_boundary():
+    """Largest finite + half an ulp (65504 + 16 for fp16, 0x1.FEp+127 +
+    2^119 for bf16) is a tie whose even neighbour is the next power of two,
+    i.e. infinity; anything below rounds to the largest finite."""
+    L = O.lib()
+    for conv, mx, half, inf in ((L.orc_f64_to_f16, 65504.0, 16.0, 0x7C00),
+                                (L.orc_f64_to_bf16, float.fromhex("0x1.FEp+127"), 2.0 ** 119, 0x7F80)):
+        big = inf - 1
+        for sgn in (1.0, -1.0):
+            s = 0x8000 if sgn < 0 else 0
+            assert conv(sgn * mx) == s | big
+            assert conv(sgn * (mx + half - half * 2 ** -40)) == s | big
+            assert conv(sgn * (mx + half)) == s | inf
+            assert conv(sgn * (mx + half * 1.5)) == s | inf
+            assert conv(sgn * mx * 4) == s | inf
+
+
 # -------------------------------------------------------------------- rng --
 
 def test_splitmix64_published_vectors():
