@@ -573,6 +573,8 @@ def bench_layers(args, cfg: Config, light: bool = False):
                                       "combine": bsattn._lib.KERNEL_COMBINE},
                              given_step, max(9, args.steps), torch)
     given_us = statistics.median(per_rep["attend"])
+    log(f"[bench] given-index kernels per step (us): attend {min(per_rep['attend']):.2f}-"
+        f"{max(per_rep['attend']):.2f}")
     given_combine_us = statistics.median(per_rep["combine"]) if per_rep["combine"] else 0.0
     attn_bytes, summ_bytes = algorithmic_bytes(cfg, nsel)
     given_achieved = attn_bytes / (given_us * 1e-6) / 1e9

@@ -923,11 +923,21 @@ __device__ __forceinline__ void wg_topk_slot_s(const WgCandT<NK>& wc, int c0, in
     gm |= bits;
     em = 0ull;
   }
-  const int ng = __popcll(gm), ne = __popcll(em);
-  const int gt_total = wave_sum_i32(ng);
-  const int krem = K - gt_total;
-  const int e_excl = wave_scan_incl(ne) - ne;
-  const int t_eq = min(max(krem - e_excl, 0), ne);
+  // equal keys at the K-th bin are split by index only when the bin holds
+  // more of them than are needed; otherwise every key of the bin is taken
+  const bool split_eq = !by_rank && cnt != need;
+  if (!split_eq) {
+    gm |= em;
+    em = 0ull;
+  }
+  const int ng = __popcll(gm);
+  int t_eq = 0;
+  if (split_eq) {
+    const int ne = __popcll(em);
+    const int krem = K - wave_sum_i32(ng);
+    const int e_excl = wave_scan_incl(ne) - ne;
+    t_eq = min(max(krem - e_excl, 0), ne);
+  }
   const int taken = ng + t_eq;
   const int t_excl = wave_scan_incl(taken) - taken;
   auto group_take = [&](uint64_t gms, uint64_t ems, int tq) -> uint64_t {
@@ -1212,41 +1222,65 @@ __device__ __forceinline__ void attend_merge(const Geometry& geo, const SeqBatch
                                              uint16_t* __restrict__ out,
                                              float* __restrict__ partials) {
   // per head: the maximum M over the waves, each wave's weight exp2(m_w - M)
-  // and the merged sum L, once (thread h < G), for all 128 dims
-  __shared__ float s_f[W][16], s_ML[2][16];
-  if (threadIdx.x < G) {
-    const int head = threadIdx.x;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][head]);
-    float L = 0.f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const float mw = s_m[w][head];
-      const float f = (M == -INFINITY || mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-      s_f[w][head] = f;
-      L += f * s_l[w][head];
-    }
-    s_ML[0][head] = M;
-    s_ML[1][head] = L;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < G * kHeadDim; e += 64 * W) {
-    const int head = e / kHeadDim, d = e % kHeadDim;
-    const float M = s_ML[0][head], L = s_ML[1][head];
-    float a = 0.f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) a += s_f[w][head] * s_o[w][head][d];
-    const size_t row = (size_t)bi * geo.hq + h * G + head;
+  // and the merged sum L.  With one element per thread every thread computes
+  // them for its own head (the same operations in the same order everywhere,
+  // so no barrier is needed to share them); otherwise once (thread h < G)
+  // behind a barrier.
+  auto emit = [&](int head, int d, float M, float L, float a) {
     if (nsplit == 1) {
       out[q_row(sb, bi, h * G + head) + d] = from_f32<DT>(L > 0.f ? a / L : 0.f);
     } else {
+      const size_t row = (size_t)bi * geo.hq + h * G + head;
       float* pp = partials + (row * nsplit + split) * (kHeadDim + 2);
       pp[d] = a;
       if (d == 0) {
         pp[kHeadDim] = M;
         pp[kHeadDim + 1] = L;
       }
+    }
+  };
+  if constexpr (G * kHeadDim <= 64 * W) {
+    const int e = threadIdx.x;
+    if (e < G * kHeadDim) {
+      const int head = e / kHeadDim, d = e % kHeadDim;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][head]);
+      float L = 0.f, a = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float mw = s_m[w][head];
+        const float f = (M == -INFINITY || mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+        L += f * s_l[w][head];
+        a += f * s_o[w][head][d];
+      }
+      emit(head, d, M, L, a);
+    }
+  } else {
+    __shared__ float s_f[W][16], s_ML[2][16];
+    if (threadIdx.x < G) {
+      const int head = threadIdx.x;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][head]);
+      float L = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float mw = s_m[w][head];
+        const float f = (M == -INFINITY || mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+        s_f[w][head] = f;
+        L += f * s_l[w][head];
+      }
+      s_ML[0][head] = M;
+      s_ML[1][head] = L;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < G * kHeadDim; e += 64 * W) {
+      const int head = e / kHeadDim, d = e % kHeadDim;
+      float a = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) a += s_f[w][head] * s_o[w][head][d];
+      emit(head, d, s_ML[0][head], s_ML[1][head], a);
     }
   }
 }
