@@ -815,13 +815,15 @@ __device__ __forceinline__ void wg_topk_slot_s(const WgCandT<NK>& wc, int c0, in
     // bins need only be monotone in the key: an approximate reciprocal will do
     const float scale = use_v ? (float)(kWaveBins - 1) * __builtin_amdgcn_rcpf(span) : 0.0f;
     const int sh = use_v ? 0 : max(0, 32 - __clz(hi - lo) - 10);
-    auto bin = [&](uint32_t k) -> int {
-      return use_v ? min(kWaveBins - 1, (int)((key_value(k) - vlo) * scale)) : (int)((k - lo) >> sh);
+    // a key in a value range is a finite score (NaN keys sit below every
+    // finite one), so its bin is taken from the score itself
+    auto bin = [&](int k) -> int {
+      return use_v ? min(kWaveBins - 1, (int)((wc.score[k] - vlo) * scale)) : (int)((key[k] - lo) >> sh);
     };
     // 2. the histogram
 #pragma unroll
     for (int k = 0; k < S; ++k) {
-      bk[k] = real[k] && key[k] >= lo && key[k] <= hi ? bin(key[k]) : -1;
+      bk[k] = real[k] && key[k] >= lo && key[k] <= hi ? bin(k) : -1;
       if (bk[k] >= 0) atomicAdd(&hist[bk[k]], 1u);
     }
     __syncthreads();
@@ -881,7 +883,8 @@ __device__ __forceinline__ void wg_topk_slot_s(const WgCandT<NK>& wc, int c0, in
       gmask[g] = gtm;
       bmask[g] = inm[k];
     }
-    gpage[64 * g + lane] = wc.page[k];
+    // only a candidate that can be taken is ever looked up
+    if (((gtm | inm[k]) >> lane) & 1ull) gpage[64 * g + lane] = wc.page[k];
   }
   if (by_rank) {
     uint32_t base = 0u;
