@@ -734,9 +734,10 @@ __device__ __forceinline__ void wg_topk(const WgCandT<NK>& wc, int c0, int nc, i
 //  1. the waves' key bounds, the histogram cleared behind the same barrier;
 //  2. the histogram fill;
 //  3. once the bin that holds the K-th key is known: every group's masks of
-//     keys above that bin and in it, every candidate's page at a fixed
-//     position and, when the bin holds more keys than are still needed and
-//     they need not be equal, the bin's keys with their candidate offsets.
+//     keys above that bin and in it, the page of every candidate that can be
+//     taken (above the bin or in it) at a fixed position and, when the bin
+//     holds more keys than are still needed and they need not be equal, the
+//     bin's keys with their candidate offsets.
 // Each wave then finds, per group, its taken blocks (the bin's keys by rank,
 // key descending and index ascending; equal keys by index), counts them,
 // finds the group and lane of its rank-th selected block, and reads its
