@@ -1082,7 +1082,8 @@ def bench_multi(args, cfg: Config, L: int = 4):
         "value": round(multi_us, 3), "unit": "us/layer-step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(multi_us * NL / 1e3, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": cfg.dtype,
-        "data": "synthetic: torch RNG on device, K/V ~ N(0,1), random-init q",
+        "data": "synthetic: layer caches from the counter-based generator (as the decode benchmark), "
+                "the L query tokens per sequence from torch's device RNG, N(0,1)",
         "config": {"workload": f"decodeMulti x{NL} distinct layer caches", "batch": cfg.B,
                    "q_heads": cfg.HQ, "kv_heads": cfg.HKV, "head_dim": D, "context": cfg.T,
                    "block_size": cfg.TB, "top_k": cfg.top_k, "query_tokens": L},
