@@ -63,7 +63,7 @@ __device__ __forceinline__ float group_score(const float (&qv)[G][8], const u32x
   float best = 0.0f;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float acc = canonical_dot16(qv[g], sv);
+    const float acc = canonical_dot16<DT>(qv[g], sv);
     if (g == 0 || acc > best) best = acc;
   }
   return best;

@@ -196,10 +196,19 @@ __device__ __forceinline__ float row_shl(float x) {
 // (c, c+4), (c, c+8), which lane 0 of the row accumulates through row
 // shifts (fp32 addition is commutative, so the order of each pair does not
 // matter).  Only lane 0 of the row (c == 0) holds the result.
+// fp16 operands (DT 0): a product of two fp16 values has at most 22
+// significant bits and a magnitude in [2^-48, 2^32], so it is exact in fp32,
+// and fma(a, b, acc) = round(a*b + acc) is the rounded sum of the rounded
+// product: one instruction per step, the same bits.  bf16 products can leave
+// fp32's normal range, so they keep the separate multiply.
+template <int DT>
 __device__ __forceinline__ float canonical_dot16(const float* a, const float* b) {
   float acc = __fmul_rn(a[0], b[0]);
 #pragma unroll
-  for (int e = 1; e < 8; ++e) acc = __fadd_rn(acc, __fmul_rn(a[e], b[e]));
+  for (int e = 1; e < 8; ++e) {
+    if constexpr (DT == 0) acc = __builtin_fmaf(a[e], b[e], acc);
+    else acc = __fadd_rn(acc, __fmul_rn(a[e], b[e]));
+  }
   acc = __fadd_rn(acc, row_shl<1>(acc));
   acc = __fadd_rn(acc, row_shl<2>(acc));
   acc = __fadd_rn(acc, row_shl<4>(acc));

@@ -195,7 +195,7 @@ __device__ __forceinline__ void score_body(const Geometry& geo, const SeqBatch& 
       float best = 0.0f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float acc = canonical_dot16(qv[g], sv);
+        const float acc = canonical_dot16<DT>(qv[g], sv);
         if (g == 0 || acc > best) best = acc;
       }
       if (c == 0) srow[j] = best;

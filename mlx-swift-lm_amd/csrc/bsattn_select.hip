@@ -72,6 +72,14 @@ __device__ __forceinline__ float row_max16(float x) {
   return fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xF, 0xF, false)));  // row_ror:8
 }
 
+// integer sum over each 16-lane row (every lane of the row gets it)
+__device__ __forceinline__ int row_sum16(int x) {
+  x += __builtin_amdgcn_mov_dpp(x, 0x121, 0xF, 0xF, false);  // row_ror:1
+  x += __builtin_amdgcn_mov_dpp(x, 0x122, 0xF, 0xF, false);  // row_ror:2
+  x += __builtin_amdgcn_mov_dpp(x, 0x124, 0xF, 0xF, false);  // row_ror:4
+  return x + __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
+}
+
 // fmaxf over the whole wave
 __device__ __forceinline__ float wave_max_f32(float x) {
   return __uint_as_float(wave_allreduce_u32(__float_as_uint(x), [](uint32_t a, uint32_t b) {
@@ -499,6 +507,19 @@ __device__ __forceinline__ bool wave_take_best(uint32_t x, bool valid, int krem)
   return valid && (off > t || (off == t && gcount + __popcll(eqm & below) < krem));
 }
 
+// 8 consecutive query elements held in LDS as fp32 (16-byte aligned)
+__device__ __forceinline__ void query8(const float* src, float (&v)[8]) {
+  const float4 a = ((const float4*)src)[0], b = ((const float4*)src)[1];
+  v[0] = a.x;
+  v[1] = a.y;
+  v[2] = a.z;
+  v[3] = a.w;
+  v[4] = b.x;
+  v[5] = b.y;
+  v[6] = b.z;
+  v[7] = b.w;
+}
+
 // thread's PER consecutive score-row entries as whole vectors
 template <int PER>
 __device__ __forceinline__ void load_scores(const float* __restrict__ src, float (&v)[PER]) {
@@ -527,13 +548,13 @@ __device__ __forceinline__ void load_scores(const float* __restrict__ src, float
 // index), as a mask over the thread's slots.  BAND: the keys are
 // approximate MFMA scores with bound e (see the top of this file), and the
 // band around the K-th is rescored in the canonical order (the query rows
-// in s_q); the argument needs only that the keys held include the row's
+// in s_qf); the argument needs only that the keys held include the row's
 // top K.
 // ---------------------------------------------------------------------------
 template <int DT, int G, bool BAND, int PER>
 __device__ uint32_t select_core(const Geometry& geo, int seq, int h, const uint32_t (&kr)[PER],
                                 const int (&jr)[PER], uint32_t vmask, int nvalid, int K, float e,
-                                SelScratch& ss, int& ph, uint32_t* s_band, const uint32_t* s_q) {
+                                SelScratch& ss, int& ph, uint32_t* s_band, const float* s_qf) {
   const int tid = threadIdx.x, lane = tid & 63;
   if (nvalid <= K) return vmask;
   if constexpr (!BAND) {
@@ -588,7 +609,6 @@ __device__ uint32_t select_core(const Geometry& geo, int seq, int h, const uint3
       if (band & (1u << p)) s_band[w++] = (uint32_t)jr[p];
     __syncthreads();
     const int c = tid & 15;
-    const uint16_t* qh = (const uint16_t*)s_q;
     for (int bk = tid >> 4; bk < nband_total; bk += kSelThreads / 16) {
       const int j = (int)s_band[bk];
       float sv[8];
@@ -597,8 +617,8 @@ __device__ uint32_t select_core(const Geometry& geo, int seq, int h, const uint3
 #pragma unroll 4
       for (int gq = 0; gq < G; ++gq) {
         float qv[8];
-        unpack8<DT>(*(const u32x4*)(qh + gq * kHeadDim + 8 * c), qv);
-        const float acc = canonical_dot16(qv, sv);
+        query8(s_qf + gq * kHeadDim + 8 * c, qv);
+        const float acc = canonical_dot16<DT>(qv, sv);
         if (gq == 0 || acc > best) best = acc;
       }
       if (c == 0) s_band[bk] = score_key(best);  // the slot's index is no longer needed
@@ -629,6 +649,161 @@ __device__ uint32_t select_core(const Geometry& geo, int seq, int h, const uint3
 }
 
 // ---------------------------------------------------------------------------
+// Banded selection after a certified floor.  The survivors (approximate
+// score v in [lim, vmax]) are histogrammed into kWaveBins bins of value;
+// bin(v) = min(kWaveBins - 1, floor(fl(fl(v - lim) * scale))) is monotone in
+// v, and fl(v - lim) * scale stays within 2^-12 of the exact (v - lim) *
+// scale (u below), so two keys D bins apart have u more than D - 1 - 2^-11
+// apart, i.e. values more than that over scale.  With b* the bin of the
+// K-th largest approximate score t1 and D chosen so that
+// (D - 1 - 2^-11) / scale > 2e:
+//   bin(x) >= b* + D:  v_x - e > t1 + e >= t2 + e, certainly selected;
+//   bin(x) <= b* - D:  v_x + e < t1 - e, certainly not;
+// the keys of the bins in between (the band, which holds the K-th) are
+// rescored in the canonical order, and the remaining places go to the band's
+// best by (exact key, index).
+// Every pass runs on few lanes: each wave first packs its own survivors
+// (bin, block) into its first lanes through LDS, in block order, so that a
+// survivor is one lane and not a slot of every thread's PER; then
+//   barrier 1: the histogram; each wave finds b* for itself, counts its
+//              certainly-selected keys and hands its band keys slots of an
+//              unordered band list (LDS counter);
+//   barrier 2: the band list; waves take its entries 4 at a time (16 lanes
+//              each) and rescore them;
+//   barrier 3: the exact keys; the same lanes rank their entry among all of
+//              them (4 per lane, then a row sum) and mark it selected or not;
+//   barrier 4: the marks; each wave counts the selected band blocks of the
+//              waves before it and writes its selected blocks.
+// (Barriers 3 and 4 are skipped when the band fills the remaining places.)
+// Each pass is a few instructions per wave: a 16-wave workgroup runs four
+// waves per SIMD, so work that every wave repeats costs sixteen times its
+// own instruction count on each SIMD.  Returns
+// false, having written nothing to out, when a wave holds more than 64
+// survivors, the band exceeds kFastBand or the bound spans too many bins (the
+// caller then runs the general passes over the same survivors); each
+// decision is uniform over the workgroup, as every wave reads the same LDS
+// words.
+// ---------------------------------------------------------------------------
+constexpr int kFastBins = kWaveBins;  // find_kth_bin's histogram
+constexpr int kFastBand = 64;
+static_assert(kFastBins <= kHistBins, "the histogram lives in SelScratch");
+
+struct FastScratch {
+  float wmax[kSelWaves];                // each wave's largest valid approximate score
+  __align__(16) int win[kSelWaves];     // each wave's certainly-selected count
+  __align__(16) int bj[kFastBand];      // band list: block
+  __align__(16) uint32_t bk[kFastBand];  // band list: exact key
+  int pk[kFastBand];                    // band list: selected
+  int bcnt;                             // band slots handed out
+  int over;                             // a wave held more than 64 survivors
+};
+
+template <int DT, int G, int PER>
+__device__ bool select_banded(const Geometry& geo, int seq, int h, const float (&sc)[PER], uint32_t vmask,
+                              int K, float e, float lim, float scale, SelScratch& ss, FastScratch& fs,
+                              uint32_t* s_band, const float* s_qf, int32_t* out) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const float y = 2.0f * e * scale * 1.001f;  // D = floor(y) + 3 > 2e * scale + 1 + 2^-11
+  if (!(y < 512.0f)) return false;
+  const int D = (int)y + 3;
+  // the wave's survivors, packed in block order: bin << 16 | block - the
+  // wave's first block.  A survivor's rank in the wave is at most its offset,
+  // so the words stay inside the wave's own blocks of s_band (< mbps words)
+  const int ct = __popc(vmask);
+  const int incl = wave_scan_incl(ct);
+  const int n_w = __builtin_amdgcn_readlane(incl, 63);
+  uint32_t* wl = s_band + wave * 64 * PER;
+  int w = incl - ct;
+#pragma unroll
+  for (int p = 0; p < PER; ++p)
+    if ((vmask >> p) & 1u) {
+      const int bn = min(kFastBins - 1, (int)((sc[p] - lim) * scale));
+      wl[w++] = ((uint32_t)bn << 16) | (uint32_t)(lane * PER + p);
+    }
+  if (n_w > 64 && lane == 0) fs.over = 1;
+  wave_lds_order();
+  const bool has = lane < n_w;
+  const uint32_t word = has ? wl[lane] : 0u;
+  const int bin = (int)(word >> 16);
+  const int j = wave * 64 * PER + (int)(word & 0xFFFFu);
+  if (has) atomicAdd(&ss.hist[bin], 1u);
+  __syncthreads();
+  if (fs.over) return false;
+  int bstar, abv, cnt;
+  find_kth_bin(ss.hist, K, bstar, abv, cnt);
+  const bool in = has && bin >= bstar + D;
+  const bool band = has && !in && bin > bstar - D;
+  const uint64_t inb = __ballot(in), bandb = __ballot(band);
+  if (lane == 0) fs.win[wave] = __popcll(inb);
+  int slot = 0;
+  if (bandb) {
+    int b0 = 0;
+    if (lane == 0) b0 = atomicAdd(&fs.bcnt, __popcll(bandb));
+    slot = __builtin_amdgcn_readlane(b0, 0) + __popcll(bandb & below);
+    if (band && slot < kFastBand) fs.bj[slot] = j;
+  }
+  __syncthreads();
+  const int nband = fs.bcnt;
+  u32x4 w4[kSelWaves / 4];
+#pragma unroll
+  for (int i = 0; i < kSelWaves / 4; ++i) w4[i] = *(const u32x4*)(fs.win + 4 * i);
+  int nin = 0, in_before = 0;  // certainly-selected keys: all, and in the waves before this one
+#pragma unroll
+  for (int v = 0; v < kSelWaves; ++v) {
+    nin += (int)w4[v >> 2][v & 3];
+    in_before += v < wave ? (int)w4[v >> 2][v & 3] : 0;
+  }
+  const int krem = K - nin;  // >= 1, and nband >= 1: the K-th is in the band
+  if (nband > kFastBand || nband < 1 || krem < 1) return false;
+  const bool rescore = nband > krem;
+  if (rescore) {
+    // band entry gi = 4 * wave + lane / 16 on 16 lanes: its canonical score,
+    // then (after the barrier) its rank among the entries by (exact key
+    // desc, block asc), as distinct 64-bit keys
+    const bool holder = 4 * wave < nband;
+    const int gi = 4 * wave + (lane >> 4), c = lane & 15;
+    const int ge = min(gi, nband - 1);
+    if (holder) {
+      const int jb = fs.bj[ge];
+      float sv[8];
+      unpack8<DT>(*(const u32x4*)(summary_row(geo, seq, h, jb) + 8 * c), sv);
+      float best = 0.0f;
+#pragma unroll 4
+      for (int gq = 0; gq < G; ++gq) {
+        float qv[8];
+        query8(s_qf + gq * kHeadDim + 8 * c, qv);
+        const float acc = canonical_dot16<DT>(qv, sv);
+        if (gq == 0 || acc > best) best = acc;
+      }
+      if (c == 0 && gi < nband) fs.bk[gi] = score_key(best);
+    }
+    __syncthreads();
+    if (holder) {
+      const uint64_t me = ((uint64_t)fs.bk[ge] << 32) | (uint32_t)~fs.bj[ge];
+      int r = 0;
+#pragma unroll
+      for (int m = 0; m < kFastBand / 16; ++m) {
+        const int L = c + 16 * m;  // < kFastBand: stale past nband, not counted
+        const uint64_t o = ((uint64_t)fs.bk[L] << 32) | (uint32_t)~fs.bj[L];
+        r += (L < nband && o > me) ? 1 : 0;
+      }
+      r = row_sum16(r);
+      if (c == 0 && gi < nband) fs.pk[gi] = r < krem ? 1 : 0;
+    }
+    __syncthreads();
+  }
+  // without rescoring the band fills the remaining places: every entry is taken
+  const int bjl = fs.bj[lane];
+  const bool pkl = lane < nband && (!rescore || fs.pk[lane] != 0);
+  const int pick_before = __popcll(__ballot(pkl && bjl / (64 * PER) < wave));
+  const bool take = in || (band && (!rescore || fs.pk[slot] != 0));
+  const int pos = geo.ns + in_before + pick_before + __popcll(__ballot(take) & below);
+  if (take && pos < geo.ns + K) out[pos] = j;
+  return true;
+}
+
+// ---------------------------------------------------------------------------
 // block-wide selection; grid (Hkv, n), 1024 threads.  Thread t owns blocks
 // j = t*PER + p, p < PER, of its score row (the candidates are ns <= j <
 // ns + nc), so thread order then p is block order.
@@ -651,7 +826,8 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
                                                         int32_t* __restrict__ idx_out) {
   extern __shared__ uint32_t s_band[];
   __shared__ SelScratch ss;
-  __shared__ __align__(16) uint32_t s_q[BAND ? G * kHeadDim / 2 : 4];
+  __shared__ FastScratch fs;
+  __shared__ __align__(16) float s_qf[BAND ? G * kHeadDim : 4];  // the group's query rows (fp32)
   __shared__ float s_lim[2];  // e, tau - 2e
   const int tid = threadIdx.x, lane = tid & 63;
   const int h = blockIdx.x, bi = blockIdx.y;
@@ -669,6 +845,12 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
     ev = erow[lane];
     fl = erow[err_stride + lane];
   }
+  // the query rows of the group (one word per thread), also issued before
+  // the length is known
+  static_assert(!BAND || G * kHeadDim / 2 <= kSelThreads, "one query word per thread");
+  uint32_t qw = 0u;
+  if (BAND && tid < G * kHeadDim / 2)
+    qw = ((const uint32_t*)(q + q_row(sb, bi, h * G + tid / (kHeadDim / 2))))[tid % (kHeadDim / 2)];
   const int len = entry_len(geo, sb, bi, seq);
   const int nb = len > 0 ? (len + geo.tb - 1) / geo.tb : 0;
   const int nc = nb - geo.nr - c0;
@@ -678,29 +860,47 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
       out[p] = selected_block(p, nb, nc > K, geo.ns, geo.nr, K, nullptr);
     return;
   }
-  uint32_t kr[PER];
   int jr[PER];
   uint32_t vmask = 0u;
+  float vm = -INFINITY;  // the largest valid approximate score (NaN skipped)
 #pragma unroll
   for (int p = 0; p < PER; ++p) {
     const bool v = i0 + p >= c0 && i0 + p < c0 + nc;
-    kr[p] = v ? score_key(sc[p]) : 0u;
     jr[p] = i0 + p;
     vmask |= (uint32_t)v << p;
+    if (v) vm = fmaxf(vm, sc[p]);
   }
+  // the keys (score order as unsigned integers), where the passes need them
+  auto keys = [&](uint32_t (&kr)[PER]) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) kr[p] = ((vmask >> p) & 1u) ? score_key(sc[p]) : 0u;
+  };
   int ph = 0;
   uint32_t take;
   int total;
   if constexpr (!BAND) {
-    take = select_core<DT, G, BAND, PER>(geo, seq, h, kr, jr, vmask, nc, K, 0.0f, ss, ph, s_band, s_q);
+    uint32_t kr[PER];
+    keys(kr);
+    take = select_core<DT, G, BAND, PER>(geo, seq, h, kr, jr, vmask, nc, K, 0.0f, ss, ph, s_band, s_qf);
     const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
     int w = geo.ns + pos;
 #pragma unroll
     for (int p = 0; p < PER; ++p)
       if (take & (1u << p)) out[w++] = jr[p];
   } else {
-    for (int e = tid; e < G * kHeadDim / 2; e += kSelThreads)
-      s_q[e] = ((const uint32_t*)(q + q_row(sb, bi, h * G + e / (kHeadDim / 2))))[e % (kHeadDim / 2)];
+    if (tid < G * kHeadDim / 2) {
+      s_qf[2 * tid] = to_f32<DT>((uint16_t)(qw & 0xFFFFu));
+      s_qf[2 * tid + 1] = to_f32<DT>((uint16_t)(qw >> 16));
+    }
+    // for the banded selection: its histogram cleared, its counters, and
+    // each wave's largest approximate score
+    for (int b = tid; b < kFastBins; b += kSelThreads) ss.hist[b] = 0u;
+    if (tid == 0) {
+      fs.bcnt = 0;
+      fs.over = 0;
+    }
+    vm = wave_max_f32(vm);
+    if (lane == 0) fs.wmax[tid >> 6] = vm;
     if (tid < 64) {
       // the bound: maximum over the chunks' bounds (NaN bounds are skipped);
       // the floor: least chunk floor, if the chunks with one hold K
@@ -716,40 +916,51 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
     }
     __syncthreads();
     const float e = s_lim[0], lim = s_lim[1];
-    // certainly out: below lim (-inf: no floor; a NaN candidate's chunk has
-    // floor -inf, so nothing is dropped then)
+    // certainly out: below lim (-inf: no floor.  A NaN candidate's chunk
+    // has floor -inf, so with a finite lim every candidate score is a number)
     if (lim > -INFINITY) {
 #pragma unroll
       for (int p = 0; p < PER; ++p)
-        if (((vmask >> p) & 1u) && key_value(kr[p]) < lim) vmask &= ~(1u << p);
+        if (((vmask >> p) & 1u) && sc[p] < lim) vmask &= ~(1u << p);
     }
-    int nv;
-    const int cpos = wg_scan_excl(__popc(vmask), ss, ph, &nv);
-    if (nv <= kSelThreads) {
-      // one candidate per thread, in block order: keys through the band
-      // buffer (mbps >= nc >= nv words), blocks through the histogram
-      // (2048 words), both free until the selection
-      int w = cpos;
+    float vmax = fs.wmax[0];
 #pragma unroll
-      for (int p = 0; p < PER; ++p)
-        if ((vmask >> p) & 1u) {
-          s_band[w] = kr[p];
-          ss.hist[w++] = (uint32_t)jr[p];
-        }
-      __syncthreads();
-      const uint32_t k1[1] = {tid < nv ? s_band[tid] : 0u};
-      const int j1[1] = {tid < nv ? (int)ss.hist[tid] : -1};
-      __syncthreads();  // read before the selection reuses both
-      take = select_core<DT, G, BAND, 1>(geo, seq, h, k1, j1, tid < nv ? 1u : 0u, nv, K, e, ss, ph, s_band, s_q);
-      const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
-      if (take) out[geo.ns + pos] = j1[0];
+    for (int w = 1; w < kSelWaves; ++w) vmax = fmaxf(vmax, fs.wmax[w]);
+    const float scale = (float)(kFastBins - 1) / (vmax - lim);
+    if (lim > -INFINITY && __builtin_isfinite(vmax) && vmax > lim && __builtin_isfinite(scale) &&
+        select_banded<DT, G, PER>(geo, seq, h, sc, vmask, K, e, lim, scale, ss, fs, s_band, s_qf, out)) {
+      total = K;
     } else {
-      take = select_core<DT, G, BAND, PER>(geo, seq, h, kr, jr, vmask, nv, K, e, ss, ph, s_band, s_q);
-      const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
-      int w = geo.ns + pos;
+      uint32_t kr[PER];
+      keys(kr);
+      int nv;
+      const int cpos = wg_scan_excl(__popc(vmask), ss, ph, &nv);
+      if (nv <= kSelThreads) {
+        // one candidate per thread, in block order: keys through the band
+        // buffer (mbps >= nc >= nv words), blocks through the histogram
+        // (2048 words), both free until the selection
+        int w = cpos;
 #pragma unroll
-      for (int p = 0; p < PER; ++p)
-        if (take & (1u << p)) out[w++] = jr[p];
+        for (int p = 0; p < PER; ++p)
+          if ((vmask >> p) & 1u) {
+            s_band[w] = kr[p];
+            ss.hist[w++] = (uint32_t)jr[p];
+          }
+        __syncthreads();
+        const uint32_t k1[1] = {tid < nv ? s_band[tid] : 0u};
+        const int j1[1] = {tid < nv ? (int)ss.hist[tid] : -1};
+        __syncthreads();  // read before the selection reuses both
+        take = select_core<DT, G, BAND, 1>(geo, seq, h, k1, j1, tid < nv ? 1u : 0u, nv, K, e, ss, ph, s_band, s_qf);
+        const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
+        if (take) out[geo.ns + pos] = j1[0];
+      } else {
+        take = select_core<DT, G, BAND, PER>(geo, seq, h, kr, jr, vmask, nv, K, e, ss, ph, s_band, s_qf);
+        const int pos = wg_scan_excl(__popc(take), ss, ph, &total);
+        int w = geo.ns + pos;
+#pragma unroll
+        for (int p = 0; p < PER; ++p)
+          if (take & (1u << p)) out[w++] = jr[p];
+      }
     }
   }
   // sinks, the chosen candidates in block order (above), recent blocks
