@@ -170,6 +170,43 @@ def test_wide_group_clustered_top_blocks(gpu, dtype, Hq, Hkv, Tb, K, lo, hi, mul
     log(f"[clustered] {dtype} G={Hq // Hkv} [{lo}, {hi}) x{mult} err={err:.3g}")
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("case", ["gap", "ties"])
+def test_wide_group_band_at_kth(gpu, dtype, case):
+    """G = 16 over 2095 - 2996 candidates (MFMA scores, certified floor):
+    the band of bins around the K-th approximate score.
+    gap: K blocks whose keys are 0.5 .. 0.89 times the group's first query
+    row score far above the rest, so the band holds only places still to
+    fill and nothing is rescored.
+    ties: twelve blocks hold the keys of the block ranked K - 4, so the K-th
+    exact score falls among equal ones: the band is rescored and its ties go
+    to the lower block indices."""
+    Tb, K = 32, 40
+    lens = [Tb * 3000 + 5, Tb * 2100]
+    w = make_workload(5700 + len(case) + len(dtype), B=len(lens), Hq=64, Hkv=4, T=max(lens), Tb=Tb,
+                      dtype=dtype, top_k=K, ns=1, nr=4, lens=lens)
+    rng = np.random.default_rng(len(case) + len(dtype))
+    for b in range(w.B):
+        nb = (lens[b] + Tb - 1) // Tb
+        cand = np.arange(w.ns, nb - w.nr)
+        for h in range(w.Hkv):
+            if case == "gap":
+                q0 = O.to_f32(w.q[b, h * w.G], dtype).astype(np.float64)
+                for i, j in enumerate(rng.choice(cand, K, replace=False)):
+                    row = ((0.5 + 0.01 * i) * q0).astype(np.float32)
+                    w.keys[b][h][j * Tb:(j + 1) * Tb] = O.from_f32(np.tile(row, (Tb, 1)), dtype)
+            else:
+                summ = O.summaries(w.keys[b][h][:(nb - 1) * Tb], Tb, dtype)
+                sc = O.score_blocks(w.q[b, h * w.G:(h + 1) * w.G], summ, dtype)
+                src = cand[np.argsort(-sc[cand], kind="stable")][K - 5]
+                for j in rng.choice(np.setdiff1d(cand, [src]), 11, replace=False):
+                    w.keys[b][h][j * Tb:(j + 1) * Tb] = w.keys[b][h][src * Tb:(src + 1) * Tb]
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    err = check(cache, w, gpu)
+    log(f"[band at K-th] {case} {dtype} err={err:.3g}")
+
+
 @pytest.mark.parametrize("dtype,Hq,Hkv,Tb,K,scale", [
     ("f16", 64, 4, 32, 128, 1e-3), ("bf16", 32, 4, 64, 40, 1e-2), ("f16", 16, 4, 64, 32, 1e-3),
 ])
