@@ -833,6 +833,12 @@ __global__ __launch_bounds__(kSelThreads) void k_select(Geometry geo, SeqBatch s
   const int h = blockIdx.x, bi = blockIdx.y;
   const int seq = sb.ids[bi];
   const int c0 = geo.ns, K = geo.top_k;
+  // the arguments of the first phase, loaded in one round of scalar loads:
+  // left to itself the compiler issues each where it is first needed, and
+  // every one of them then waits behind the round before it
+  asm volatile("" ::"s"(seq), "s"(sb.len[bi]), "s"(sb.qoff[bi]), "s"(sb.qhs), "s"(geo.hkv), "s"(geo.sstride),
+               "s"(geo.tb), "s"(c0), "s"(geo.nr), "s"(K), "s"(geo.nsel_max), "s"(geo.meta), "s"(q), "s"(scores),
+               "s"(err), "s"(err_stride), "s"(err_count), "s"(idx_out));
   // scores (and the chunk bounds and floors) are loaded before the sequence
   // length is known: the row reads stay inside the score buffer (its slack
   // covers the last row), and entries that are not candidates are never used
