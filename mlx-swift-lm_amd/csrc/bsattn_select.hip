@@ -80,6 +80,14 @@ __device__ __forceinline__ int row_sum16(int x) {
   return x + __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
 }
 
+// a workgroup barrier that orders LDS only: global loads still in flight stay
+// in flight (__syncthreads() also waits for every outstanding global access)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // fmaxf over the whole wave
 __device__ __forceinline__ float wave_max_f32(float x) {
   return __uint_as_float(wave_allreduce_u32(__float_as_uint(x), [](uint32_t a, uint32_t b) {
@@ -728,7 +736,7 @@ __device__ bool select_banded(const Geometry& geo, int seq, int h, const float (
   const int bin = (int)(word >> 16);
   const int j = wave * 64 * PER + (int)(word & 0xFFFFu);
   if (has) atomicAdd(&ss.hist[bin], 1u);
-  __syncthreads();
+  lds_barrier();
   if (fs.over) return false;
   int bstar, abv, cnt;
   find_kth_bin(ss.hist, K, bstar, abv, cnt);
@@ -736,6 +744,12 @@ __device__ bool select_banded(const Geometry& geo, int seq, int h, const float (
   const bool band = has && !in && bin > bstar - D;
   const uint64_t inb = __ballot(in), bandb = __ballot(band);
   if (lane == 0) fs.win[wave] = __popcll(inb);
+  // each band key's summary row, requested by its owner now and read by the
+  // rescoring lanes after the band list is out (then from the cache); every
+  // lane loads (the others the first candidate's row), so that the load is
+  // not waited for where a branch joins
+  const uint16_t* pfr = summary_row(geo, seq, h, band ? j : geo.ns);
+  const uint32_t pf0 = *(const uint32_t*)pfr, pf1 = *(const uint32_t*)(pfr + 64);
   int slot = 0;
   if (bandb) {
     int b0 = 0;
@@ -743,7 +757,7 @@ __device__ bool select_banded(const Geometry& geo, int seq, int h, const float (
     slot = __builtin_amdgcn_readlane(b0, 0) + __popcll(bandb & below);
     if (band && slot < kFastBand) fs.bj[slot] = j;
   }
-  __syncthreads();
+  lds_barrier();
   const int nband = fs.bcnt;
   u32x4 w4[kSelWaves / 4];
 #pragma unroll
@@ -778,7 +792,7 @@ __device__ bool select_banded(const Geometry& geo, int seq, int h, const float (
       }
       if (c == 0 && gi < nband) fs.bk[gi] = score_key(best);
     }
-    __syncthreads();
+    lds_barrier();
     if (holder) {
       const uint64_t me = ((uint64_t)fs.bk[ge] << 32) | (uint32_t)~fs.bj[ge];
       int r = 0;
@@ -791,7 +805,7 @@ __device__ bool select_banded(const Geometry& geo, int seq, int h, const float (
       r = row_sum16(r);
       if (c == 0 && gi < nband) fs.pk[gi] = r < krem ? 1 : 0;
     }
-    __syncthreads();
+    lds_barrier();
   }
   // without rescoring the band fills the remaining places: every entry is taken
   const int bjl = fs.bj[lane];
@@ -799,6 +813,7 @@ __device__ bool select_banded(const Geometry& geo, int seq, int h, const float (
   const int pick_before = __popcll(__ballot(pkl && bjl / (64 * PER) < wave));
   const bool take = in || (band && (!rescore || fs.pk[slot] != 0));
   const int pos = geo.ns + in_before + pick_before + __popcll(__ballot(take) & below);
+  asm volatile("" ::"v"(pf0), "v"(pf1));  // the prefetch's registers, consumed before the store
   if (take && pos < geo.ns + K) out[pos] = j;
   return true;
 }
