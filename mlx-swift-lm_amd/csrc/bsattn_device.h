@@ -191,24 +191,20 @@ __device__ __forceinline__ float row_shl(float x) {
 }
 
 // Canonical dot product of one 128-dim pair held by the 16 lanes of a DPP
-// row (lane c = chunk c: dims 8c .. 8c+7): left fold of the chunk's 8
+// row (lane c = chunk c: dims 8c .. 8c+7): fused left fold of the chunk's 8
 // products, then the pairwise tree over chunks, (c, c+1), then (c, c+2),
 // (c, c+4), (c, c+8), which lane 0 of the row accumulates through row
 // shifts (fp32 addition is commutative, so the order of each pair does not
 // matter).  Only lane 0 of the row (c == 0) holds the result.
-// fp16 operands (DT 0): a product of two fp16 values has at most 22
-// significant bits and a magnitude in [2^-48, 2^32], so it is exact in fp32,
-// and fma(a, b, acc) = round(a*b + acc) is the rounded sum of the rounded
-// product: one instruction per step, the same bits.  bf16 products can leave
-// fp32's normal range, so they keep the separate multiply.
+// Each step is one fused multiply-add, fma(a, b, acc) = round(a*b + acc):
+// the normative order (the oracle folds with fmaf the same way).  A product
+// of two 16-bit values is exact in fp32 unless it leaves fp32's range (bf16
+// only), so this is also the rounded sum of the rounded product there.
 template <int DT>
 __device__ __forceinline__ float canonical_dot16(const float* a, const float* b) {
   float acc = __fmul_rn(a[0], b[0]);
 #pragma unroll
-  for (int e = 1; e < 8; ++e) {
-    if constexpr (DT == 0) acc = __builtin_fmaf(a[e], b[e], acc);
-    else acc = __fadd_rn(acc, __fmul_rn(a[e], b[e]));
-  }
+  for (int e = 1; e < 8; ++e) acc = __builtin_fmaf(a[e], b[e], acc);
   acc = __fadd_rn(acc, row_shl<1>(acc));
   acc = __fadd_rn(acc, row_shl<2>(acc));
   acc = __fadd_rn(acc, row_shl<4>(acc));

@@ -339,9 +339,10 @@ int orc_summaries_q(const uint32_t* codes, const uint16_t* scales,
 /* ------------------------------------------------------------------ */
 /* block scoring                                                       */
 /*   dot(a, b): chunk c (c = 0..D/8-1) covers dims 8c..8c+7;           */
-/*     p_c = (((a0*b0 + a1*b1) + a2*b2) + ...) + a7*b7  (fp32)         */
-/*   (fp16 x fp16 and bf16 x bf16 products are exact in fp32, so this  */
-/*   equals the fused-multiply-add chain);                              */
+/*     p_c = fma(a7, b7, ... fma(a2, b2, fma(a1, b1, a0*b0)))  (fp32,  */
+/*     each step one rounding of the exact a*b + acc).  A product of   */
+/*     two 16-bit values is exact in fp32 unless it leaves fp32's range */
+/*     (bf16 only), so elsewhere this is the unfused chain too;          */
 /*   then a pairwise tree: p_c <- p_c + p_{c^1}, then + p_{c^2}, ...   */
 /*   with the lower chunk on the left (fp32 addition is commutative,   */
 /*   so every lane of an xor-butterfly holds the same bits).           */
@@ -355,7 +356,7 @@ float orc_dot_canonical(const uint16_t* a, const uint16_t* b, int D, int dtype) 
   for (int c = 0; c < nc; c++) {
     float acc = to_f32(a[8 * c], dtype) * to_f32(b[8 * c], dtype);
     for (int j = 1; j < 8; j++)
-      acc = acc + to_f32(a[8 * c + j], dtype) * to_f32(b[8 * c + j], dtype);
+      acc = fmaf(to_f32(a[8 * c + j], dtype), to_f32(b[8 * c + j], dtype), acc);
     p[c] = acc;
   }
   for (int stride = 1; stride < nc; stride <<= 1)

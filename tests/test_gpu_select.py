@@ -170,6 +170,43 @@ def test_wide_group_clustered_top_blocks(gpu, dtype, Hq, Hkv, Tb, K, lo, hi, mul
     log(f"[clustered] {dtype} G={Hq // Hkv} [{lo}, {hi}) x{mult} err={err:.3g}")
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (64, 4)])
+def test_fused_dot_steps_select_like_oracle(gpu, Hq, Hkv):
+    """bf16 scores whose in-chunk steps differ fused and unfused: in block 50
+    of kv head 0, chunk 0 folds (-2^127)(1), then 2^64 * 2^64 = 2^128 (out of
+    fp32's range alone), then (-2^127)(1).  Fused, each step rounds a*b + acc
+    once and the chunk sums to 0, so the block scores like any other; with a
+    separate multiply the second product would be +inf and the block the
+    top one.  Every other block is zero in dims 0 - 2.  The VALU scoring
+    (G = 4) and the MFMA path (G = 16, whose bound is then not finite, so
+    every candidate is rescored) must select like the oracle.  Indices
+    only: the attention of such keys overflows."""
+    import torch
+    Tb, K, nblk = 64, 20, 300
+    w = make_workload(5800 + Hq, B=1, Hq=Hq, Hkv=Hkv, T=nblk * Tb, Tb=Tb, dtype="bf16", top_k=K, ns=1, nr=1)
+    k = O.to_f32(w.keys[0][0], "bf16")
+    k[:, :3] = 0.0
+    k[50 * Tb:51 * Tb, :3] = [1.0, 2.0 ** 64, 1.0]
+    w.keys[0][0][:] = O.from_f32(k, "bf16")
+    q = O.to_f32(w.q[0, :w.G], "bf16")
+    q[:, :3] = [-(2.0 ** 127), 2.0 ** 64, -(2.0 ** 127)]
+    w.q[0, :w.G] = O.from_f32(q, "bf16")
+    summ = O.summaries(w.keys[0][0], Tb, "bf16")
+    sc = O.score_blocks(w.q[0, :w.G], summ, "bf16")
+    assert np.isfinite(sc[50]) and sc[50] < np.sort(sc[1:nblk - 1])[-K]  # not selected when fused
+    cache = new_cache(w)
+    fill(cache, w, gpu)
+    qd = to_dev(w.q[:, :, None, :], w.dtype, gpu)
+    idx_ref, _ = oracle_decode(w)
+    assert 50 not in idx_ref[0, 0]
+    got = cache.selectBlocks(qd).cpu().numpy()
+    idx2 = torch.empty_like(torch.from_numpy(got)).to(gpu)
+    cache.decode(qd, w.scale, idx_out=idx2)
+    torch.cuda.synchronize()
+    assert np.array_equal(got, idx_ref), f"differ at {np.argwhere(got != idx_ref)[:5]}"
+    assert np.array_equal(idx2.cpu().numpy(), idx_ref)
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("case", ["gap", "ties"])
 def test_wide_group_band_at_kth(gpu, dtype, case):

@@ -204,6 +204,17 @@ def test_dot_within_chunk_left_fold():
     assert O.dot_canonical(_bf(a), _bf(b), "bf16") == 0.0  # ((2^24+1)+1)-2^24, ties to even
 
 
+def test_dot_within_chunk_steps_are_fused():
+    """Each in-chunk step rounds a*b + acc once: 2^64 * 2^64 = 2^128 leaves
+    fp32's range, but added to -2^127 it is 2^127 (a separate multiply
+    would give +inf)."""
+    a = np.zeros(128, np.float32)
+    b = np.zeros(128, np.float32)
+    a[0], b[0] = -(2.0 ** 127), 1.0
+    a[1], b[1] = 2.0 ** 64, 2.0 ** 64
+    assert O.dot_canonical(_bf(a), _bf(b), "bf16") == 2.0 ** 127
+
+
 def test_dot_exact_on_small_integers_and_error_bound():
     for dt in ("f16", "bf16"):
         ia = rng.integers(-8, 9, (50, 128)).astype(np.float32)
