@@ -179,6 +179,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   const float q1max = max_over_groups(q1h);
   float emax = 0.0f;
   bool wbad = false;
+  float st[kMfmaTiles];  // each tile's scores, stored after the last tile
   float* srow = score_row(geo, scores, bi, h);
 #pragma unroll
   for (int t = 0; t < kMfmaTiles; ++t) {
@@ -208,12 +209,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     const bool any_bad = (((bm | (bm >> 16) | (bm >> 32) | (bm >> 48)) >> n) & 1ull) != 0ull;
     const int j = j0 + n;
     float tv = -INFINITY;
+    st[t] = any_bad ? __builtin_nanf("") : sc;
     if (j < c1) {
-      const float v = any_bad ? __builtin_nanf("") : sc;
-      if (g == 0) {
-        srow[j] = v;
-        s_sc[wave * 16 * kMfmaTiles + 16 * t + n] = v;
-      }
+      if (g == 0) s_sc[wave * 16 * kMfmaTiles + 16 * t + n] = st[t];
       if (!any_bad) {
         emax = fmaxf(emax, am);
         tv = sc;
@@ -222,6 +220,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     wbad = wbad || __ballot(j < c1 && any_bad) != 0ull;
     tv = row_max16(tv);
     if (lane == 0) s_tm[wave * kMfmaTiles + t] = tv;
+  }
+  // the scores, once every row load has been consumed (a store after each
+  // tile slowed the rows' arrival)
+  if (g == 0) {
+#pragma unroll
+    for (int t = 0; t < kMfmaTiles; ++t)
+      if (jw + 16 * t + n < c1) srow[jw + 16 * t + n] = st[t];
   }
   emax = wave_max_f32(emax);
   if (lane == 0) {
