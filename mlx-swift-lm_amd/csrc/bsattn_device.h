@@ -1230,6 +1230,12 @@ __device__ __forceinline__ void attend_merge(const Geometry& geo, const SeqBatch
                                              const float (*s_o)[G][kHeadDim],
                                              uint16_t* __restrict__ out,
                                              float* __restrict__ partials) {
+  // Wide groups (G >= 8: G heads of partials per split, megabytes per
+  // launch) store them nontemporally: left dirty in the L2s they are written
+  // back while the next layer's scoring streams its summaries; narrow groups'
+  // small partials are cheaper cached, for the combine right after.  (A
+  // runtime choice between the two stores compiles to the cached one.)
+  constexpr bool nt = G >= 8;
   // per head: the maximum M over the waves, each wave's weight exp2(m_w - M)
   // and the merged sum L.  With one element per thread every thread computes
   // them for its own head (the same operations in the same order everywhere,
@@ -1241,10 +1247,18 @@ __device__ __forceinline__ void attend_merge(const Geometry& geo, const SeqBatch
     } else {
       const size_t row = (size_t)bi * geo.hq + h * G + head;
       float* pp = partials + (row * nsplit + split) * (kHeadDim + 2);
-      pp[d] = a;
-      if (d == 0) {
-        pp[kHeadDim] = M;
-        pp[kHeadDim + 1] = L;
+      if constexpr (nt) {
+        __builtin_nontemporal_store(a, pp + d);
+        if (d == 0) {
+          __builtin_nontemporal_store(M, pp + kHeadDim);
+          __builtin_nontemporal_store(L, pp + kHeadDim + 1);
+        }
+      } else {
+        pp[d] = a;
+        if (d == 0) {
+          pp[kHeadDim] = M;
+          pp[kHeadDim + 1] = L;
+        }
       }
     }
   };
