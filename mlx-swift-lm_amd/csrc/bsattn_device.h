@@ -1192,9 +1192,10 @@ __device__ __forceinline__ void attend_pick(const Geometry& geo, int bi, int h, 
 }
 
 // Stores one 16-dim tile of this wave's O (MFMA accumulator layout: lane
-// (dim n, group g) holds heads 4g .. 4g+3) into s_o[head][dim].
-template <int G>
-__device__ __forceinline__ void store_o_tile(float (*s_o)[kHeadDim], int dt, int n, int g,
+// (dim n, group g) holds heads 4g .. 4g+3) into s_o[head][dim] (OD < 128:
+// a buffer of OD dims, dt counted within it).
+template <int G, int OD = kHeadDim>
+__device__ __forceinline__ void store_o_tile(float (*s_o)[OD], int dt, int n, int g,
                                              const f32x4& o) {
   if constexpr (G >= 4) {
     if (4 * g < G) {
@@ -1210,14 +1211,89 @@ __device__ __forceinline__ void store_o_tile(float (*s_o)[kHeadDim], int dt, int
 }
 
 // Per-wave (m, l, o) of an empty slot.
-template <int G>
-__device__ __forceinline__ void store_empty(float* s_m, float* s_l, float (*s_o)[kHeadDim],
-                                            int lane) {
+template <int G, int OD = kHeadDim>
+__device__ __forceinline__ void store_empty(float* s_m, float* s_l, float (*s_o)[OD], int lane) {
   if (lane < G) {
     s_m[lane] = -INFINITY;
     s_l[lane] = 0.f;
   }
-  for (int e = lane; e < G * kHeadDim; e += 64) s_o[e / kHeadDim][e % kHeadDim] = 0.f;
+  for (int e = lane; e < G * OD; e += 64) s_o[e / OD][e % OD] = 0.f;
+}
+
+// One output element of a merged split: the normalised output (nsplit ==
+// 1) or the unnormalised partial (o, m, l) of split `split` of nsplit for
+// k_combine.  Wide groups (G >= 8: G heads of partials per split, megabytes
+// per launch) store them nontemporally: left dirty in the L2s they are
+// written back while the next layer's scoring streams its summaries; narrow
+// groups' small partials are cheaper cached, for the combine right after.
+// (A runtime choice between the two stores compiles to the cached one.)
+template <int DT, int G>
+__device__ __forceinline__ void merge_emit(const Geometry& geo, const SeqBatch& sb, int bi, int h,
+                                           int split, int nsplit, int head, int d, float M,
+                                           float L, float a, uint16_t* __restrict__ out,
+                                           float* __restrict__ partials) {
+  constexpr bool nt = G >= 8;
+  if (nsplit == 1) {
+    out[q_row(sb, bi, h * G + head) + d] = from_f32<DT>(L > 0.f ? a / L : 0.f);
+  } else {
+    const size_t row = (size_t)bi * geo.hq + h * G + head;
+    float* pp = partials + (row * nsplit + split) * (kHeadDim + 2);
+    if constexpr (nt) {
+      __builtin_nontemporal_store(a, pp + d);
+      if (d == 0) {
+        __builtin_nontemporal_store(M, pp + kHeadDim);
+        __builtin_nontemporal_store(L, pp + kHeadDim + 1);
+      }
+    } else {
+      pp[d] = a;
+      if (d == 0) {
+        pp[kHeadDim] = M;
+        pp[kHeadDim + 1] = L;
+      }
+    }
+  }
+}
+
+// Thread head < G: the maximum M of head `head` over the W waves, each
+// wave's weight exp2(m_w - M) (s_f) and the merged sum L (s_ML).
+template <int G, int W>
+__device__ __forceinline__ void merge_weights(const float (*s_m)[16], const float (*s_l)[16],
+                                              float (*s_f)[16], float (*s_ML)[16]) {
+  if (threadIdx.x < G) {
+    const int head = threadIdx.x;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][head]);
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float mw = s_m[w][head];
+      const float f = (M == -INFINITY || mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+      s_f[w][head] = f;
+      L += f * s_l[w][head];
+    }
+    s_ML[0][head] = M;
+    s_ML[1][head] = L;
+  }
+}
+
+// Dims d0 .. d0 + OD - 1 of the merged split from the waves' outputs in
+// s_o[w][head][d - d0], with the weights of merge_weights (behind a
+// barrier): each element is sum_w s_f[w][head] * o_w, summed from wave 0 up.
+template <int DT, int G, int W, int OD>
+__device__ __forceinline__ void merge_dims(const Geometry& geo, const SeqBatch& sb, int bi, int h,
+                                           int split, int nsplit, const float (*s_f)[16],
+                                           const float (*s_ML)[16], const float (*s_o)[G][OD],
+                                           int d0, uint16_t* __restrict__ out,
+                                           float* __restrict__ partials) {
+  for (int e = threadIdx.x; e < G * OD; e += 64 * W) {
+    const int head = e / OD, d = e % OD;
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) a += s_f[w][head] * s_o[w][head][d];
+    merge_emit<DT, G>(geo, sb, bi, h, split, nsplit, head, d0 + d, s_ML[0][head], s_ML[1][head], a,
+                      out, partials);
+  }
 }
 
 // Merges the W waves' (m, l, o) (after a workgroup barrier) and writes the
@@ -1230,38 +1306,11 @@ __device__ __forceinline__ void attend_merge(const Geometry& geo, const SeqBatch
                                              const float (*s_o)[G][kHeadDim],
                                              uint16_t* __restrict__ out,
                                              float* __restrict__ partials) {
-  // Wide groups (G >= 8: G heads of partials per split, megabytes per
-  // launch) store them nontemporally: left dirty in the L2s they are written
-  // back while the next layer's scoring streams its summaries; narrow groups'
-  // small partials are cheaper cached, for the combine right after.  (A
-  // runtime choice between the two stores compiles to the cached one.)
-  constexpr bool nt = G >= 8;
   // per head: the maximum M over the waves, each wave's weight exp2(m_w - M)
   // and the merged sum L.  With one element per thread every thread computes
   // them for its own head (the same operations in the same order everywhere,
   // so no barrier is needed to share them); otherwise once (thread h < G)
   // behind a barrier.
-  auto emit = [&](int head, int d, float M, float L, float a) {
-    if (nsplit == 1) {
-      out[q_row(sb, bi, h * G + head) + d] = from_f32<DT>(L > 0.f ? a / L : 0.f);
-    } else {
-      const size_t row = (size_t)bi * geo.hq + h * G + head;
-      float* pp = partials + (row * nsplit + split) * (kHeadDim + 2);
-      if constexpr (nt) {
-        __builtin_nontemporal_store(a, pp + d);
-        if (d == 0) {
-          __builtin_nontemporal_store(M, pp + kHeadDim);
-          __builtin_nontemporal_store(L, pp + kHeadDim + 1);
-        }
-      } else {
-        pp[d] = a;
-        if (d == 0) {
-          pp[kHeadDim] = M;
-          pp[kHeadDim + 1] = L;
-        }
-      }
-    }
-  };
   if constexpr (G * kHeadDim <= 64 * W) {
     const int e = threadIdx.x;
     if (e < G * kHeadDim) {
@@ -1277,34 +1326,13 @@ __device__ __forceinline__ void attend_merge(const Geometry& geo, const SeqBatch
         L += f * s_l[w][head];
         a += f * s_o[w][head][d];
       }
-      emit(head, d, M, L, a);
+      merge_emit<DT, G>(geo, sb, bi, h, split, nsplit, head, d, M, L, a, out, partials);
     }
   } else {
     __shared__ float s_f[W][16], s_ML[2][16];
-    if (threadIdx.x < G) {
-      const int head = threadIdx.x;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][head]);
-      float L = 0.f;
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        const float mw = s_m[w][head];
-        const float f = (M == -INFINITY || mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-        s_f[w][head] = f;
-        L += f * s_l[w][head];
-      }
-      s_ML[0][head] = M;
-      s_ML[1][head] = L;
-    }
+    merge_weights<G, W>(s_m, s_l, s_f, s_ML);
     __syncthreads();
-    for (int e = threadIdx.x; e < G * kHeadDim; e += 64 * W) {
-      const int head = e / kHeadDim, d = e % kHeadDim;
-      float a = 0.f;
-#pragma unroll
-      for (int w = 0; w < W; ++w) a += s_f[w][head] * s_o[w][head][d];
-      emit(head, d, s_ML[0][head], s_ML[1][head], a);
-    }
+    merge_dims<DT, G, W, kHeadDim>(geo, sb, bi, h, split, nsplit, s_f, s_ML, s_o, 0, out, partials);
   }
 }
 

@@ -336,7 +336,7 @@ __global__ __launch_bounds__(128) void k_summary_q(Geometry geo, SummaryBatch sb
 // grid (nsplit, Hkv, n)
 // ---------------------------------------------------------------------------
 template <int TB, int G, int W, int SEL, int KB>
-__global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo, SeqBatch sb,
+__global__ __launch_bounds__(64 * W, W > 4 ? 1 : G > 4 && SEL == 0 && TB == 32 ? 5 : 2) void k_attend_q(Geometry geo, SeqBatch sb,
                                                      const uint16_t* __restrict__ q,
                                                      int32_t* __restrict__ idx,
                                                      const float* __restrict__ scores,
@@ -348,11 +348,19 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
   constexpr int KS2 = TB / 32;  // PV k-steps
   constexpr int KF = QC::KF;
   constexpr int NVF = (8 / QC::DPF) * KS2;  // V fragments
+  // HALF (16-head groups): the waves' outputs are merged in two halves of
+  // 64 dims through one half-width buffer (16 KB less LDS: over given
+  // indices the workgroup fits 32 KB, five to a CU)
+  constexpr bool HALF = G > 8 && W <= 4;
+  constexpr int OD = HALF ? kHeadDim / 2 : kHeadDim;
   __shared__ float s_m[W][16], s_l[W][16];
-  __shared__ float s_o[W][G][kHeadDim];
+  __shared__ float s_o[W][G][OD];
   __shared__ int s_sel[SEL ? kSelMaxK : 1];
   __shared__ int s_selp[SEL ? kSelMaxK : 1];
   __shared__ __align__(16) uint32_t s_ws[SEL == 2 ? slot_scratch_words<W>() : SEL ? kWaveScratch : 4];
+  // wide groups: each wave's block of TB scale / bias entries, one per lane
+  // through LDS (4 registers held while K and V are in flight, not EPL x 4)
+  __shared__ __align__(16) u32x4 s_sb[G > 4 ? W : 1][G > 4 ? TB : 1];
   const int split = blockIdx.x, h = blockIdx.y, bi = blockIdx.z;
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
@@ -383,6 +391,7 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
   }
   const int len = uniform(entry_len(geo, sb, bi, seq));
   int j, page;
+  f32x4 oh[HALF ? 4 : 1];  // HALF: O's dims 64 .. 127, stored after the first merge
   attend_pick<TB, W, SEL>(geo, bi, h, seq, len, split * W + wave, split == 0 && wave == 0, wave, lane,
                           idx, jg, &wc, &wgc, s_sel, s_selp, s_ws, j, page);
   if (j >= 0) {
@@ -391,6 +400,11 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
     const u32x4* Kf = (const u32x4*)(slab + geo.k_off) + lane;
     const u32x4* Vf = (const u32x4*)(slab + geo.v_off) + lane;
     const u32x4* Sf = (const u32x4*)(slab + geo.sb_off) + g * EPL;
+    constexpr bool CMP = G <= 4;
+    // wide groups: entry lane of the block's scales / biases (lanes past TB
+    // repeat one), requested ahead of K and V
+    u32x4 sbx;
+    if constexpr (!CMP) sbx = ((const u32x4*)(slab + geo.sb_off))[lane & (TB - 1)];
     u32x4 kf[NT][KF];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -403,17 +417,22 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
     // are the lanes of bank 0 (n < 4) of each row, so tile t is rotated into
     // bank t and the per-score work runs on 4 registers instead of EPL;
     // lane (n, g) then holds head n & 3, tile n >> 2, entries 4 (n >> 2) + i
-    constexpr bool CMP = G <= 4;
-    constexpr int NSB = CMP ? 4 : EPL;  // scale / bias entries per lane
     const int tcp = n >> 2;
-    u32x4 sbv[NSB];
+    u32x4 sbv[CMP ? 4 : 1];  // CMP: this lane's scale / bias entries
     if constexpr (CMP) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) sbv[i] = tcp < NT ? Sf[4 * tcp + i] : u32x4{0u, 0u, 0u, 0u};
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) sbv[e] = Sf[e];
     }
+    // entry e of this lane (wide groups: from LDS; past the block's valid
+    // tokens zero, so that no stale scale / bias reaches PV)
+    auto sbe = [&](int e) __attribute__((always_inline)) -> u32x4 {
+      if constexpr (CMP) {
+        return sbv[e];
+      } else {
+        const u32x4 x = s_sb[wave][g * EPL + e];
+        return valid < TB && tok_of(g, e) >= valid ? u32x4{0u, 0u, 0u, 0u} : x;
+      }
+    };
     __builtin_amdgcn_sched_barrier(0);
     const u32x4 ones = u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
     const uint32_t base = f16_pair_1024();
@@ -440,6 +459,11 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
       qb0 = mfma_f16(ones, qf[1], qb0);
       qb1 = mfma_f16(ones, qf[2], f32x4{0.f, 0.f, 0.f, 0.f});
       qb1 = mfma_f16(ones, qf[3], qb1);
+    }
+    if constexpr (!CMP) {
+      // lane (n, g) reads entries g * EPL + e, stored by their lanes here
+      if (lane < TB) s_sb[wave][lane] = sbx;
+      wave_lds_order();
     }
     // A operands: P_g = p * v_scale_g and p * v_bias_g per dim group
     u32x4 pa0[KS2], pa1[KS2], pb0[KS2], pb1[KS2];
@@ -557,7 +581,7 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
         r1 = mfma_f16(k_operand<KB>(kf[t], 3, base), qk[3], r1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const u32x4& f = sbv[4 * t + i];
+          const u32x4 f = sbe(4 * t + i);
           const float d0 = r0[i] - q0c;  // sum_d q_d c_d, group 0
           const float d1 = r1[i] - q1c;
           float sc = lo_f(f[0]) * d0;
@@ -568,13 +592,10 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
         }
       }
       if (valid < TB) {
-        // tokens past the end: no score, and no stale scale / bias reaches PV
+        // tokens past the end: no score (sbe gives them zero scale / bias)
 #pragma unroll
         for (int e = 0; e < EPL; ++e)
-          if (tok_of(g, e) >= valid) {
-            pv[e] = -INFINITY;
-            sbv[e] = u32x4{0u, 0u, 0u, 0u};
-          }
+          if (tok_of(g, e) >= valid) pv[e] = -INFINITY;
       }
       mx = pv[0];
 #pragma unroll
@@ -594,7 +615,7 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
           const int e0 = 8 * s2 + 2 * jj, e1 = e0 + 1;
           const float p0 = pv[e0], p1 = pv[e1];
           const float u = KB == 4 && (jj & 1) ? kUnit16 : 1.0f;  // int4's unit-16 V elements
-          const u32x4 &f0 = sbv[e0], &f1 = sbv[e1];
+          const u32x4 f0 = sbe(e0), f1 = sbe(e1);
           pa0[s2][jj] = cvt_pk<0>(p0 * u * lo_f(f0[2]), p1 * u * lo_f(f1[2]));
           pa1[s2][jj] = cvt_pk<0>(p0 * u * hi_f(f0[2]), p1 * u * hi_f(f1[2]));
           pb0[s2][jj] = cvt_pk<0>(p0 * lo_f(f0[3]), p1 * lo_f(f1[3]));
@@ -620,17 +641,34 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : 2) void k_attend_q(Geometry geo
       const f32x4& vbg = dt < 4 ? vb0 : vb1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(-kDecOff, psg[i], o[i]) + vbg[i];
-      store_o_tile<G>(s_o[wave], dt, n, g, o);
+      if (!HALF || dt < 4) store_o_tile<G, OD>(s_o[wave], dt, n, g, o);
+      else oh[dt & 3] = o;
     }
     if (g == 0 && n < G) {
       s_m[wave][n] = mx;
       s_l[wave][n] = ps;
     }
   } else {
-    store_empty<G>(s_m[wave], s_l[wave], s_o[wave], lane);
+    store_empty<G, OD>(s_m[wave], s_l[wave], s_o[wave], lane);
+    if constexpr (HALF) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) oh[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
   __syncthreads();
-  attend_merge<0, G, W>(geo, sb, bi, h, split, (int)gridDim.x, s_m, s_l, s_o, out, partials);
+  if constexpr (HALF) {
+    __shared__ float s_f[W][16], s_ML[2][16];
+    merge_weights<G, W>(s_m, s_l, s_f, s_ML);
+    __syncthreads();
+    merge_dims<0, G, W, OD>(geo, sb, bi, h, split, (int)gridDim.x, s_f, s_ML, s_o, 0, out, partials);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) store_o_tile<G, OD>(s_o[wave], t, n, g, oh[t]);
+    __syncthreads();
+    merge_dims<0, G, W, OD>(geo, sb, bi, h, split, (int)gridDim.x, s_f, s_ML, s_o, OD, out, partials);
+  } else {
+    attend_merge<0, G, W>(geo, sb, bi, h, split, (int)gridDim.x, s_m, s_l, s_o, out, partials);
+  }
 }
 
 // ---------------------------------------------------------------------------
