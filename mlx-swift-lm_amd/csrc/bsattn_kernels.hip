@@ -775,10 +775,12 @@ static void combine_dispatch(const Geometry& g, const SeqBatch& b, const float* 
   // one round of loads: up to 16 splits with every split's (m, l) in each
   // thread (8 sequences x 32 heads, 9 splits: 4.1 against 4.3 us for the
   // loop), up to 64 with one exp2 per split shared through LDS (17 splits:
-  // 4.0 against 4.3 us, 34: 4.1 against 4.6 us); the loop beyond
+  // 4.0 against 4.3 us, 34: 4.1 against 4.6 us; 34 splits take the 40-split
+  // form, 6 clamped loads per thread rather than 14); the loop beyond
   if (nsplit <= 8) launch(k_combine_r<DT, 8>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
   else if (nsplit <= 16) launch(k_combine_r<DT, 16>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
   else if (nsplit <= 32) launch(k_combine_x<DT, 32>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
+  else if (nsplit <= 40) launch(k_combine_x<DT, 40>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
   else if (nsplit <= 48) launch(k_combine_x<DT, 48>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
   else if (nsplit <= 64) launch(k_combine_x<DT, 64>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);
   else launch(k_combine<DT>, grid, blk, 0, s, prof, kc, g, b, partials, oo, nsplit);

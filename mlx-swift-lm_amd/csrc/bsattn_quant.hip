@@ -423,15 +423,10 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : G > 4 && SEL == 0 && TB == 32 ?
 #pragma unroll
       for (int i = 0; i < 4; ++i) sbv[i] = tcp < NT ? Sf[4 * tcp + i] : u32x4{0u, 0u, 0u, 0u};
     }
-    // entry e of this lane (wide groups: from LDS; past the block's valid
-    // tokens zero, so that no stale scale / bias reaches PV)
+    // entry e of this lane (wide groups: from LDS)
     auto sbe = [&](int e) __attribute__((always_inline)) -> u32x4 {
-      if constexpr (CMP) {
-        return sbv[e];
-      } else {
-        const u32x4 x = s_sb[wave][g * EPL + e];
-        return valid < TB && tok_of(g, e) >= valid ? u32x4{0u, 0u, 0u, 0u} : x;
-      }
+      if constexpr (CMP) return sbv[e];
+      else return s_sb[wave][g * EPL + e];
     };
     __builtin_amdgcn_sched_barrier(0);
     const u32x4 ones = u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
@@ -461,8 +456,11 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : G > 4 && SEL == 0 && TB == 32 ?
       qb1 = mfma_f16(ones, qf[3], qb1);
     }
     if constexpr (!CMP) {
-      // lane (n, g) reads entries g * EPL + e, stored by their lanes here
-      if (lane < TB) s_sb[wave][lane] = sbx;
+      // lane (n, g) reads entries g * EPL + e (token tok_of(g, e)), stored by
+      // their lanes here; those of tokens past the block's valid ones are
+      // zero, so that no stale scale / bias reaches PV
+      if (lane < TB)
+        s_sb[wave][lane] = tok_of(lane / EPL, lane % EPL) < valid ? sbx : u32x4{0u, 0u, 0u, 0u};
       wave_lds_order();
     }
     // A operands: P_g = p * v_scale_g and p * v_bias_g per dim group
@@ -592,7 +590,7 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : G > 4 && SEL == 0 && TB == 32 ?
         }
       }
       if (valid < TB) {
-        // tokens past the end: no score (sbe gives them zero scale / bias)
+        // tokens past the end: no score (their scales / biases are zero)
 #pragma unroll
         for (int e = 0; e < EPL; ++e)
           if (tok_of(g, e) >= valid) pv[e] = -INFINITY;
