@@ -728,18 +728,22 @@ static void attend_dispatch(const Geometry& g, int waves, dim3 grid, const SeqBa
 
 int attend_waves(const Geometry& g, int nseq) {
   // the wide workgroup: groups of up to 4 heads, and splits that fit one
-  // workgroup per CU; then only where no CU holds more waves than with
-  // kWaves-wave workgroups spread over the CUs.  (Its fused selection holds
-  // 64 * kWavesWide * attend_keys = 2304 candidates, more than the 2048 a
-  // decode selects inside the attention kernel; beyond those it takes the
-  // given-index kernel, as kWaves does.)
-  if (kWaves != 4 || g.group > 4 || g.cus <= 0) return kWaves;
+  // workgroup per CU (quantized 16-head groups of 32-token blocks, whose
+  // wide workgroup holds half its outputs in LDS at a time and fits 72
+  // VGPRs: two per CU); then only where no CU
+  // holds more waves than with kWaves-wave workgroups spread over the CUs.
+  // (Its fused selection holds 64 * kWavesWide * attend_keys = 2304
+  // candidates, more than the 2048 a decode selects inside the attention
+  // kernel; beyond those it takes the given-index kernel, as kWaves does.)
+  const bool two = g.kv_bits != 0 && g.group == 16 && g.tb == 32;
+  if (kWaves != 4 || (g.group > 4 && !two) || g.cus <= 0) return kWaves;
   const int64_t pairs = (int64_t)std::min(std::max(nseq, 1), kMaxBatch) * g.hkv;
   const int64_t wide = pairs * ((g.nsel_max + kWavesWide - 1) / kWavesWide);
-  if (wide > g.cus) return kWaves;
+  const int64_t per_cu = (wide + g.cus - 1) / g.cus;
+  if (per_cu > (two ? 2 : 1)) return kWaves;
   const int64_t base = pairs * g.nsplit;
   const int64_t base_waves = (int64_t)kWaves * ((base + g.cus - 1) / g.cus);
-  return kWavesWide < base_waves ? kWavesWide : kWaves;
+  return kWavesWide * per_cu < base_waves ? kWavesWide : kWaves;
 }
 
 template <int SEL>

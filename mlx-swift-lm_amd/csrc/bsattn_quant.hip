@@ -336,7 +336,7 @@ __global__ __launch_bounds__(128) void k_summary_q(Geometry geo, SummaryBatch sb
 // grid (nsplit, Hkv, n)
 // ---------------------------------------------------------------------------
 template <int TB, int G, int W, int SEL, int KB>
-__global__ __launch_bounds__(64 * W, W > 4 ? 1 : G > 4 && SEL == 0 && TB == 32 ? 5 : 2) void k_attend_q(Geometry geo, SeqBatch sb,
+__global__ __launch_bounds__(64 * W, W > 4 ? (G > 8 && SEL == 0 ? 2 : 1) : G > 4 && SEL == 0 && TB == 32 ? 5 : 2) void k_attend_q(Geometry geo, SeqBatch sb,
                                                      const uint16_t* __restrict__ q,
                                                      int32_t* __restrict__ idx,
                                                      const float* __restrict__ scores,
@@ -349,9 +349,10 @@ __global__ __launch_bounds__(64 * W, W > 4 ? 1 : G > 4 && SEL == 0 && TB == 32 ?
   constexpr int KF = QC::KF;
   constexpr int NVF = (8 / QC::DPF) * KS2;  // V fragments
   // HALF (16-head groups): the waves' outputs are merged in two halves of
-  // 64 dims through one half-width buffer (16 KB less LDS: over given
-  // indices the workgroup fits 32 KB, five to a CU)
-  constexpr bool HALF = G > 8 && W <= 4;
+  // 64 dims through one half-width buffer (4 KB less LDS per wave: over
+  // given indices a 4-wave workgroup fits 32 KB, five to a CU, and two
+  // 9-wave workgroups fit a CU)
+  constexpr bool HALF = G > 8;
   constexpr int OD = HALF ? kHeadDim / 2 : kHeadDim;
   __shared__ float s_m[W][16], s_l[W][16];
   __shared__ float s_o[W][G][OD];
@@ -758,13 +759,14 @@ static void attend_q_group(const Geometry& g, int waves, dim3 grid, const SeqBat
                            int32_t* idx, const float* sc, float sl2, uint16_t* out, float* part,
                            hipStream_t s, Timing* prof) {
   const int kd = kProfAttend;
-  if constexpr (SEL != 1) {  // the wide workgroup: groups of up to 4 heads, never one selecting wave
+  if constexpr (SEL != 1) {  // the wide workgroup: groups of up to 4 or of 16 heads, never one selecting wave
     if (waves == kWavesWide) {
       constexpr int W = kWavesWide;
       const dim3 blk(64 * W);
       switch (g.group) {
         case 1: launch(k_attend_q<TB, 1, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
         case 2: launch(k_attend_q<TB, 2, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
+        case 16: launch(k_attend_q<TB, 16, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
         default: launch(k_attend_q<TB, 4, W, SEL, KB>, grid, blk, 0, s, prof, kd, g, b, q, idx, sc, sl2, out, part); break;
       }
       return;

@@ -2,7 +2,9 @@
 CU with one workgroup of 9 waves takes them instead of 4-wave workgroups
 (attend_waves in csrc/bsattn_kernels.hip): 2 sequences x 8 kv heads with 130
 selected blocks are 16 pairs x 15 splits = 240 workgroups, where 4 waves
-would make 528, 3 on some CUs.  Each shape here has more than 256 candidates
+would make 528, 3 on some CUs.  Quantized caches with groups of 16 heads and
+32-token blocks may take two such workgroups per CU (4 sequences x 8 kv
+heads: 480 workgroups, 18 waves on the busiest CU against 20).  Each shape here has more than 256 candidates
 per sequence, so the decode runs the scoring kernel and the attention kernel
 with the selection inside (not the one-launch fused decode), and is held to
 the parity bars: selection bit-exact, decode == select + attend, outputs
@@ -25,17 +27,20 @@ pytestmark = pytest.mark.gpu
 WIDE, BASE, MAX_BATCH = 9, 4, 64
 
 
-def takes_wide(Hkv: int, G: int, nsel: int, nseq: int, cus: int) -> bool:
+def takes_wide(Hkv: int, G: int, nsel: int, nseq: int, cus: int, bits: int = 0, Tb: int = 64) -> bool:
     """The library's choice of 9-wave workgroups, restated: groups of up to 4
-    heads, at most one workgroup per CU, and fewer waves on the busiest CU
+    heads with at most one workgroup per CU, or quantized groups of 16 heads
+    in 32-token blocks with at most two; and fewer waves on the busiest CU
     than 4-wave workgroups spread over the CUs would leave."""
-    if G > 4:
+    two = bits != 0 and G == 16 and Tb == 32
+    if G > 4 and not two:
         return False
     pairs = min(max(nseq, 1), MAX_BATCH) * Hkv
-    if pairs * -(-nsel // WIDE) > cus:
+    per_cu = -(-pairs * -(-nsel // WIDE) // cus)
+    if per_cu > (2 if two else 1):
         return False
     base = pairs * -(-nsel // BASE)
-    return WIDE < BASE * -(-base // cus)
+    return WIDE * per_cu < BASE * -(-base // cus)
 
 
 def cus() -> int:
@@ -53,6 +58,9 @@ CASES = {
     "int4-tb32-g2": ("int4", 32, 2, [330 * 32 + 5, 270 * 32 + 2]),
     "int8-tb64-g1": ("int8", 64, 1, [300 * 64 + 11, 285 * 64]),
     "int8-tb32-g4": ("int8", 32, 4, [340 * 32 - 3, 310 * 32 + 1]),
+    # 16-head groups: one workgroup per CU, then two
+    "int8-tb32-g16": ("int8", 32, 16, [330 * 32 + 7, 290 * 32 - 1]),
+    "int8-tb32-g16-two": ("int8", 32, 16, [300 * 32 + 1, 320 * 32 - 5, 280 * 32 + 16, 340 * 32]),
 }
 HKV, TOP_K = 8, 128
 
@@ -64,7 +72,7 @@ def test_wide_workgroups_against_the_oracle(gpu, case):
     dtype = "f16" if bits else kind
     w = make_workload(9700 + len(case) + Tb + G, B=len(lens), Hq=HKV * G, Hkv=HKV, T=max(lens), Tb=Tb,
                       dtype=dtype, top_k=TOP_K, ns=1, nr=1, lens=lens, salient_frac=0.01)
-    assert takes_wide(HKV, G, w.nsel_max, w.B, cus()), "shape does not take the 9-wave workgroups"
+    assert takes_wide(HKV, G, w.nsel_max, w.B, cus(), bits, Tb), "shape does not take the 9-wave workgroups"
     log(f"[wide] {case}: {w.B} x {HKV} pairs, {w.nsel_max} slots, {-(-w.nsel_max // WIDE)} splits")
     cache = new_cache(w, kv_bits=bits) if bits else new_cache(w)
     fill(cache, w, gpu)
