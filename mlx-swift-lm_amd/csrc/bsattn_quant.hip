@@ -18,7 +18,8 @@
 //     tokens) is the A operand against the codes; the same P_g and
 //     p * v_bias_g against an all-ones operand give sum_t P_g and
 //     sum_t p v_bias_g in the accumulator layout of O, so
-//     o = raw - 1024 sum P_g + sum p v_bias_g needs no shuffles.
+//     o = raw - 1024 sum P_g + sum p v_bias_g needs no shuffles (the PV
+//     accumulator starts at sum p v_bias_g - 1024 sum P_g).
 // Summaries of a quantized cache are fp16 means of the dequantized keys
 // (fmaf(scale, code, bias), sequential fold), so scoring and selection are
 // the 16-bit kernels' own.
@@ -630,16 +631,19 @@ __global__ __launch_bounds__(64 * W, W > 4 ? (G > 8 && SEL == 0 ? 2 : 1) : G > 4
       vb0 = mfma_f16(pb0[s2], ones, vb0);
       vb1 = mfma_f16(pb1[s2], ones, vb1);
     }
-    // O = P_g . V codes, corrected per dim group
+    // O = P_g . V codes, corrected per dim group: each tile's accumulator
+    // starts at sum_t p v_bias_g - kDecOff sum_t P_g (the codes' offset)
+    f32x4 oc0, oc1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      oc0[i] = __builtin_fmaf(-kDecOff, ps0[i], vb0[i]);
+      oc1[i] = __builtin_fmaf(-kDecOff, ps1[i], vb1[i]);
+    }
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 o = dt < 4 ? oc0 : oc1;
 #pragma unroll
       for (int s2 = 0; s2 < KS2; ++s2) o = mfma_f16(dt < 4 ? pa0[s2] : pa1[s2], v_operand<KB, KS2>(vf, dt, s2, base), o);
-      const f32x4& psg = dt < 4 ? ps0 : ps1;
-      const f32x4& vbg = dt < 4 ? vb0 : vb1;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(-kDecOff, psg[i], o[i]) + vbg[i];
       if (!HALF || dt < 4) store_o_tile<G, OD>(s_o[wave], dt, n, g, o);
       else oh[dt & 3] = o;
     }
