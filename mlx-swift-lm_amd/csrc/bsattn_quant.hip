@@ -334,7 +334,10 @@ __global__ __launch_bounds__(128) void k_summary_q(Geometry geo, SummaryBatch sb
 // (one block per wave, W waves per workgroup, selection fused when SEL,
 // split partials merged by k_combine), with the dequantisation folded into
 // the MFMAs as described at the top of this file.  q / out are fp16.
-// grid (nsplit, Hkv, n)
+// grid (nsplit, Hkv, n).  Workgroups per CU the register budget is sized
+// for: two 9-wave ones for 16-head groups over given indices (launched
+// for 32-token blocks, 72 VGPRs), five 4-wave ones for wide groups of
+// 32-token blocks over given indices, otherwise one (9 waves) or two (4).
 // ---------------------------------------------------------------------------
 template <int TB, int G, int W, int SEL, int KB>
 __global__ __launch_bounds__(64 * W, W > 4 ? (G > 8 && SEL == 0 ? 2 : 1) : G > 4 && SEL == 0 && TB == 32 ? 5 : 2) void k_attend_q(Geometry geo, SeqBatch sb,
