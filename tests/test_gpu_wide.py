@@ -91,6 +91,7 @@ MULTI = {
     "bf16-tb64-g4-l3": ("bf16", 64, 32, 8, 127, 3, 0, [320 * 64 + 2, 300 * 64 + 1]),
     "f16-tb32-g2-l4": ("f16", 32, 16, 8, 127, 4, 0, [300 * 32 + 3, 310 * 32 + 1]),
     "int8-tb64-g4-l2": ("f16", 64, 32, 8, 127, 2, 8, [300 * 64 + 9, 280 * 64]),
+    "int8-tb32-g16-l2": ("f16", 32, 128, 8, 127, 2, 8, [300 * 32 + 5, 280 * 32 + 3]),
 }
 
 
@@ -98,6 +99,6 @@ MULTI = {
 def test_wide_multi_decode_equals_single_decodes(gpu, case):
     dtype, Tb, Hq, Hkv, K, L, bits, lens = MULTI[case]
     # the multi-token test's caches keep 1 sink and 2 recent blocks
-    assert takes_wide(Hkv, Hq // Hkv, K + 3, len(lens), cus())
+    assert takes_wide(Hkv, Hq // Hkv, K + 3, len(lens), cus(), bits, Tb)
     log(f"[wide multi] {case}")
     multi_check(gpu, dtype, Hq, Hkv, Tb, K, L, bits, lens)
