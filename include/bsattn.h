@@ -70,7 +70,7 @@ typedef struct bsattn_desc {
 /* Derived sizes, for callers sizing buffers. */
 typedef struct bsattn_info {
   int32_t nsel_max;        /* sink + recent + top_k: width of index outputs */
-  int32_t num_splits;      /* attention partials per (sequence, q head) */
+  int32_t num_splits;      /* attention partials per (sequence, q head): the most a call uses */
   int64_t page_bytes;      /* bytes of one page across all kv heads, incl. summaries */
   int64_t pool_bytes;      /* device bytes held by the handle */
   int64_t free_pages;      /* pages not owned by any sequence */
